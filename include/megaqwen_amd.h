@@ -1,0 +1,101 @@
+/* C ABI of the MI355X-native Qwen3-0.6B megakernel (gfx950).
+ *
+ * Drop-in for the reference's `csrc/megakernel` launchers: the entry points
+ * below keep the reference's names, argument order and meaning; the
+ * differences are (1) `hipStream_t` instead of `cudaStream_t`, (2) every entry
+ * returns an int status (MQ_OK or a negative MQ_ERR_*) instead of void, and
+ * (3) no cuBLAS handle (prefill uses hand-written MFMA kernels).
+ *
+ * All pointers are device pointers unless stated otherwise. Buffers belong to
+ * the caller; the library keeps one small per-device workspace of its own
+ * (exchange buffers, counters), allocated on the first call on that device.
+ * Calls that overlap in time on one device race on that workspace.
+ */
+#ifndef MEGAQWEN_AMD_H
+#define MEGAQWEN_AMD_H
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MQ_OK 0
+#define MQ_ERR_ARG (-1)      /* invalid argument (checked on the host before any HIP call) */
+#define MQ_ERR_HIP (-2)      /* a HIP runtime call failed */
+#define MQ_ERR_DEVICE (-3)   /* device cannot run the cooperative grid */
+#define MQ_ERR_ALLOC (-4)    /* workspace allocation failed */
+
+/* Per-layer weight pointers, bf16, HF nn.Linear layout [out, in].
+ * Same fields and order as the reference's LDGLayerWeights
+ * (csrc/megakernel/fused_decode_ldg.cu:24-36) and PrefillLayerWeights
+ * (csrc/megakernel/megakernel_decode.py:281-293). */
+typedef struct LDGLayerWeights {
+  const void* input_layernorm_weight;     /* [1024] */
+  const void* q_proj_weight;              /* [2048, 1024] */
+  const void* k_proj_weight;              /* [1024, 1024] */
+  const void* v_proj_weight;              /* [1024, 1024] */
+  const void* q_norm_weight;              /* [128] */
+  const void* k_norm_weight;              /* [128] */
+  const void* o_proj_weight;              /* [1024, 2048] */
+  const void* post_attn_layernorm_weight; /* [1024] */
+  const void* gate_proj_weight;           /* [3072, 1024] */
+  const void* up_proj_weight;             /* [3072, 1024] */
+  const void* down_proj_weight;           /* [1024, 3072] */
+} LDGLayerWeights;
+
+typedef LDGLayerWeights PrefillLayerWeights;
+
+/* One greedy decode step of the full model.
+ * Replaces `launch_ldg_decode` (csrc/megakernel/fused_decode_ldg.cu:893-921).
+ *   layer_weights : DEVICE array of num_layers structs (as in the reference).
+ *   k_cache/v_cache: bf16 [num_layers, 8, max_seq_len, 128]; slot `position` is written.
+ *   cache_len must equal position + 1.
+ *   On return (stream-ordered): *output_token_id = argmax of the bf16 logits
+ *   (lowest index on ties), or a negative value -(1 + flags) if the kernel's
+ *   watchdog fired; hidden_buffer = final hidden bf16[1024]; g_normalized =
+ *   final-norm output as fp32[1024]. The other scratch pointers
+ *   (g_activations .. g_mlp_intermediate, block_max_vals, block_max_idxs) are
+ *   accepted for ABI compatibility and not used. */
+int launch_ldg_decode(int input_token_id, int* output_token_id, const void* embed_weight,
+                      const LDGLayerWeights* layer_weights, const void* final_norm_weight,
+                      const void* lm_head_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                      void* v_cache, void* hidden_buffer, void* g_activations, void* g_residual, void* g_q,
+                      void* g_k, void* g_v, void* g_attn_out, void* g_mlp_intermediate, void* g_normalized,
+                      void* block_max_vals, void* block_max_idxs, int num_layers, int position, int cache_len,
+                      int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* As launch_ldg_decode, and also writes the bf16-rounded logits (as fp32) of
+ * all 151936 vocabulary rows to logits_output.
+ * Replaces `launch_ldg_decode_with_logits` (csrc/megakernel/fused_decode_ldg.cu:972-1001). */
+int launch_ldg_decode_with_logits(int input_token_id, int* output_token_id, float* logits_output,
+                                  const void* embed_weight, const LDGLayerWeights* layer_weights,
+                                  const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
+                                  const void* sin_table, void* k_cache, void* v_cache, void* hidden_buffer,
+                                  void* g_activations, void* g_residual, void* g_q, void* g_k, void* g_v,
+                                  void* g_attn_out, void* g_mlp_intermediate, void* g_normalized,
+                                  void* block_max_vals, void* block_max_idxs, int num_layers, int position,
+                                  int cache_len, int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* One decoder block at `position` on a given bf16 hidden vector (no embedding,
+ * no LM head): hidden_out = layer(hidden_in); K/V slot `position` of the
+ * single-layer caches k_cache/v_cache ([1, 8, max_seq_len, 128]) is written.
+ * Debug/parity entry for a single block; the reference has no separate
+ * launcher for it (its layer body is ldg_decode_kernel's loop,
+ * csrc/megakernel/fused_decode_ldg.cu:655-686). */
+int mq_decode_layer(const void* hidden_in, void* hidden_out, const LDGLayerWeights* layer_weights,
+                    const void* cos_table, const void* sin_table, void* k_cache, void* v_cache, int position,
+                    int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* Zero this device's workspace (exchange buffers and counters). Needed only
+ * after a launch reported a watchdog error. Synchronous. */
+int mq_reset_workspace(int device);
+
+/* Human-readable name of a status code. */
+const char* mq_strerror(int status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEGAQWEN_AMD_H */

@@ -1,0 +1,104 @@
+// Shared device helpers for the MI355X (gfx950, CDNA4) Qwen3-0.6B kernels.
+//
+// Model shapes follow the reference's constants (csrc/megakernel/config.cuh:33-40).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mq {
+
+constexpr int H = 1024;        // hidden size
+constexpr int I = 3072;        // MLP intermediate size
+constexpr int NQ = 16;         // query heads
+constexpr int NKV = 8;         // key/value heads
+constexpr int HD = 128;        // head dim
+constexpr int QS = NQ * HD;    // 2048
+constexpr int KVS = NKV * HD;  // 1024
+constexpr int VOCAB = 151936;
+constexpr int MAX_LAYERS = 32;
+constexpr float EPS = 1e-6f;
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// ------------------------------------------------------------------ bf16
+__device__ __forceinline__ float bf2f(uint32_t b16) { return __uint_as_float(b16 << 16); }
+__device__ __forceinline__ float bflo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bfhi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+// fp32 -> bf16 bits, round to nearest even (inputs are finite).
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+// Round an fp32 value to the nearest bf16 value (kept in fp32).
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// Unpack 8 bf16 (one 16-byte load) into fp32.
+__device__ __forceinline__ void unpack8(const u32x4& w, float (&f)[8]) {
+  f[0] = bflo(w.x); f[1] = bfhi(w.x);
+  f[2] = bflo(w.y); f[3] = bfhi(w.y);
+  f[4] = bflo(w.z); f[5] = bfhi(w.z);
+  f[6] = bflo(w.w); f[7] = bfhi(w.w);
+}
+__device__ __forceinline__ float dot8(const u32x4& w, const float (&x)[8]) {
+  float s = bflo(w.x) * x[0];
+  s = fmaf(bfhi(w.x), x[1], s);
+  s = fmaf(bflo(w.y), x[2], s);
+  s = fmaf(bfhi(w.y), x[3], s);
+  s = fmaf(bflo(w.z), x[4], s);
+  s = fmaf(bfhi(w.z), x[5], s);
+  s = fmaf(bflo(w.w), x[6], s);
+  s = fmaf(bfhi(w.w), x[7], s);
+  return s;
+}
+
+// ------------------------------------------------------------------ wave64 reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+// Sum over aligned groups of 16 lanes.
+__device__ __forceinline__ float group16_sum(float v) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ------------------------------------------------------------------ device-coherent access
+// Plain loads/stores of data written by other CUs during the same launch can
+// hit stale L2 lines of another XCD: inter-workgroup traffic uses sc1
+// (device scope) buffer operations, which the compiler tracks like ordinary
+// loads for s_waitcnt.
+constexpr int SC1 = 16;  // gfx940+ cache-policy bit for device scope
+
+struct Buf {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ explicit Buf(const void* base)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000)) {}
+  __device__ __forceinline__ u32x4 ld4(uint32_t byte_off) const {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, SC1);
+  }
+  __device__ __forceinline__ uint32_t ld1(uint32_t byte_off) const {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, SC1);
+  }
+  __device__ __forceinline__ void st1(uint32_t v, uint32_t byte_off) const {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, byte_off, 0, SC1);
+  }
+  __device__ __forceinline__ void st4(u32x4 v, uint32_t byte_off) const {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, byte_off, 0, SC1);
+  }
+};
+
+// Wait for all of this wave's outstanding vector-memory operations (loads and
+// stores; gfx9 counts both in vmcnt) to complete. simm16 = vmcnt(0),
+// expcnt(7), lgkmcnt(15).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+}  // namespace mq

@@ -1,0 +1,82 @@
+"""CPU tests of the C ABI boundary: the library loads, exports every entry
+point include/*.h declares, and rejects invalid arguments on the host before
+touching the GPU (no compute calls here)."""
+
+import ctypes
+import glob
+import os
+import re
+import subprocess
+
+import pytest
+
+from megaqwen_amd import _abi
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+
+
+def declared_functions():
+    names = []
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for n in ("launch_ldg_decode", "launch_ldg_decode_with_logits", "mq_decode_layer",
+              "mq_reset_workspace", "mq_strerror"):
+        assert n in names, n
+
+
+def test_library_exports_every_declared_symbol():
+    assert os.path.exists(_abi.LIB_PATH), "build the library first (python -m megaqwen_amd.build)"
+    out = subprocess.run(["nm", "-D", "--defined-only", _abi.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\sT\s+(\w+)$", out, flags=re.M))
+    missing = [n for n in declared_functions() if n not in exported]
+    assert not missing, missing
+
+
+def test_python_binding_covers_header():
+    assert set(_abi.SIGNATURES) == set(declared_functions())
+
+
+def test_layer_struct_layout():
+    assert ctypes.sizeof(_abi.LDGLayerWeights) == 11 * 8
+    assert _abi.LDGLayerWeights.down_proj_weight.offset == 80
+
+
+def _decode_args(**over):
+    a = dict(token=1, out=1, embed=1, layers=1, norm=1, lm=1, cos=1, sin=1, k=1, v=1, hidden=1,
+             num_layers=28, position=0, cache_len=1, max_seq_len=16, scale=0.088)
+    a.update(over)
+    return [a["token"], a["out"], a["embed"], a["layers"], a["norm"], a["lm"], a["cos"], a["sin"], a["k"], a["v"],
+            a["hidden"]] + [None] * 10 + [a["num_layers"], a["position"], a["cache_len"], a["max_seq_len"],
+                                           a["scale"], None]
+
+
+@pytest.mark.parametrize("bad", [
+    dict(out=None), dict(embed=None), dict(layers=None), dict(k=None),
+    dict(num_layers=0), dict(num_layers=33), dict(position=-1), dict(position=16), dict(cache_len=5),
+    dict(token=-1), dict(token=151936), dict(scale=0.0), dict(scale=float("nan")), dict(max_seq_len=0),
+])
+def test_decode_rejects_invalid_arguments(bad):
+    st = _abi.lib().launch_ldg_decode(*_decode_args(**bad))
+    assert st == _abi.MQ_ERR_ARG
+
+
+def test_decode_layer_rejects_invalid_arguments():
+    L = _abi.lib()
+    assert L.mq_decode_layer(None, 1, 1, 1, 1, 1, 1, 0, 16, 0.088, None) == _abi.MQ_ERR_ARG
+    assert L.mq_decode_layer(1, 1, 1, 1, 1, 1, 1, 16, 16, 0.088, None) == _abi.MQ_ERR_ARG
+    assert L.mq_decode_layer(1, 1, 1, 1, 1, 1, 1, 0, 16, -1.0, None) == _abi.MQ_ERR_ARG
+
+
+def test_strerror():
+    L = _abi.lib()
+    assert L.mq_strerror(0) == b"ok"
+    assert b"argument" in L.mq_strerror(-1)
+    with pytest.raises(_abi.MegakernelError):
+        _abi.check(-1, "x")
