@@ -6,18 +6,25 @@
 // (csrc/megakernel/fused_decode_ldg.cu:617-887).
 //
 // Layout on the chip: 256 workgroups x 256 threads (4 waves of 64), one per
-// CU. A cooperative launch places workgroup w on XCD w % 8, so KV head g is
-// owned by XCD g: its 32 workgroups compute the 512 q/k/v rows of that head
-// group and split its attention over positions. Every other matvec is
-// split evenly over all 256 workgroups by output rows, so each workgroup
-// streams the same number of weight bytes per stage.
+// CU. A cooperative launch places workgroup w on XCD g = w % 8 as its j = w / 8
+// -th member. XCD g owns KV group g end to end:
+//   * the 512 q/k/v rows of group g (16 rows per workgroup),
+//   * the attention of its two query heads (split over positions),
+//   * the o_proj columns of those two heads (all 1024 rows, 32 per workgroup),
+//   * MLP units [384g, 384g+384): their gate/up rows and down_proj columns.
+// Every workgroup streams the same 120 KB of weights per layer. The only
+// data that crosses XCDs are the o_proj and down_proj partial sums: workgroup
+// (g, j) owns residual-stream rows [32j, 32j+32) and reduces them from the 8
+// XCDs' partials, so each XCD keeps a full copy of the residual stream.
 //
-// Inter-workgroup data moves through a small device workspace as "tagged
-// words": each 32-bit word holds a bf16 value in its low half and a 16-bit
-// tag (launch epoch x 32 + layer) in its high half, written and read with
-// device-scope (sc1) buffer operations. A consumer polls the words it needs
-// until every tag matches, so one exchange costs one memory round trip and
-// no separate barrier. A watchdog bounds every poll.
+// Exchanges use "tagged words": a bf16 value in the low half of a 32-bit word
+// and a 16-bit tag (launch epoch x 32 + layer) in the high half, or an fp32
+// value with a 32-bit tag in a 64-bit word. A consumer issues all its loads at
+// once and re-polls only words with a stale tag, so an exchange costs one
+// memory round trip and no barrier. Inside an XCD, producers use plain stores
+// and consumers non-temporal loads, which bypass the per-CU L1 and are served
+// by the XCD's shared L2; across XCDs both sides use device-scope (sc1)
+// accesses. A watchdog bounds every poll.
 //
 // Numerics follow HF Qwen3 in bf16 (transformers/models/qwen3/modeling_qwen3.py):
 // every Linear / norm / RoPE op / residual add / SiLU / product result is
@@ -38,27 +45,40 @@ constexpr int NWG = 256;
 constexpr int NT = 256;
 constexpr int NXCD = 8;
 constexpr int WG_PER_XCD = NWG / NXCD;  // 32
-constexpr int CH_MIN = 32;              // minimum positions per attention split
+constexpr int ROWS = H / WG_PER_XCD;    // residual rows owned per workgroup: 32
+constexpr int UNITS = I / NWG;          // MLP units per workgroup: 12
+constexpr int XUNITS = I / NXCD;        // MLP units per XCD: 384
+// Attention: one workgroup per KV group up to CH_MIN positions; longer contexts
+// are split over up to 32 workgroups of the owning XCD. The first PF rounds
+// of 16 positions are prefetched while the q/k/v rows are still in flight.
+constexpr int CH_MIN = 128;
+constexpr int PF = 8;
 
 // Workspace layout, in 32-bit words.
 constexpr uint32_t WS_EPOCH = 0;
 constexpr uint32_t WS_ERR = 32;
 constexpr uint32_t WS_FINAL_TICKET = 64;
-constexpr uint32_t WS_ATTN_TICKET = 1024;  // [MAX_LAYERS][NKV], 32 words apart
-constexpr uint32_t WS_XH = WS_ATTN_TICKET + MAX_LAYERS * NKV * 32;
-constexpr uint32_t WS_XQKV = WS_XH + H;           // [NKV][512]
-constexpr uint32_t WS_XATTN = WS_XQKV + NKV * 512;  // [2048]
-constexpr uint32_t WS_XH1 = WS_XATTN + QS;        // [1024]
-constexpr uint32_t WS_XM = WS_XH1 + H;            // [3072]
-constexpr uint32_t APART = 132;                   // m, l, o[128], pad
-constexpr uint32_t WS_APART = WS_XM + I;          // [NKV][32][2][APART] fp32
-constexpr uint32_t WS_LMPART = WS_APART + NKV * WG_PER_XCD * 2 * APART;  // [NWG][2]
+// per-XCD regions (128 KB apart), written and read only by that XCD's workgroups
+constexpr uint32_t WS_LOCAL = 1024;
+constexpr uint32_t LOCAL_WORDS = 32768;
+constexpr uint32_t LX_H = 0;        // [1024] tagged bf16: residual stream h (layer input)
+constexpr uint32_t LX_H1 = 1024;    // [1024] tagged bf16: residual after attention
+constexpr uint32_t LX_M = 2048;     // [384]  tagged bf16: SiLU(gate) * up of this XCD's units
+constexpr uint32_t LX_ATTN = 2432;  // [256]  tagged bf16: attention output of the two heads
+constexpr uint32_t LX_QKV = 2688;   // [512]  tagged bf16: raw q0, q1, k, v rows
+constexpr uint32_t APART = 130;     // split partial: m, l, o[128]
+constexpr uint32_t LX_PART = 4096;  // [32 splits][2 heads][APART] (fp32, tag) pairs
+// cross-XCD partial sums: [j][row][g] (fp32, tag) pairs
+constexpr uint32_t WS_OPART = WS_LOCAL + NXCD * LOCAL_WORDS;
+constexpr uint32_t WS_DPART = WS_OPART + 2 * WG_PER_XCD * ROWS * NXCD;
+constexpr uint32_t WS_LMPART = WS_DPART + 2 * WG_PER_XCD * ROWS * NXCD;  // [NWG][2]
 constexpr uint32_t WS_WORDS = WS_LMPART + NWG * 2;
-constexpr size_t WS_BYTES = ((WS_WORDS * 4 + 65535) / 65536) * 65536;
+constexpr size_t WS_BYTES = ((WS_WORDS * 4 + 4 + 65535) / 65536) * 65536;
 
 constexpr uint32_t POLL_LIMIT = 1u << 21;  // ~1 s of polling before the watchdog fires
 constexpr uint32_t ERR_POLL = 1u;
-constexpr uint32_t ERR_TICKET = 2u;
+
+constexpr int NT_LD = 2;  // non-temporal cache policy: bypasses the CU's L1, served by the XCD's L2
 
 enum : int { MODE_INPUT_HIDDEN = 1, MODE_NO_LMHEAD = 2, MODE_LOGITS = 4 };
 
@@ -94,26 +114,74 @@ __device__ __forceinline__ bool tags_ok(const u32x4& v, uint32_t tag) {
   return ((v.x >> 16) == tag) & ((v.y >> 16) == tag) & ((v.z >> 16) == tag) & ((v.w >> 16) == tag);
 }
 
+// The error word is written and read with sc1 buffer operations only.
 __device__ __noinline__ void raise_error(uint32_t* ws, uint32_t code) {
-  __hip_atomic_fetch_or(ws + WS_ERR, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_raw_buffer_store_b32(code, __builtin_amdgcn_make_buffer_rsrc(ws, 0, 0x7fffffff, 0x00020000),
+                                        WS_ERR * 4u, 0, SC1);
 }
 
-// Poll 4 tagged words at word offset `word` until all carry `tag`.
-__device__ __forceinline__ u32x4 poll4(const Buf& wsb, uint32_t* ws, uint32_t word, uint32_t tag) {
-  u32x4 v = wsb.ld4(word * 4u);
+__device__ __forceinline__ bool watchdog(const Buf& wsb, uint32_t* ws, uint32_t spins) {
+  if ((spins & 1023u) == 0 && (spins > POLL_LIMIT || wsb.ld1(WS_ERR * 4u) != 0)) {
+    raise_error(ws, ERR_POLL);
+    return true;
+  }
+  return false;
+}
+
+// ---- XCD-local exchange: plain stores, non-temporal loads (L2)
+__device__ __forceinline__ u32x4 ldl4(const Buf& b, uint32_t word) {
+  return __builtin_amdgcn_raw_buffer_load_b128(b.r, word * 4u, 0, NT_LD);
+}
+__device__ __forceinline__ u32x2 ldl64(const Buf& b, uint32_t word) {
+  return __builtin_amdgcn_raw_buffer_load_b64(b.r, word * 4u, 0, NT_LD);
+}
+__device__ __forceinline__ void stl1(const Buf& b, uint32_t word, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, b.r, word * 4u, 0, 0);
+}
+__device__ __forceinline__ void stl64(const Buf& b, uint32_t word, float v, uint32_t tag) {
+  u32x2 x;
+  x.x = __float_as_uint(v);
+  x.y = tag;
+  __builtin_amdgcn_raw_buffer_store_b64(x, b.r, word * 4u, 0, 0);
+}
+__device__ __forceinline__ u32x4 repoll_l4(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, u32x4 v) {
   uint32_t spins = 0;
   while (!tags_ok(v, tag)) {
-    ++spins;
-    if ((spins & 1023u) == 0) {
-      if (spins > POLL_LIMIT || wsb.ld1(WS_ERR * 4u) != 0) {
-        raise_error(ws, ERR_POLL);
-        break;
-      }
-    }
+    if (watchdog(b, ws, ++spins)) break;
     __builtin_amdgcn_s_sleep(1);
-    v = wsb.ld4(word * 4u);
+    v = ldl4(b, word);
   }
   return v;
+}
+__device__ __forceinline__ float repoll_l64(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, u32x2 v) {
+  uint32_t spins = 0;
+  while (v.y != tag) {
+    if (watchdog(b, ws, ++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+    v = ldl64(b, word);
+  }
+  return __uint_as_float(v.x);
+}
+
+// ---- cross-XCD exchange: device-scope (sc1) stores and loads of (fp32, tag) pairs;
+// aligned 8-byte accesses are single-copy atomic
+__device__ __forceinline__ u32x2 ldx64(const Buf& b, uint32_t word) {
+  return __builtin_amdgcn_raw_buffer_load_b64(b.r, word * 4u, 0, SC1);
+}
+__device__ __forceinline__ void stx64(const Buf& b, uint32_t word, float v, uint32_t tag) {
+  u32x2 x;
+  x.x = __float_as_uint(v);
+  x.y = tag;
+  __builtin_amdgcn_raw_buffer_store_b64(x, b.r, word * 4u, 0, SC1);
+}
+__device__ __forceinline__ float repoll_x64(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, u32x2 v) {
+  uint32_t spins = 0;
+  while (v.y != tag) {
+    if (watchdog(b, ws, ++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+    v = ldx64(b, word);
+  }
+  return __uint_as_float(v.x);
 }
 
 // Weight pointers arrive through the LDGLayerWeights array, so the compiler
@@ -125,12 +193,13 @@ typedef const __attribute__((address_space(1))) u32x2 gu32x2;
 typedef const __attribute__((address_space(1))) uint16_t gu16;
 __device__ __forceinline__ u32x4 ldw(const uint16_t* p) { return *(gu32x4*)(p); }
 __device__ __forceinline__ u32x2 ldw2(const uint16_t* p) { return *(gu32x2*)(p); }
-__device__ __forceinline__ float ldbf(const uint16_t* p) { return bf2f(*(gu16*)(p)); }
+__device__ __forceinline__ uint32_t ldraw16(const uint16_t* p) { return *(gu16*)(p); }
 
 // Block-wide RMSNorm of s_x[H] (bf16 values held as fp32) with bf16 weight w:
 // HF Qwen3RMSNorm (modeling_qwen3.py:59-64): y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))).
-__device__ __forceinline__ void block_rmsnorm(const float* s_x, const uint16_t* __restrict__ w, float* s_y,
-                                              float* s_red) {
+// `wv` holds this thread's 4 weights (elements 4*tid .. 4*tid+3), loaded by the
+// caller ahead of time so that no global load sits on the reduction's path.
+__device__ __forceinline__ void block_rmsnorm(const float* s_x, const u32x2 wv, float* s_y, float* s_red) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float x[4];
   float ss = 0.f;
@@ -144,34 +213,60 @@ __device__ __forceinline__ void block_rmsnorm(const float* s_x, const uint16_t* 
   __syncthreads();
   const float tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
   const float rstd = 1.0f / sqrtf(tot * (1.0f / H) + EPS);
-  const u32x2 wv = ldw2(w + tid * 4);
   const float wf[4] = {bflo(wv.x), bfhi(wv.x), bflo(wv.y), bfhi(wv.y)};
 #pragma unroll
   for (int i = 0; i < 4; i++) s_y[tid * 4 + i] = rbf(wf[i] * rbf(x[i] * rstd));
   __syncthreads();
 }
 
-// Gather `n` tagged words (n a multiple of 4*NT or <= 4*NT) into s_dst as fp32.
-__device__ __forceinline__ void gather_lds(const Buf& wsb, uint32_t* ws, uint32_t base, int n, uint32_t tag,
-                                           float* s_dst) {
-  for (int i = threadIdx.x * 4; i < n; i += NT * 4) {
-    const u32x4 v = poll4(wsb, ws, base + i, tag);
-    s_dst[i + 0] = bflo(v.x);
-    s_dst[i + 1] = bflo(v.y);
-    s_dst[i + 2] = bflo(v.z);
-    s_dst[i + 3] = bflo(v.w);
-  }
+// Gather the 1024 tagged words of an XCD-local vector into s_dst as fp32.
+__device__ __forceinline__ void gather_local_h(const Buf& b, uint32_t* ws, uint32_t base, uint32_t tag,
+                                               float* s_dst) {
+  const int i = threadIdx.x * 4;
+  const u32x4 x = repoll_l4(b, ws, base + i, tag, ldl4(b, base + i));
+  s_dst[i + 0] = bflo(x.x);
+  s_dst[i + 1] = bflo(x.y);
+  s_dst[i + 2] = bflo(x.z);
+  s_dst[i + 3] = bflo(x.w);
+}
+
+// Gather 8 consecutive XCD-local tagged words starting at `word`.
+__device__ __forceinline__ void gather8_local(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag,
+                                              float (&x)[8]) {
+  u32x4 a = ldl4(b, word);
+  u32x4 c = ldl4(b, word + 4);
+  a = repoll_l4(b, ws, word, tag, a);
+  c = repoll_l4(b, ws, word + 4, tag, c);
+  x[0] = bflo(a.x); x[1] = bflo(a.y); x[2] = bflo(a.z); x[3] = bflo(a.w);
+  x[4] = bflo(c.x); x[5] = bflo(c.y); x[6] = bflo(c.z); x[7] = bflo(c.w);
+}
+
+// Residual rows [32j, 32j+32) of this workgroup: r_out = bf16(r_in + bf16(sum over the 8
+// XCDs' partials in XCD order)); thread r < 32 handles row r. Returns the new row value.
+__device__ __forceinline__ float reduce_rows(const Buf& wsb, uint32_t* ws, uint32_t part_base, int j, int r,
+                                             uint32_t tag64, float r_in) {
+  const uint32_t base = part_base + 2 * ((j * ROWS + r) * NXCD);
+  u32x2 v[NXCD];
+#pragma unroll
+  for (int q = 0; q < NXCD; q++) v[q] = ldx64(wsb, base + 2 * q);
+  float s = 0.f;
+#pragma unroll
+  for (int q = 0; q < NXCD; q++) s += repoll_x64(wsb, ws, base + 2 * q, tag64, v[q]);
+  return rbf(r_in + rbf(s));
 }
 
 // ---------------------------------------------------------------- the kernel
 __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
-  __shared__ float s_h[H];    // layer input h (residual stream)
-  __shared__ float s_h1[H];   // residual after attention
-  __shared__ float s_y[H];    // normalized vector
+  __shared__ float s_h[H];      // a full residual-stream vector (h or h1)
+  __shared__ float s_y[H];      // its RMSNorm output
+  __shared__ float s_rh[ROWS];  // this workgroup's rows of h (layer input)
+  __shared__ float s_rh1[ROWS]; // this workgroup's rows of h1
   __shared__ float s_qkv[4 * HD];
   __shared__ float s_red[4][16];
-  __shared__ float s_att[4][2][APART];
+  __shared__ float s_att[16][2][APART];
+  __shared__ float s_part[WG_PER_XCD * 2 * APART];
   __shared__ uint32_t s_flag;
+  __shared__ const uint16_t* s_lw[MAX_LAYERS][11];  // weight pointers, copied once per launch
   __shared__ float s_bestv[4];
   __shared__ int s_besti[4];
 
@@ -180,19 +275,29 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   uint32_t* ws = P.ws;
   const Buf wsb(ws);
   const uint32_t epoch = wsb.ld1(WS_EPOCH * 4u);
+  const uint32_t lb = WS_LOCAL + g * LOCAL_WORDS;  // this XCD's exchange region
 
   const int p = P.position;
   const int n_ctx = p + 1;
   int CH = (n_ctx + WG_PER_XCD - 1) / WG_PER_XCD;
   CH = CH < CH_MIN ? CH_MIN : CH;
-  CH = (CH + 3) & ~3;
+  CH = (CH + 15) & ~15;
   const int nsplit = (n_ctx + CH - 1) / CH;
 
   const size_t kv_layer_stride = (size_t)NKV * P.max_seq_len * HD;
 
+  // The pointer table lives in device memory the kernel also writes to, so the
+  // compiler cannot fetch it with scalar loads; fetch it once into LDS instead of
+  // paying a dependent global round trip before every stage's weight stream.
+  for (int i = tid; i < P.num_layers * 11; i += NT)
+    s_lw[i / 11][i % 11] = reinterpret_cast<const uint16_t* const*>(P.layers)[i];
+  __syncthreads();
+
   for (int layer = 0; layer < P.num_layers; layer++) {
-    const LDGLayerWeights& LW = P.layers[layer];
+    const uint16_t* const* LW = s_lw[layer];
+    enum { W_IN = 0, W_Q, W_K, W_V, W_QN, W_KN, W_O, W_POST, W_G, W_U, W_D };
     const uint32_t tag = tag_of(epoch, layer);
+    const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
 
     // ============ stage 1: input RMSNorm + q/k/v rows of KV group g ============
     // workgroup (g, j) owns rows r = 16j + 4*wave + k of [q_{2g}; q_{2g+1}; k_g; v_g].
@@ -202,11 +307,12 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       for (int k = 0; k < 4; k++) {
         const int r = 16 * j + 4 * wave + k;
         const uint16_t* base;
-        if (r < 256) base = (const uint16_t*)LW.q_proj_weight + (size_t)(256 * g + r) * H;
-        else if (r < 384) base = (const uint16_t*)LW.k_proj_weight + (size_t)(128 * g + r - 256) * H;
-        else base = (const uint16_t*)LW.v_proj_weight + (size_t)(128 * g + r - 384) * H;
+        if (r < 256) base = LW[W_Q] + (size_t)(256 * g + r) * H;
+        else if (r < 384) base = LW[W_K] + (size_t)(128 * g + r - 256) * H;
+        else base = LW[W_V] + (size_t)(128 * g + r - 384) * H;
         rows[k] = base;
       }
+      const u32x2 wln = ldw2(LW[W_IN] + tid * 4);
       u32x4 wq[4][2];
 #pragma unroll
       for (int k = 0; k < 4; k++) {
@@ -220,11 +326,13 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         s_h[tid * 4 + 1] = bfhi(v.x);
         s_h[tid * 4 + 2] = bflo(v.y);
         s_h[tid * 4 + 3] = bfhi(v.y);
+        __syncthreads();
+        if (tid < ROWS) s_rh[tid] = s_h[ROWS * j + tid];
       } else {
-        gather_lds(wsb, ws, WS_XH, H, tag_of(epoch, layer - 1), s_h);
+        gather_local_h(wsb, ws, lb + LX_H, tag_of(epoch, layer - 1), s_h);
       }
       __syncthreads();
-      block_rmsnorm(s_h, (const uint16_t*)LW.input_layernorm_weight, s_y, &s_red[0][0]);
+      block_rmsnorm(s_h, wln, s_y, &s_red[0][0]);
       float x0[8], x1[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) {
@@ -236,26 +344,56 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       for (int k = 0; k < 4; k++) acc[k] = wave_sum(dot8(wq[k][0], x0) + dot8(wq[k][1], x1));
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        if (lane == k) wsb.st1(tagged(tag, rbf(acc[k])), (WS_XQKV + 512 * g + 16 * j + 4 * wave + k) * 4u);
+        if (lane == k) stl1(wsb, lb + LX_QKV + 16 * j + 4 * wave + k, tagged(tag, rbf(acc[k])));
       }
     }
 
-    // ============ stage 2: QK-norm, RoPE, KV append, split-K attention ============
+    // ============ stage 2: QK-norm, RoPE, KV append, attention ============
     if (j < nsplit) {
-      gather_lds(wsb, ws, WS_XQKV + 512 * g, 512, tag, s_qkv);
+      // ---- this workgroup's chunk of positions: lane group grp (16 lanes, 8 dims each)
+      // takes positions c_begin + 4*wave + grp + 16*r.
+      const int c_begin = j * CH;
+      const int c_end = min(n_ctx, c_begin + CH);
+      const int grp = lane >> 4, d0 = (lane & 15) * 8;
+      const int pos0 = c_begin + wave * 4 + grp;
+      const int nround = (c_end - c_begin + 15) >> 4;
+      const uint16_t* kc = P.k_cache + layer * kv_layer_stride + (size_t)g * P.max_seq_len * HD + d0;
+      const uint16_t* vc = P.v_cache + layer * kv_layer_stride + (size_t)g * P.max_seq_len * HD + d0;
+      // QK-norm weights and this position's cos/sin first (the in-order load queue would
+      // otherwise put them behind the K/V stream), then K/V of positions < p, which do
+      // not depend on this layer's q/k/v.
+      // (unconditional: a load merged from a branch would be waited for at the merge)
+      const uint16_t* nw = wave < 2 ? LW[W_QN] : LW[W_KN];
+      const uint16_t* ct = P.cos_tab + (size_t)p * HD;
+      const uint16_t* st = P.sin_tab + (size_t)p * HD;
+      const uint32_t rnw0 = ldraw16(nw + lane), rnw1 = ldraw16(nw + 64 + lane);
+      const uint32_t rc0 = ldraw16(ct + lane), rs0 = ldraw16(st + lane);
+      const uint32_t rc1 = ldraw16(ct + 64 + lane), rs1 = ldraw16(st + 64 + lane);
+      u32x4 KP[PF], VP[PF];
+#pragma unroll
+      for (int u = 0; u < PF; u++) {
+        const int pos = pos0 + 16 * u;
+        if (pos < c_end && pos != p) {
+          KP[u] = ldw(kc + (size_t)pos * HD);
+          VP[u] = ldw(vc + (size_t)pos * HD);
+        }
+      }
+      if (tid < 128) {
+        const u32x4 v = repoll_l4(wsb, ws, lb + LX_QKV + 4 * tid, tag, ldl4(wsb, lb + LX_QKV + 4 * tid));
+        s_qkv[4 * tid + 0] = bflo(v.x);
+        s_qkv[4 * tid + 1] = bflo(v.y);
+        s_qkv[4 * tid + 2] = bflo(v.z);
+        s_qkv[4 * tid + 3] = bflo(v.w);
+      }
       __syncthreads();
       if (wave < 3) {
         // HF: q_norm/k_norm over 128 (modeling_qwen3.py:252-253), then apply_rotary_pos_emb (:147-170).
         float a = s_qkv[wave * HD + lane], b = s_qkv[wave * HD + 64 + lane];
         const float ss = wave_sum(a * a + b * b);
         const float rstd = 1.0f / sqrtf(ss * (1.0f / HD) + EPS);
-        const uint16_t* nw = (const uint16_t*)(wave < 2 ? LW.q_norm_weight : LW.k_norm_weight);
-        a = rbf(ldbf(nw + lane) * rbf(a * rstd));
-        b = rbf(ldbf(nw + 64 + lane) * rbf(b * rstd));
-        const uint16_t* ct = P.cos_tab + (size_t)p * HD;
-        const uint16_t* st = P.sin_tab + (size_t)p * HD;
-        const float c0 = ldbf(ct + lane), s0 = ldbf(st + lane);
-        const float c1 = ldbf(ct + 64 + lane), s1 = ldbf(st + 64 + lane);
+        const float c0 = bf2f(rc0), s0 = bf2f(rs0), c1 = bf2f(rc1), s1 = bf2f(rs1);
+        a = rbf(bf2f(rnw0) * rbf(a * rstd));
+        b = rbf(bf2f(rnw1) * rbf(b * rstd));
         const float ra = rbf(rbf(a * c0) - rbf(b * s0));
         const float rb = rbf(rbf(b * c1) + rbf(a * s1));
         s_qkv[wave * HD + lane] = ra;
@@ -269,24 +407,18 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         dst[lane] = (uint16_t)f2bf(src[lane]);
         dst[64 + lane] = (uint16_t)f2bf(src[64 + lane]);
       }
-      // ---- this workgroup's chunk of positions
-      const int c_begin = j * CH;
-      const int c_end = min(n_ctx, c_begin + CH);
-      const int grp = lane >> 4, d0 = (lane & 15) * 8;
       float q0[8], q1[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         q0[i] = s_qkv[d0 + i];
         q1[i] = s_qkv[HD + d0 + i];
       }
-      const uint16_t* kc = P.k_cache + layer * kv_layer_stride + (size_t)g * P.max_seq_len * HD;
-      const uint16_t* vc = P.v_cache + layer * kv_layer_stride + (size_t)g * P.max_seq_len * HD;
       float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;
       float a0[8], a1[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) a0[i] = a1[i] = 0.f;
       const float scale = P.attn_scale;
-      for (int pos = c_begin + wave * 4 + grp; pos < c_end; pos += 16) {
+      auto step = [&](int pos, const u32x4& Kw, const u32x4& Vw) {
         float kf[8], vf[8];
         if (pos == p) {
 #pragma unroll
@@ -295,8 +427,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             vf[i] = s_qkv[3 * HD + d0 + i];
           }
         } else {
-          unpack8(ldw(kc + (size_t)pos * HD + d0), kf);
-          unpack8(ldw(vc + (size_t)pos * HD + d0), vf);
+          unpack8(Kw, kf);
+          unpack8(Vw, vf);
         }
         float d0s = 0.f, d1s = 0.f;
 #pragma unroll
@@ -304,8 +436,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           d0s = fmaf(q0[i], kf[i], d0s);
           d1s = fmaf(q1[i], kf[i], d1s);
         }
-        const float s0 = group16_sum(d0s) * scale;
-        const float s1 = group16_sum(d1s) * scale;
+        const float s0 = row16_sum(d0s) * scale;
+        const float s1 = row16_sum(d1s) * scale;
         const float n0 = fmaxf(m0, s0), n1 = fmaxf(m1, s1);
         const float al0 = expf(m0 - n0), al1 = expf(m1 - n1);
         const float p0 = expf(s0 - n0), p1 = expf(s1 - n1);
@@ -318,196 +450,206 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         }
         m0 = n0;
         m1 = n1;
-      }
-      // merge the 4 position groups of this wave (lanes 16 apart)
+      };
 #pragma unroll
-      for (int off = 16; off < 64; off <<= 1) {
-        const float om0 = __shfl_xor(m0, off, 64), om1 = __shfl_xor(m1, off, 64);
-        const float ol0 = __shfl_xor(l0, off, 64), ol1 = __shfl_xor(l1, off, 64);
-        const float n0 = fmaxf(m0, om0), n1 = fmaxf(m1, om1);
-        const float e0a = n0 == -INFINITY ? 0.f : expf(m0 - n0), e0b = n0 == -INFINITY ? 0.f : expf(om0 - n0);
-        const float e1a = n1 == -INFINITY ? 0.f : expf(m1 - n1), e1b = n1 == -INFINITY ? 0.f : expf(om1 - n1);
+      for (int u = 0; u < PF; u++) {
+        const int pos = pos0 + 16 * u;
+        if (pos < c_end) step(pos, KP[u], VP[u]);
+      }
+      // rounds beyond the prefetch window: two batches of 4 rounds in flight
+      auto load_batch = [&](int r0, u32x4 (&K)[4], u32x4 (&V)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int pos = pos0 + 16 * (r0 + u);
+          if (pos < c_end && pos != p) {
+            K[u] = ldw(kc + (size_t)pos * HD);
+            V[u] = ldw(vc + (size_t)pos * HD);
+          }
+        }
+      };
+      auto run_batch = [&](int r0, const u32x4 (&K)[4], const u32x4 (&V)[4]) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int pos = pos0 + 16 * (r0 + u);
+          if (pos < c_end) step(pos, K[u], V[u]);
+        }
+      };
+      if (nround > PF) {
+        u32x4 KA[4], VA[4], KB[4], VB[4];
+        load_batch(PF, KA, VA);
+        for (int r = PF; r < nround; r += 8) {
+          load_batch(r + 4, KB, VB);
+          run_batch(r, KA, VA);
+          load_batch(r + 8, KA, VA);
+          run_batch(r + 4, KB, VB);
+        }
+      }
+      // merge the 16 partial states (4 waves x 4 lane groups) through LDS:
+      // thread t -> (head t / 128, dim t % 128)
+      {
+        const int st = wave * 4 + grp;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-          const float o0 = __shfl_xor(a0[i], off, 64), o1 = __shfl_xor(a1[i], off, 64);
-          a0[i] = a0[i] * e0a + o0 * e0b;
-          a1[i] = a1[i] * e1a + o1 * e1b;
+          s_att[st][0][2 + d0 + i] = a0[i];
+          s_att[st][1][2 + d0 + i] = a1[i];
         }
-        l0 = l0 * e0a + ol0 * e0b;
-        l1 = l1 * e1a + ol1 * e1b;
-        m0 = n0;
-        m1 = n1;
-      }
-      if (lane < 16) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          s_att[wave][0][2 + d0 + i] = a0[i];
-          s_att[wave][1][2 + d0 + i] = a1[i];
-        }
-        if (lane == 0) {
-          s_att[wave][0][0] = m0;
-          s_att[wave][0][1] = l0;
-          s_att[wave][1][0] = m1;
-          s_att[wave][1][1] = l1;
+        if ((lane & 15) == 0) {
+          s_att[st][0][0] = m0;
+          s_att[st][0][1] = l0;
+          s_att[st][1][0] = m1;
+          s_att[st][1][1] = l1;
         }
       }
       __syncthreads();
-      // merge the 4 waves: thread t -> (head t / 128, dim t % 128)
       const int hh = tid >> 7, dim = tid & 127;
       float M = -INFINITY;
 #pragma unroll
-      for (int v = 0; v < 4; v++) M = fmaxf(M, s_att[v][hh][0]);
+      for (int v = 0; v < 16; v++) M = fmaxf(M, s_att[v][hh][0]);
       float L = 0.f, O = 0.f;
 #pragma unroll
-      for (int v = 0; v < 4; v++) {
+      for (int v = 0; v < 16; v++) {
         const float e = M == -INFINITY ? 0.f : expf(s_att[v][hh][0] - M);
         L = fmaf(s_att[v][hh][1], e, L);
         O = fmaf(s_att[v][hh][2 + dim], e, O);
       }
-      const uint32_t out_word = WS_XATTN + (2 * g + hh) * HD + dim;
+      const uint32_t out_word = lb + LX_ATTN + hh * HD + dim;
       if (nsplit == 1) {
-        wsb.st1(tagged(tag, rbf(O * (1.0f / L))), out_word * 4u);
+        stl1(wsb, out_word, tagged(tag, rbf(O * (1.0f / L))));
       } else {
-        const uint32_t pbase = WS_APART + ((g * WG_PER_XCD + j) * 2 + hh) * APART;
-        wsb.st1(__float_as_uint(O), (pbase + 2 + dim) * 4u);
+        // split partial as (fp32, tag) pairs; workgroup (g, 0) combines them
+        const uint32_t pb = lb + LX_PART + 2 * ((j * 2 + hh) * APART);
+        stl64(wsb, pb + 2 * (2 + dim), O, tag64);
         if (dim == 0) {
-          wsb.st1(__float_as_uint(M), (pbase + 0) * 4u);
-          wsb.st1(__float_as_uint(L), (pbase + 1) * 4u);
+          stl64(wsb, pb + 0, M, tag64);
+          stl64(wsb, pb + 2, L, tag64);
         }
-        wait_vmem();
-        __syncthreads();
-        if (tid == 0) {
-          const uint32_t old = __hip_atomic_fetch_add(ws + WS_ATTN_TICKET + (layer * NKV + g) * 32, 1u,
-                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          s_flag = (old == (uint32_t)(nsplit - 1)) ? 1u : 0u;
-        }
-        __syncthreads();
-        if (s_flag) {
-          // last arriving split combines all partials of this KV group
-          float Mc = -INFINITY;
-          for (int c = 0; c < nsplit; c++) {
-            const uint32_t pb = WS_APART + ((g * WG_PER_XCD + c) * 2 + hh) * APART;
-            Mc = fmaxf(Mc, __uint_as_float(wsb.ld1(pb * 4u)));
+        if (j == 0) {
+          // thread t gathers pairs t, t + NT, ... of the nsplit * 2 * APART partial values
+          const int total = nsplit * 2 * APART;
+          constexpr int MAXL = (WG_PER_XCD * 2 * APART + NT - 1) / NT;  // 33
+          u32x2 v[MAXL];
+#pragma unroll
+          for (int k = 0; k < MAXL; k++) {
+            const int i = tid + NT * k;
+            if (i < total) v[k] = ldl64(wsb, lb + LX_PART + 2 * i);
           }
+#pragma unroll
+          for (int k = 0; k < MAXL; k++) {
+            const int i = tid + NT * k;
+            if (i < total) s_part[i] = repoll_l64(wsb, ws, lb + LX_PART + 2 * i, tag64, v[k]);
+          }
+          __syncthreads();
+          float Mc = -INFINITY;
+          for (int c = 0; c < nsplit; c++) Mc = fmaxf(Mc, s_part[(c * 2 + hh) * APART]);
           float Lc = 0.f, Oc = 0.f;
           for (int c = 0; c < nsplit; c++) {
-            const uint32_t pb = WS_APART + ((g * WG_PER_XCD + c) * 2 + hh) * APART;
-            const float mc = __uint_as_float(wsb.ld1(pb * 4u));
-            const float lc = __uint_as_float(wsb.ld1((pb + 1) * 4u));
-            const float oc = __uint_as_float(wsb.ld1((pb + 2 + dim) * 4u));
-            const float e = mc == -INFINITY ? 0.f : expf(mc - Mc);
-            Lc = fmaf(lc, e, Lc);
-            Oc = fmaf(oc, e, Oc);
+            const float* pc = &s_part[(c * 2 + hh) * APART];
+            const float e = pc[0] == -INFINITY ? 0.f : expf(pc[0] - Mc);
+            Lc = fmaf(pc[1], e, Lc);
+            Oc = fmaf(pc[2 + dim], e, Oc);
           }
-          wsb.st1(tagged(tag, rbf(Oc * (1.0f / Lc))), out_word * 4u);
+          stl1(wsb, out_word, tagged(tag, rbf(Oc * (1.0f / Lc))));
         }
       }
     }
 
-    // ============ stage 3: o_proj rows 4w..4w+3, residual ============
+    // ============ stage 3: o_proj columns of heads 2g, 2g+1 for rows [32j, 32j+32) ============
+    // thread t: 16-byte column chunk c = t & 31 (columns 256g + 8c ..), rows rg + 8i with
+    // rg = t >> 5 (so wave v holds rows 2v, 2v+1 (+8i)).
     {
-      const uint16_t* wo = (const uint16_t*)LW.o_proj_weight;
+      const int c = tid & 31, rg = tid >> 5;
+      const uint16_t* wo = LW[W_O] + 256 * g + 8 * c;
       u32x4 wv[4];
 #pragma unroll
-      for (int k = 0; k < 4; k++) wv[k] = ldw(wo + (size_t)(4 * w + k) * QS + 8 * tid);
-      const u32x4 va = poll4(wsb, ws, WS_XATTN + 8 * tid, tag);
-      const u32x4 vb = poll4(wsb, ws, WS_XATTN + 8 * tid + 4, tag);
-      const float x[8] = {bflo(va.x), bflo(va.y), bflo(va.z), bflo(va.w),
-                          bflo(vb.x), bflo(vb.y), bflo(vb.z), bflo(vb.w)};
-      float acc[4];
+      for (int i = 0; i < 4; i++) wv[i] = ldw(wo + (size_t)(ROWS * j + rg + 8 * i) * QS);
+      float x[8];
+      gather8_local(wsb, ws, lb + LX_ATTN + 8 * c, tag, x);
 #pragma unroll
-      for (int k = 0; k < 4; k++) acc[k] = wave_sum(dot8(wv[k], x));
-      if (lane == 0) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) s_red[wave][k] = acc[k];
+      for (int i = 0; i < 4; i++) {
+        const float s = row16_sum(dot8(wv[i], x));
+        // lanes 0-31 hold row 2*wave + 8i (rows 0, 1 of the wave), lanes 32-63 row 2*wave+1 + 8i
+        const float lo = readlane(s, 0) + readlane(s, 16);
+        const float hi = readlane(s, 32) + readlane(s, 48);
+        const int r0 = 2 * wave + 8 * i;
+        if (lane == 0) stx64(wsb, WS_OPART + 2 * ((j * ROWS + r0) * NXCD + g), lo, tag64);
+        if (lane == 32) stx64(wsb, WS_OPART + 2 * ((j * ROWS + r0 + 1) * NXCD + g), hi, tag64);
       }
-      __syncthreads();
-      if (tid < 4) {
-        const float o = rbf((s_red[0][tid] + s_red[1][tid]) + (s_red[2][tid] + s_red[3][tid]));
-        const float h1 = rbf(s_h[4 * w + tid] + o);
-        wsb.st1(tagged(tag, h1), (WS_XH1 + 4 * w + tid) * 4u);
+      // residual rows: h1 = bf16(h + bf16(o)), o summed over the 8 XCDs
+      if (tid < ROWS) {
+        const float h1 = reduce_rows(wsb, ws, WS_OPART, j, tid, tag64, s_rh[tid]);
+        s_rh1[tid] = h1;
+        stl1(wsb, lb + LX_H1 + ROWS * j + tid, tagged(tag, h1));
       }
     }
 
     // ============ stage 4: post-attention RMSNorm, gate/up rows, SiLU * up ============
+    // units u0 + [0, 12) with u0 = 384g + 12j; threads 0-127 gate rows, 128-255 up rows.
     {
       const int cc = tid & 127, half = tid >> 7;
-      const uint16_t* wm = (const uint16_t*)(half == 0 ? LW.gate_proj_weight : LW.up_proj_weight);
-      u32x4 wv[12];
+      const int u0 = XUNITS * g + UNITS * j;
+      const uint16_t* wm = half == 0 ? LW[W_G] : LW[W_U];
+      const u32x2 wln = ldw2(LW[W_POST] + tid * 4);
+      u32x4 wv[UNITS];
 #pragma unroll
-      for (int r = 0; r < 12; r++) wv[r] = ldw(wm + (size_t)(12 * w + r) * H + 8 * cc);
-      gather_lds(wsb, ws, WS_XH1, H, tag, s_h1);
+      for (int r = 0; r < UNITS; r++) wv[r] = ldw(wm + (size_t)(u0 + r) * H + 8 * cc);
+      gather_local_h(wsb, ws, lb + LX_H1, tag, s_h);
       __syncthreads();
-      block_rmsnorm(s_h1, (const uint16_t*)LW.post_attn_layernorm_weight, s_y, &s_red[0][0]);
+      block_rmsnorm(s_h, wln, s_y, &s_red[0][0]);
       float x[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) x[i] = s_y[8 * cc + i];
-      float acc[12];
+      float acc[UNITS];
 #pragma unroll
-      for (int r = 0; r < 12; r++) acc[r] = wave_sum(dot8(wv[r], x));
+      for (int r = 0; r < UNITS; r++) acc[r] = wave_sum(dot8(wv[r], x));
       if (lane == 0) {
 #pragma unroll
-        for (int r = 0; r < 12; r++) s_red[wave][r] = acc[r];
+        for (int r = 0; r < UNITS; r++) s_red[wave][r] = acc[r];
       }
       __syncthreads();
-      if (tid < 12) {
+      if (tid < UNITS) {
         // HF Qwen3MLP (modeling_qwen3.py:81-83): bf16(bf16(silu(gate)) * up)
         const float gt = rbf(s_red[0][tid] + s_red[1][tid]);
         const float up = rbf(s_red[2][tid] + s_red[3][tid]);
         const float sl = rbf(gt / (1.0f + expf(-gt)));
-        wsb.st1(tagged(tag, rbf(sl * up)), (WS_XM + 12 * w + tid) * 4u);
+        stl1(wsb, lb + LX_M + UNITS * j + tid, tagged(tag, rbf(sl * up)));
       }
     }
 
-    // ============ stage 5: down_proj rows 4w..4w+3, residual ============
+    // ============ stage 5: down_proj columns of this XCD's units for rows [32j, 32j+32) ============
+    // wave v: rows 8v + i (i < 8); lane l < 48: 16-byte column chunk l (columns 384g + 8l ..).
     {
-      const uint16_t* wd = (const uint16_t*)LW.down_proj_weight;
-      const bool two = tid < 128;
-      u32x4 wv[4], wv2[4];
+      const bool act = lane < 48;
+      const uint16_t* wd = LW[W_D] + XUNITS * g + 8 * lane;
+      u32x4 wv[8];
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        wv[k] = ldw(wd + (size_t)(4 * w + k) * I + 8 * tid);
-        if (two) wv2[k] = ldw(wd + (size_t)(4 * w + k) * I + 2048 + 8 * tid);
+      for (int i = 0; i < 8; i++) {
+        if (act) wv[i] = ldw(wd + (size_t)(ROWS * j + 8 * wave + i) * I);
       }
-      const u32x4 ma = poll4(wsb, ws, WS_XM + 8 * tid, tag);
-      const u32x4 mb = poll4(wsb, ws, WS_XM + 8 * tid + 4, tag);
-      const float x[8] = {bflo(ma.x), bflo(ma.y), bflo(ma.z), bflo(ma.w),
-                          bflo(mb.x), bflo(mb.y), bflo(mb.z), bflo(mb.w)};
-      float x2[8];
-      if (two) {
-        const u32x4 mc = poll4(wsb, ws, WS_XM + 2048 + 8 * tid, tag);
-        const u32x4 md = poll4(wsb, ws, WS_XM + 2048 + 8 * tid + 4, tag);
-        x2[0] = bflo(mc.x); x2[1] = bflo(mc.y); x2[2] = bflo(mc.z); x2[3] = bflo(mc.w);
-        x2[4] = bflo(md.x); x2[5] = bflo(md.y); x2[6] = bflo(md.z); x2[7] = bflo(md.w);
-      }
-      float acc[4];
+      float x[8];
+      if (act) gather8_local(wsb, ws, lb + LX_M + 8 * lane, tag, x);
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        float s = dot8(wv[k], x);
-        if (two) s += dot8(wv2[k], x2);
-        acc[k] = wave_sum(s);
+      for (int i = 0; i < 8; i++) {
+        const float s = wave_sum(act ? dot8(wv[i], x) : 0.f);
+        if (lane == 0) stx64(wsb, WS_DPART + 2 * ((j * ROWS + 8 * wave + i) * NXCD + g), s, tag64);
       }
-      __syncthreads();  // s_red reuse
-      if (lane == 0) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) s_red[wave][k] = acc[k];
-      }
-      __syncthreads();
-      if (tid < 4) {
-        const float d = rbf((s_red[0][tid] + s_red[1][tid]) + (s_red[2][tid] + s_red[3][tid]));
-        const float hn = rbf(s_h1[4 * w + tid] + d);
-        wsb.st1(tagged(tag, hn), (WS_XH + 4 * w + tid) * 4u);
+      // residual rows: h' = bf16(h1 + bf16(d)), d summed over the 8 XCDs
+      if (tid < ROWS) {
+        const float hn = reduce_rows(wsb, ws, WS_DPART, j, tid, tag64, s_rh1[tid]);
+        s_rh[tid] = hn;
+        stl1(wsb, lb + LX_H + ROWS * j + tid, tagged(tag, hn));
       }
     }
   }
 
   // ============ final norm + tied LM head + argmax ============
   const int last = P.num_layers - 1;
-  gather_lds(wsb, ws, WS_XH, H, tag_of(epoch, last), s_h);
-  __syncthreads();
   // The single-block entry (MODE_NO_LMHEAD) passes no final-norm weight.
   const bool lm = !(P.mode & MODE_NO_LMHEAD);
-  if (lm) block_rmsnorm(s_h, P.final_norm, s_y, &s_red[0][0]);
+  u32x2 wfn = {0u, 0u};
+  if (lm) wfn = ldw2(P.final_norm + tid * 4);
+  gather_local_h(wsb, ws, lb + LX_H, tag_of(epoch, last), s_h);
+  __syncthreads();
+  if (lm) block_rmsnorm(s_h, wfn, s_y, &s_red[0][0]);
   if (w == 0) {
     for (int i = tid; i < H; i += NT) {
       P.hidden_out[i] = (uint16_t)f2bf(s_h[i]);
@@ -516,7 +658,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   }
   float bestv = -INFINITY;
   int besti = 0x7fffffff;
-  if (!(P.mode & MODE_NO_LMHEAD)) {
+  if (lm) {
     const int r0 = w < 128 ? w * 594 : 128 * 594 + (w - 128) * 593;
     const int r1 = r0 + (w < 128 ? 594 : 593);
     float x0[8], x1[8];
@@ -526,33 +668,39 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       x1[i] = s_y[512 + 8 * lane + i];
     }
     const bool want_logits = (P.mode & MODE_LOGITS) != 0;
-    int r = r0 + wave;
-    for (; r + 12 < r1; r += 16) {
-      u32x4 wv[4][2];
+    // wave `wave` takes rows r0 + wave + 4*i, four rows per batch, two batches in flight
+    auto load_rows = [&](int rb, u32x4 (&Wr)[4][2]) {
 #pragma unroll
       for (int u = 0; u < 4; u++) {
-        const uint16_t* row = P.lm_head + (size_t)(r + 4 * u) * H;
-        wv[u][0] = ldw(row + 8 * lane);
-        wv[u][1] = ldw(row + 512 + 8 * lane);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const float v = rbf(wave_sum(dot8(wv[u][0], x0) + dot8(wv[u][1], x1)));
-        if (want_logits && lane == 0) P.logits_out[r + 4 * u] = v;
-        if (v > bestv) {
-          bestv = v;
-          besti = r + 4 * u;
+        const int r = rb + 4 * u;
+        if (r < r1) {
+          const uint16_t* row = P.lm_head + (size_t)r * H;
+          Wr[u][0] = ldw(row + 8 * lane);
+          Wr[u][1] = ldw(row + 512 + 8 * lane);
         }
       }
-    }
-    for (; r < r1; r += 4) {
-      const uint16_t* row = P.lm_head + (size_t)r * H;
-      const float v = rbf(wave_sum(dot8(ldw(row + 8 * lane), x0) + dot8(ldw(row + 512 + 8 * lane), x1)));
-      if (want_logits && lane == 0) P.logits_out[r] = v;
-      if (v > bestv) {
-        bestv = v;
-        besti = r;
+    };
+    auto score_rows = [&](int rb, const u32x4 (&Wr)[4][2]) {
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int r = rb + 4 * u;
+        if (r < r1) {
+          const float v = rbf(wave_sum(dot8(Wr[u][0], x0) + dot8(Wr[u][1], x1)));
+          if (want_logits && lane == 0) P.logits_out[r] = v;
+          if (v > bestv) {
+            bestv = v;
+            besti = r;
+          }
+        }
       }
+    };
+    u32x4 WA[4][2], WB[4][2];
+    load_rows(r0 + wave, WA);
+    for (int rb = r0 + wave; rb < r1; rb += 32) {
+      load_rows(rb + 16, WB);
+      score_rows(rb, WA);
+      load_rows(rb + 32, WA);
+      score_rows(rb + 16, WB);
     }
     if (lane == 0) {
       s_bestv[wave] = bestv;
@@ -581,7 +729,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __syncthreads();
   if (!s_flag) return;
   int tok = 0;
-  if (!(P.mode & MODE_NO_LMHEAD)) {
+  if (lm) {
     float v = __uint_as_float(wsb.ld1((WS_LMPART + 2 * tid) * 4u));
     int i = (int)wsb.ld1((WS_LMPART + 2 * tid + 1) * 4u);
 #pragma unroll
@@ -615,7 +763,6 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     wsb.st1(0u, WS_FINAL_TICKET * 4u);
     wsb.st1(epoch + 1u, WS_EPOCH * 4u);
   }
-  for (int i = tid; i < P.num_layers * NKV; i += NT) wsb.st1(0u, (WS_ATTN_TICKET + i * 32) * 4u);
 }
 
 // ---------------------------------------------------------------- host side
@@ -655,6 +802,7 @@ static int launch(DecodeParams& P, hipStream_t stream) {
   const int st = ensure_device(dev);
   if (st != MQ_OK) return st;
   P.ws = g_dev[dev].ws;
+  if (!P.out_token) P.out_token = reinterpret_cast<int*>(g_dev[dev].ws + WS_WORDS);
   void* args[] = {&P};
   const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mq_decode_kernel), dim3(NWG),
                                                   dim3(NT), args, 0, stream);
@@ -740,12 +888,8 @@ extern "C" int mq_decode_layer(const void* hidden_in, void* hidden_out, const LD
   P.max_seq_len = max_seq_len;
   P.attn_scale = attn_scale;
   P.mode = MODE_INPUT_HIDDEN | MODE_NO_LMHEAD;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return MQ_ERR_HIP;
-  if (ensure_device(dev) != MQ_OK) return g_dev[dev].status;
-  // The kernel reports watchdog errors through the token slot; this entry has
-  // no token output, so it uses a word of the workspace tail.
-  P.out_token = reinterpret_cast<int*>(g_dev[dev].ws + WS_WORDS);
+  // No token output: the kernel's status word goes to the workspace tail.
+  P.out_token = nullptr;
   return launch(P, stream);
 }
 
