@@ -21,6 +21,10 @@ constexpr float EPS = 1e-6f;
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x3 __attribute__((ext_vector_type(3)));
+typedef short bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ bf16
 __device__ __forceinline__ float bf2f(uint32_t b16) { return __uint_as_float(b16 << 16); }
@@ -53,6 +57,30 @@ __device__ __forceinline__ float dot8(const u32x4& w, const float (&x)[8]) {
   return s;
 }
 
+// Two bf16 values (low half first) in one word.
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+
+// acc + w.lo * x.lo + w.hi * x.hi on one word of bf16 pairs (v_dot2_f32_bf16: the
+// products are exact in fp32, the sum is accumulated in fp32).
+__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, x), acc, false);
+}
+// acc + (8 bf16 weights) . (8 bf16 inputs), both as 16-byte chunks.
+__device__ __forceinline__ float dot_chunk(const u32x4& w, const u32x4& x, float acc) {
+  acc = dot2(w.x, x.x, acc);
+  acc = dot2(w.y, x.y, acc);
+  acc = dot2(w.z, x.z, acc);
+  return dot2(w.w, x.w, acc);
+}
+
+// 16x16x32 bf16 matrix product-accumulate. For A (16 x 32) lane l holds row l % 16,
+// for B (32 x 16) column l % 16, each as 8 values of the k range owned by lane group
+// l / 16 (the same k order in A and B); D lane l holds rows 4 * (l / 16) + e of column l % 16.
+__device__ __forceinline__ f32x4 mfma_16x16x32(const u32x4& a, const u32x4& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                  0, 0);
+}
+
 // ------------------------------------------------------------------ wave64 reductions
 // DPP row operations (16-lane rows): quad_perm [1,0,3,2] and [2,3,0,1] pair
 // lanes within quads, row_half_mirror pairs lane i with 7-i, row_mirror lane i
@@ -75,6 +103,36 @@ __device__ __forceinline__ float readlane(float v, int l) {
 __device__ __forceinline__ float wave_sum(float v) {
   v = row16_sum(v);
   return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
+}
+
+// ------------------------------------------------------------------ global loads
+// Pointers that arrive through structs in device memory have no known address
+// space; loading through an explicit global pointer gives global_load (counted in
+// vmcnt only) instead of a flat load (which also counts in lgkmcnt and would make
+// every LDS wait wait for the weight stream as well).
+typedef const __attribute__((address_space(1))) u32x4 gu32x4;
+typedef const __attribute__((address_space(1))) u32x2 gu32x2;
+typedef const __attribute__((address_space(1))) uint32_t gu32;
+typedef const __attribute__((address_space(1))) uint16_t gu16;
+__device__ __forceinline__ u32x4 ldw(const uint16_t* p) { return *(gu32x4*)(p); }
+__device__ __forceinline__ u32x2 ldw2(const uint16_t* p) { return *(gu32x2*)(p); }
+__device__ __forceinline__ uint32_t ldw1(const uint16_t* p) { return *(gu32*)(p); }
+__device__ __forceinline__ uint32_t ldraw16(const uint16_t* p) { return *(gu16*)(p); }
+
+// A pointer that is the same in every lane, moved to scalar registers.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
 }
 
 // ------------------------------------------------------------------ device-coherent access

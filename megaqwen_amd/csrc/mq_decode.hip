@@ -5,30 +5,42 @@
 // reference's ldg_decode_kernel + ldg_lm_head_phase1/2
 // (csrc/megakernel/fused_decode_ldg.cu:617-887).
 //
-// Layout on the chip: 256 workgroups x 256 threads (4 waves of 64), one per
-// CU. A cooperative launch places workgroup w on XCD g = w % 8 as its j = w / 8
-// -th member. XCD g owns KV group g end to end:
-//   * the 512 q/k/v rows of group g (16 rows per workgroup),
-//   * the attention of its two query heads (split over positions),
-//   * the o_proj columns of those two heads (all 1024 rows, 32 per workgroup),
-//   * MLP units [384g, 384g+384): their gate/up rows and down_proj columns.
-// Every workgroup streams the same 120 KB of weights per layer. The only
-// data that crosses XCDs are the o_proj and down_proj partial sums: workgroup
-// (g, j) owns residual-stream rows [32j, 32j+32) and reduces them from the 8
-// XCDs' partials, so each XCD keeps a full copy of the residual stream.
+// Chip layout: 256 workgroups (one per CU; a cooperative launch puts workgroup
+// w on XCD g = w % 8 as its j = w / 8 -th member) of 512 threads. Each
+// workgroup runs two kinds of waves:
+//   * 4 stream waves hold the workgroup's slice of the NEXT layer's weights in
+//     registers: right after a stage consumes its weight registers they are
+//     reloaded with the same stage of the following layer (the LM-head rows
+//     after the last layer), so every weight byte is requested one full layer
+//     before it is needed and HBM latency is off the critical path. Stream
+//     waves only ever issue loads, so the compiler's in-order vmcnt bookkeeping
+//     stays exact across the layer loop.
+//   * 4 exchange waves poll the inter-workgroup exchanges, normalise, apply
+//     residuals and publish results. They never have a weight load queued
+//     ahead of a poll (vector-memory loads retire in order within a wave).
+// Per layer and workgroup w:
+//   q/k/v : 16 rows of KV group g (XCD g owns the group's 512 q/k/v rows)
+//   attn  : workgroup (g, j < nsplit) attends over a chunk of <= 256 positions
+//           for the group's two query heads; K/V rows are copied to LDS by the
+//           stream waves (LDS DMA) one layer ahead; QK^T and PV run on MFMA
+//   o_proj: residual rows 4w..4w+3 over all 2048 attention outputs
+//   MLP   : units 12w..12w+11 (gate and up rows), then down_proj rows 4w..4w+3
+// Every output row is complete inside one workgroup, so each exchange is a
+// single all-gather: a consumer reads the whole (<= 12 KB) vector directly.
 //
 // Exchanges use "tagged words": a bf16 value in the low half of a 32-bit word
 // and a 16-bit tag (launch epoch x 32 + layer) in the high half, or an fp32
 // value with a 32-bit tag in a 64-bit word. A consumer issues all its loads at
-// once and re-polls only words with a stale tag, so an exchange costs one
-// memory round trip and no barrier. Inside an XCD, producers use plain stores
-// and consumers non-temporal loads, which bypass the per-CU L1 and are served
-// by the XCD's shared L2; across XCDs both sides use device-scope (sc1)
-// accesses. A watchdog bounds every poll.
+// once and re-polls only stale words, so an exchange costs one memory round
+// trip and no grid barrier. Across XCDs both sides use device-scope (sc1)
+// accesses; inside an XCD producers use plain stores and consumers
+// non-temporal loads, served by the XCD's shared L2. A watchdog bounds every
+// poll and turns a lost producer into an error code instead of a hang.
 //
 // Numerics follow HF Qwen3 in bf16 (transformers/models/qwen3/modeling_qwen3.py):
 // every Linear / norm / RoPE op / residual add / SiLU / product result is
 // rounded to bf16 where HF rounds it, dot products accumulate in fp32, the
+// attention probabilities enter P.V as bf16 (torch's CPU flash kernel), the
 // logits are rounded to bf16 and the argmax takes the lowest index on ties.
 
 #include "mq_common.h"
@@ -39,39 +51,48 @@
 
 #include "../../include/megaqwen_amd.h"
 
+// Instrumentation hook (per-stage timestamps); compiles to nothing by default.
+#ifndef MQ_TRACE
+#define MQ_TRACE(i) ((void)0)
+#endif
+
 namespace mq {
 
 constexpr int NWG = 256;
-constexpr int NT = 256;
+constexpr int NT = 512;
+constexpr int NSW = 4;  // stream waves 0..3
+constexpr int NPW = 2;  // poll waves 4..5; wave 6 reduces the cross-XCD partial sums, wave 7 stores
 constexpr int NXCD = 8;
-constexpr int WG_PER_XCD = NWG / NXCD;  // 32
-constexpr int ROWS = H / WG_PER_XCD;    // residual rows owned per workgroup: 32
-constexpr int UNITS = I / NWG;          // MLP units per workgroup: 12
-constexpr int XUNITS = I / NXCD;        // MLP units per XCD: 384
-// Attention: one workgroup per KV group up to CH_MIN positions; longer contexts
-// are split over up to 32 workgroups of the owning XCD. The first PF rounds
-// of 16 positions are prefetched while the q/k/v rows are still in flight.
-constexpr int CH_MIN = 128;
-constexpr int PF = 8;
+constexpr int WG_PER_XCD = NWG / NXCD;        // 32
+constexpr int ROWS = H / WG_PER_XCD;          // residual-stream rows owned per workgroup: 32
+constexpr int UNITS = I / NWG;                // MLP units per workgroup: 12
+constexpr int XUNITS = I / NXCD;              // MLP units per XCD: 384
+constexpr int KV_CAP = 256;                   // positions per attention workgroup
+constexpr int MAX_CTX = WG_PER_XCD * KV_CAP;  // 8192
+constexpr int LM_PRE = 16;                    // LM-head rows each stream wave loads during the last layer
+// Vector-memory instructions a stream wave issues per layer (q/k/v 8 + input norm 1
+// + q/k norm 1, o_proj 4, gate/up 12 + post norm 1, down 8); the K/V copy of a layer
+// is followed by at least this many before it is needed.
+constexpr int S_LOADS_PER_LAYER = 35;
 
 // Workspace layout, in 32-bit words.
 constexpr uint32_t WS_EPOCH = 0;
 constexpr uint32_t WS_ERR = 32;
 constexpr uint32_t WS_FINAL_TICKET = 64;
-// per-XCD regions (128 KB apart), written and read only by that XCD's workgroups
+// per-XCD regions of tagged bf16 words, written and read only by that XCD's workgroups
 constexpr uint32_t WS_LOCAL = 1024;
 constexpr uint32_t LOCAL_WORDS = 32768;
-constexpr uint32_t LX_H = 0;        // [1024] tagged bf16: residual stream h (layer input)
-constexpr uint32_t LX_H1 = 1024;    // [1024] tagged bf16: residual after attention
-constexpr uint32_t LX_M = 2048;     // [384]  tagged bf16: SiLU(gate) * up of this XCD's units
-constexpr uint32_t LX_ATTN = 2432;  // [256]  tagged bf16: attention output of the two heads
-constexpr uint32_t LX_QKV = 2688;   // [512]  tagged bf16: raw q0, q1, k, v rows
-constexpr uint32_t APART = 130;     // split partial: m, l, o[128]
-constexpr uint32_t LX_PART = 4096;  // [32 splits][2 heads][APART] (fp32, tag) pairs
-// cross-XCD partial sums: [j][row][g] (fp32, tag) pairs
-constexpr uint32_t WS_OPART = WS_LOCAL + NXCD * LOCAL_WORDS;
-constexpr uint32_t WS_DPART = WS_OPART + 2 * WG_PER_XCD * ROWS * NXCD;
-constexpr uint32_t WS_LMPART = WS_DPART + 2 * WG_PER_XCD * ROWS * NXCD;  // [NWG][2]
+constexpr uint32_t LX_H = 0;        // [1024] residual stream after the layer (a full copy per XCD)
+constexpr uint32_t LX_H1 = 1024;    // [1024] residual stream after attention
+constexpr uint32_t LX_QKV = 2048;   // [512]  raw q0, q1, k, v rows of the XCD's KV group
+constexpr uint32_t LX_ATT = 2560;   // [256]  attention output of the group's two query heads
+constexpr uint32_t LX_M = 2816;     // [384]  SiLU(gate) * up of the XCD's MLP units
+constexpr uint32_t APART = 130;     // attention partial of one head: m, l, acc[128]
+constexpr uint32_t LX_PART = 4096;  // [32 chunks][2 heads][APART] (fp32, tag) pairs
+// cross-XCD partial sums: [j][row][xcd] (fp32, tag) pairs
+constexpr uint32_t X_OPART = WS_LOCAL + NXCD * LOCAL_WORDS;
+constexpr uint32_t X_DPART = X_OPART + 2 * WG_PER_XCD * ROWS * NXCD;
+constexpr uint32_t WS_LMPART = X_DPART + 2 * WG_PER_XCD * ROWS * NXCD;  // [NWG][2]: best logit, index
 constexpr uint32_t WS_WORDS = WS_LMPART + NWG * 2;
 constexpr size_t WS_BYTES = ((WS_WORDS * 4 + 4 + 65535) / 65536) * 65536;
 
@@ -81,6 +102,7 @@ constexpr uint32_t ERR_POLL = 1u;
 constexpr int NT_LD = 2;  // non-temporal cache policy: bypasses the CU's L1, served by the XCD's L2
 
 enum : int { MODE_INPUT_HIDDEN = 1, MODE_NO_LMHEAD = 2, MODE_LOGITS = 4 };
+enum { W_IN = 0, W_Q, W_K, W_V, W_QN, W_KN, W_O, W_POST, W_G, W_U, W_D };
 
 struct DecodeParams {
   const LDGLayerWeights* layers;
@@ -105,21 +127,29 @@ struct DecodeParams {
   int mode;
 };
 
+// Workgroup barrier without a memory fence: LDS writes are complete once
+// lgkmcnt reaches zero, and no vector-memory wait is implied, so the stream
+// waves keep their weight loads in flight across it.
+#define BAR() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+// Keeps the compiler from issuing the loads that follow before `v` (which
+// depends on every use of the registers being reloaded) is computed.
+#define AFTER(v) asm volatile("" ::"v"(v) : "memory")
+
 __device__ __forceinline__ uint32_t tag_of(uint32_t epoch, int layer) {
   return 1u + ((epoch * 32u + (uint32_t)layer) % 65535u);
 }
 __device__ __forceinline__ uint32_t tagged(uint32_t tag, float bfval) { return (tag << 16) | f2bf(bfval); }
-
 __device__ __forceinline__ bool tags_ok(const u32x4& v, uint32_t tag) {
   return ((v.x >> 16) == tag) & ((v.y >> 16) == tag) & ((v.z >> 16) == tag) & ((v.w >> 16) == tag);
 }
+// low halves (bf16 values) of two tagged words as one bf16 pair
+__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
 
 // The error word is written and read with sc1 buffer operations only.
 __device__ __noinline__ void raise_error(uint32_t* ws, uint32_t code) {
   __builtin_amdgcn_raw_buffer_store_b32(code, __builtin_amdgcn_make_buffer_rsrc(ws, 0, 0x7fffffff, 0x00020000),
                                         WS_ERR * 4u, 0, SC1);
 }
-
 __device__ __forceinline__ bool watchdog(const Buf& wsb, uint32_t* ws, uint32_t spins) {
   if ((spins & 1023u) == 0 && (spins > POLL_LIMIT || wsb.ld1(WS_ERR * 4u) != 0)) {
     raise_error(ws, ERR_POLL);
@@ -128,21 +158,34 @@ __device__ __forceinline__ bool watchdog(const Buf& wsb, uint32_t* ws, uint32_t 
   return false;
 }
 
+// ---- cross-XCD exchange: device-scope (sc1) loads and stores
+__device__ __forceinline__ u32x4 xld4(const Buf& b, uint32_t word) { return b.ld4(word * 4u); }
+__device__ __forceinline__ void xst4(const Buf& b, uint32_t word, u32x4 v) { b.st4(v, word * 4u); }
+__device__ __forceinline__ void xst1(const Buf& b, uint32_t word, uint32_t v) { b.st1(v, word * 4u); }
+__device__ __forceinline__ u32x4 xrepoll4(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, u32x4 v) {
+  uint32_t spins = 0;
+  while (!tags_ok(v, tag)) {
+    if (watchdog(b, ws, ++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+    v = xld4(b, word);
+  }
+  return v;
+}
+
+// two (fp32, tag) pairs in one 16-byte load
+__device__ __forceinline__ u32x4 xrepoll64x2(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, u32x4 v) {
+  uint32_t spins = 0;
+  while ((v.y != tag) | (v.w != tag)) {
+    if (watchdog(b, ws, ++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+    v = xld4(b, word);
+  }
+  return v;
+}
+
 // ---- XCD-local exchange: plain stores, non-temporal loads (L2)
 __device__ __forceinline__ u32x4 ldl4(const Buf& b, uint32_t word) {
   return __builtin_amdgcn_raw_buffer_load_b128(b.r, word * 4u, 0, NT_LD);
-}
-__device__ __forceinline__ u32x2 ldl64(const Buf& b, uint32_t word) {
-  return __builtin_amdgcn_raw_buffer_load_b64(b.r, word * 4u, 0, NT_LD);
-}
-__device__ __forceinline__ void stl1(const Buf& b, uint32_t word, uint32_t v) {
-  __builtin_amdgcn_raw_buffer_store_b32(v, b.r, word * 4u, 0, 0);
-}
-__device__ __forceinline__ void stl64(const Buf& b, uint32_t word, float v, uint32_t tag) {
-  u32x2 x;
-  x.x = __float_as_uint(v);
-  x.y = tag;
-  __builtin_amdgcn_raw_buffer_store_b64(x, b.r, word * 4u, 0, 0);
 }
 __device__ __forceinline__ u32x4 repoll_l4(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, u32x4 v) {
   uint32_t spins = 0;
@@ -150,6 +193,30 @@ __device__ __forceinline__ u32x4 repoll_l4(const Buf& b, uint32_t* ws, uint32_t 
     if (watchdog(b, ws, ++spins)) break;
     __builtin_amdgcn_s_sleep(1);
     v = ldl4(b, word);
+  }
+  return v;
+}
+__device__ __forceinline__ uint32_t ldl1(const Buf& b, uint32_t word) {
+  return __builtin_amdgcn_raw_buffer_load_b32(b.r, word * 4u, 0, NT_LD);
+}
+__device__ __forceinline__ u32x2 ldl64(const Buf& b, uint32_t word) {
+  return __builtin_amdgcn_raw_buffer_load_b64(b.r, word * 4u, 0, NT_LD);
+}
+__device__ __forceinline__ void stl4(const Buf& b, uint32_t word, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, b.r, word * 4u, 0, 0);
+}
+__device__ __forceinline__ void stl64(const Buf& b, uint32_t word, float v, uint32_t tag) {
+  u32x2 x;
+  x.x = __float_as_uint(v);
+  x.y = tag;
+  __builtin_amdgcn_raw_buffer_store_b64(x, b.r, word * 4u, 0, 0);
+}
+__device__ __forceinline__ uint32_t repoll_l1(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, uint32_t v) {
+  uint32_t spins = 0;
+  while ((v >> 16) != tag) {
+    if (watchdog(b, ws, ++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+    v = ldl1(b, word);
   }
   return v;
 }
@@ -163,516 +230,832 @@ __device__ __forceinline__ float repoll_l64(const Buf& b, uint32_t* ws, uint32_t
   return __uint_as_float(v.x);
 }
 
-// ---- cross-XCD exchange: device-scope (sc1) stores and loads of (fp32, tag) pairs;
-// aligned 8-byte accesses are single-copy atomic
-__device__ __forceinline__ u32x2 ldx64(const Buf& b, uint32_t word) {
-  return __builtin_amdgcn_raw_buffer_load_b64(b.r, word * 4u, 0, SC1);
+// One 16-byte LDS DMA per lane: lane l's 16 bytes at `gptr` land at LDS byte
+// address lds + 16 * l. Issued as inline assembly so that the compiler's vmcnt
+// bookkeeping for the stream waves' register loads ignores it (the waits it
+// derives stay correct, at worst longer); its completion is awaited explicitly.
+// M0 (which carries the LDS address) is saved and restored around it.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gptr), "s"(lds)
+      : "memory");
 }
-__device__ __forceinline__ void stx64(const Buf& b, uint32_t word, float v, uint32_t tag) {
-  u32x2 x;
-  x.x = __float_as_uint(v);
-  x.y = tag;
-  __builtin_amdgcn_raw_buffer_store_b64(x, b.r, word * 4u, 0, SC1);
-}
-__device__ __forceinline__ float repoll_x64(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, u32x2 v) {
-  uint32_t spins = 0;
-  while (v.y != tag) {
-    if (watchdog(b, ws, ++spins)) break;
-    __builtin_amdgcn_s_sleep(1);
-    v = ldx64(b, word);
+
+// K/V rows of a chunk live in LDS as [row][16 chunks of 8 dims], chunk c of row r
+// stored in slot c ^ (r & 15) so that 16 rows read at one chunk hit distinct banks.
+__device__ __forceinline__ uint32_t kv_off(int row, int chunk) { return row * 256 + 16 * (chunk ^ (row & 15)); }
+
+// Stream wave s copies K and V rows [0, nc) of the chunk starting at position c0
+// (except position p, which the layer itself produces) into LDS.
+__device__ __forceinline__ void kv_dma(const DecodeParams& P, int layer, int g, int c0, int nc, int p, uint32_t lds,
+                                       int s, int lane) {
+  const size_t base = ((size_t)(layer * NKV + g) * P.max_seq_len + c0) * HD;
+  const uint16_t* kb = P.k_cache + base;
+  const uint16_t* vb = P.v_cache + base;
+  const int nq = (nc + 3) >> 2;  // one instruction moves 4 rows
+  const int rin = lane >> 4, slot = lane & 15;
+  for (int q = s; q < nq; q += NSW) {
+    const int row = 4 * q + rin;
+    if (row < nc && c0 + row != p) {
+      const int chunk = slot ^ (row & 15);
+      dma16(kb + row * HD + 8 * chunk, lds + q * 1024);
+      dma16(vb + row * HD + 8 * chunk, lds + KV_CAP * 256 + q * 1024);
+    }
   }
-  return __uint_as_float(v.x);
 }
 
-// Weight pointers arrive through the LDGLayerWeights array, so the compiler
-// cannot infer their address space; load through an explicit global pointer
-// (global_load, vmcnt only) rather than a flat load (which also counts in
-// lgkmcnt and would make every LDS wait also wait for the weight stream).
-typedef const __attribute__((address_space(1))) u32x4 gu32x4;
-typedef const __attribute__((address_space(1))) u32x2 gu32x2;
-typedef const __attribute__((address_space(1))) uint16_t gu16;
-__device__ __forceinline__ u32x4 ldw(const uint16_t* p) { return *(gu32x4*)(p); }
-__device__ __forceinline__ u32x2 ldw2(const uint16_t* p) { return *(gu32x2*)(p); }
-__device__ __forceinline__ uint32_t ldraw16(const uint16_t* p) { return *(gu16*)(p); }
+// ---- stream-wave stores: inline assembly, so that the compiler's vmcnt
+// bookkeeping for the stream waves' register loads ignores them (each makes a
+// later wait at most one instruction longer). The exchange waves never store
+// inside the layer loop, so their polls never queue behind a store's write
+// acknowledgement. `dev` stores (sc1) write through to memory for readers on
+// other XCDs; plain stores stay in this XCD's L2.
+__device__ __forceinline__ void st1_dev(uint32_t* p, uint32_t v) {
+  asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st2_dev(uint32_t* p, u32x2 v) {
+  asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st3_dev(uint32_t* p, u32x3 v) {
+  asm volatile("global_store_dwordx3 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st4_dev(uint32_t* p, u32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st1_plain(uint32_t* p, uint32_t v) {
+  asm volatile("global_store_dword %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st2_plain(uint32_t* p, u32x2 v) {
+  asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st4_plain(uint32_t* p, u32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
 
-// Block-wide RMSNorm of s_x[H] (bf16 values held as fp32) with bf16 weight w:
-// HF Qwen3RMSNorm (modeling_qwen3.py:59-64): y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))).
-// `wv` holds this thread's 4 weights (elements 4*tid .. 4*tid+3), loaded by the
-// caller ahead of time so that no global load sits on the reduction's path.
-__device__ __forceinline__ void block_rmsnorm(const float* s_x, const u32x2 wv, float* s_y, float* s_red) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float x[4];
+// ---- stream waves -> store wave hand-off: each stream wave writes its results to
+// LDS and then bumps an LDS counter; the store wave spins on the counter. LDS
+// operations of one wave complete in order, and both sides use DS instructions
+// only (no fences, no vector-memory waits).
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+__device__ __forceinline__ void signal_store(uint32_t* cnt) {
+  asm volatile("" ::: "memory");
+  __hip_atomic_fetch_add((lds_u32*)(cnt), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void wait_count(uint32_t* cnt, uint32_t target) {
+  while (__hip_atomic_load((lds_u32*)(cnt), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
+    __builtin_amdgcn_s_sleep(0);
+  asm volatile("" ::: "memory");
+}
+
+// ---- attention of one chunk for the two query heads of a KV group (all 8 waves)
+// scores s_sc[h][r] = (q_h . k_r) * scale for rows r < nc, -inf for rows nc..255.
+// Rows at or past nc hold stale LDS contents; they are masked by selects only.
+__device__ __forceinline__ void attn_scores(const uint8_t* s_kv, const uint16_t* s_q, float (*s_sc)[KV_CAP], int nc,
+                                            float scale, int v, int lane) {
+  const int r16 = lane & 15, kg = lane >> 4;
+  u32x4 qb[4];
+#pragma unroll
+  for (int s4 = 0; s4 < 4; s4++) {
+    const u32x4 t = *reinterpret_cast<const u32x4*>(s_q + (r16 & 1) * HD + 32 * s4 + 8 * kg);
+    qb[s4] = r16 < 2 ? t : u32x4{0u, 0u, 0u, 0u};
+  }
+  // wave v: row blocks v and v + 8 (16 rows each); a block's K operands are read before its MFMAs
+#pragma unroll 1
+  for (int bb = 0; bb < 2; bb++) {
+    const int row = 16 * (v + 8 * bb) + r16;
+    u32x4 ka[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++) ka[s4] = *reinterpret_cast<const u32x4*>(s_kv + kv_off(row, 4 * s4 + kg));
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++) acc = mfma_16x16x32(ka[s4], qb[s4], acc);
+    if (r16 < 2) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int r = 16 * (v + 8 * bb) + 4 * kg + e;
+        s_sc[r16][r] = r < nc ? acc[e] * scale : -INFINITY;
+      }
+    }
+  }
+}
+
+// Softmax statistics of both heads (every wave computes them); wave 0 also
+// stores the bf16 numerators exp(s - max) for the P.V product (0 past nc).
+__device__ __forceinline__ void attn_softmax(float (*s_sc)[KV_CAP], uint16_t* s_p, int nc, int v, int lane,
+                                             float& M0, float& M1, float& L0, float& L1) {
+  float a[4], b[4];
+  float m0 = -INFINITY, m1 = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int r = lane + 64 * k;
+    a[k] = r < nc ? s_sc[0][r] : -INFINITY;
+    b[k] = r < nc ? s_sc[1][r] : -INFINITY;
+    m0 = fmaxf(m0, a[k]);
+    m1 = fmaxf(m1, b[k]);
+  }
+  M0 = wave_max(m0);
+  M1 = wave_max(m1);
+  float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int r = lane + 64 * k;
+    const float e0 = r < nc ? expf(a[k] - M0) : 0.f;
+    const float e1 = r < nc ? expf(b[k] - M1) : 0.f;
+    l0 += e0;
+    l1 += e1;
+    if (v == 0) {
+      s_p[r] = (uint16_t)f2bf(e0);
+      s_p[KV_CAP + r] = (uint16_t)f2bf(e1);
+    }
+  }
+  L0 = wave_sum(l0);
+  L1 = wave_sum(l1);
+}
+
+// acc[h][d] = sum_r bf16(p_h[r]) * v_r[d] for this wave's 16 dims d = 16v + (lane & 15),
+// scaled by inv0 / inv1 into s_ao. All 8 blocks of 32 rows are processed: past nc
+// both operands are zero (P by the softmax, V by select), so no branch is needed
+// and every LDS read can be issued ahead of the MFMAs.
+__device__ __forceinline__ void attn_pv(const uint8_t* s_kv, const uint16_t* s_p, float (*s_ao)[HD], int nc, int v,
+                                        int lane, float inv0, float inv1) {
+  const int r16 = lane & 15, kg = lane >> 4;
+  const int dim = 16 * v + r16, ch = dim >> 3, within = 2 * (dim & 7);
+  const uint8_t* vbase = s_kv + KV_CAP * 256;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int t0 = 0; t0 < 8; t0 += 2) {
+    u32x4 pa[2], vb[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int rr = 32 * (t0 + u) + 8 * kg;
+      const u32x4 pt = *reinterpret_cast<const u32x4*>(s_p + (r16 & 1) * KV_CAP + rr);
+      pa[u] = r16 < 2 ? pt : u32x4{0u, 0u, 0u, 0u};
+      uint32_t h16[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) h16[e] = *reinterpret_cast<const uint16_t*>(vbase + kv_off(rr + e, ch) + within);
+      uint32_t vw[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        vw[e] = (rr + 2 * e < nc ? h16[2 * e] : 0u) | ((rr + 2 * e + 1 < nc ? h16[2 * e + 1] : 0u) << 16);
+      vb[u] = u32x4{vw[0], vw[1], vw[2], vw[3]};
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) acc = mfma_16x16x32(pa[u], vb[u], acc);
+  }
+  if (kg == 0) {
+    s_ao[0][dim] = acc[0] * inv0;
+    s_ao[1][dim] = acc[1] * inv1;
+  }
+}
+
+// LM-head row r: bf16 logit of x (two 16-byte chunks per lane) against the row's
+// chunks w0, w1; tracks this wave's best (first index on ties) and records the logit.
+__device__ __forceinline__ void lm_score(int r, int r0, const u32x4& w0, const u32x4& w1, const u32x4& x0,
+                                         const u32x4& x1, float* s_lg, int lane, float& bestv, int& besti) {
+  const float v = rbf(wave_sum(dot_chunk(w0, x0, dot_chunk(w1, x1, 0.f))));
+  if (lane == 0) s_lg[r - r0] = v;
+  if (v > bestv) {
+    bestv = v;
+    besti = r;
+  }
+}
+
+// Stream-wave weight registers: one stage's slice each.
+struct StreamRegs {
+  u32x4 a[8];    // q/k/v: 4 rows x 2 chunks
+  u32x4 o[4];    // o_proj partials: 4 rows x 1 chunk
+  u32x4 gu[12];  // gate rows of 3 units, then their up rows: 6 rows x 2 chunks
+  u32x4 d[8];    // down_proj partials: 8 rows x 1 chunk
+  u32x2 wln;     // input_layernorm elements 4t .. 4t+3
+  u32x2 wpost;   // post_attention_layernorm elements 4t .. 4t+3
+  uint32_t qkn;  // q_norm (t < 64) / k_norm (t >= 64) elements 2t, 2t+1 (mod 128)
+};
+
+// Exchange waves: one 16-byte chunk (4 tagged words) as fp32 values.
+__device__ __forceinline__ void unpack_tagged(const u32x4& v, float* f) {
+  f[0] = bflo(v.x);
+  f[1] = bflo(v.y);
+  f[2] = bflo(v.z);
+  f[3] = bflo(v.w);
+}
+// chunk k (uniform) of four
+__device__ __forceinline__ u32x4 pick4(const u32x4 (&v)[4], int k) {
+  return k == 0 ? v[0] : k == 1 ? v[1] : k == 2 ? v[2] : v[3];
+}
+
+// Poll waves: gather a whole 1024-word XCD-local residual-stream vector (chunks
+// lane + 64k), polled until tagged `tag`; returns the sum of squares of its values.
+__device__ __forceinline__ float gather_local(const Buf& b, uint32_t* ws, uint32_t base, uint32_t tag, int lane,
+                                              u32x4 (&v)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) v[k] = ldl4(b, base + 4 * (lane + 64 * k));
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    x[i] = s_x[tid * 4 + i];
-    ss += x[i] * x[i];
+  for (int k = 0; k < 4; k++) {
+    v[k] = repoll_l4(b, ws, base + 4 * (lane + 64 * k), tag, v[k]);
+    float f[4];
+    unpack_tagged(v[k], f);
+    ss += (f[0] * f[0] + f[1] * f[1]) + (f[2] * f[2] + f[3] * f[3]);
   }
-  ss = wave_sum(ss);
-  if (lane == 0) s_red[wave] = ss;
-  __syncthreads();
-  const float tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-  const float rstd = 1.0f / sqrtf(tot * (1.0f / H) + EPS);
-  const float wf[4] = {bflo(wv.x), bfhi(wv.x), bflo(wv.y), bfhi(wv.y)};
-#pragma unroll
-  for (int i = 0; i < 4; i++) s_y[tid * 4 + i] = rbf(wf[i] * rbf(x[i] * rstd));
-  __syncthreads();
+  return wave_sum(ss);
 }
 
-// Gather the 1024 tagged words of an XCD-local vector into s_dst as fp32.
-__device__ __forceinline__ void gather_local_h(const Buf& b, uint32_t* ws, uint32_t base, uint32_t tag,
-                                               float* s_dst) {
-  const int i = threadIdx.x * 4;
-  const u32x4 x = repoll_l4(b, ws, base + i, tag, ldl4(b, base + i));
-  s_dst[i + 0] = bflo(x.x);
-  s_dst[i + 1] = bflo(x.y);
-  s_dst[i + 2] = bflo(x.z);
-  s_dst[i + 3] = bflo(x.w);
-}
-
-// Gather 8 consecutive XCD-local tagged words starting at `word`.
-__device__ __forceinline__ void gather8_local(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag,
-                                              float (&x)[8]) {
-  u32x4 a = ldl4(b, word);
-  u32x4 c = ldl4(b, word + 4);
-  a = repoll_l4(b, ws, word, tag, a);
-  c = repoll_l4(b, ws, word + 4, tag, c);
-  x[0] = bflo(a.x); x[1] = bflo(a.y); x[2] = bflo(a.z); x[3] = bflo(a.w);
-  x[4] = bflo(c.x); x[5] = bflo(c.y); x[6] = bflo(c.z); x[7] = bflo(c.w);
-}
-
-// Residual rows [32j, 32j+32) of this workgroup: r_out = bf16(r_in + bf16(sum over the 8
-// XCDs' partials in XCD order)); thread r < 32 handles row r. Returns the new row value.
-__device__ __forceinline__ float reduce_rows(const Buf& wsb, uint32_t* ws, uint32_t part_base, int j, int r,
-                                             uint32_t tag64, float r_in) {
-  const uint32_t base = part_base + 2 * ((j * ROWS + r) * NXCD);
-  u32x2 v[NXCD];
-#pragma unroll
-  for (int q = 0; q < NXCD; q++) v[q] = ldx64(wsb, base + 2 * q);
-  float s = 0.f;
-#pragma unroll
-  for (int q = 0; q < NXCD; q++) s += repoll_x64(wsb, ws, base + 2 * q, tag64, v[q]);
-  return rbf(r_in + rbf(s));
+// HF Qwen3RMSNorm (modeling_qwen3.py:59-64) of one chunk: y = bf16(w * bf16(x * rstd)),
+// written as two bf16 pairs.
+__device__ __forceinline__ void norm_chunk(const float* x, float rstd, uint32_t w0, uint32_t w1, uint32_t* dst) {
+  dst[0] = pack_bf2(rbf(bflo(w0) * rbf(x[0] * rstd)), rbf(bfhi(w0) * rbf(x[1] * rstd)));
+  dst[1] = pack_bf2(rbf(bflo(w1) * rbf(x[2] * rstd)), rbf(bfhi(w1) * rbf(x[3] * rstd)));
 }
 
 // ---------------------------------------------------------------- the kernel
 __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
-  __shared__ float s_h[H];      // a full residual-stream vector (h or h1)
-  __shared__ float s_y[H];      // its RMSNorm output
-  __shared__ float s_rh[ROWS];  // this workgroup's rows of h (layer input)
-  __shared__ float s_rh1[ROWS]; // this workgroup's rows of h1
-  __shared__ float s_qkv[4 * HD];
-  __shared__ float s_red[4][16];
-  __shared__ float s_att[16][2][APART];
-  __shared__ float s_part[WG_PER_XCD * 2 * APART];
+  __shared__ __align__(16) uint8_t s_kv[2 * KV_CAP * HD * 2];  // K rows, then V rows of the chunk
+  __shared__ __align__(16) uint32_t s_x0[H / 2];               // normed h or h1 (bf16 pairs)
+  __shared__ __align__(16) uint32_t s_x1[XUNITS / 2];          // attention output or m of the XCD (bf16 pairs)
+  __shared__ __align__(16) uint32_t s_wln[H / 2];              // input_layernorm weights
+  __shared__ __align__(16) uint32_t s_wpost[H / 2];            // post_attention_layernorm weights
+  __shared__ __align__(16) uint32_t s_wfn[H / 2];              // final norm weights
+  __shared__ uint32_t s_qkn[HD];                               // q_norm words, then k_norm words
+  __shared__ float s_cos[HD], s_sin[HD];
+  __shared__ __align__(16) uint16_t s_q[2 * HD];      // normed, rotated q of the two heads
+  __shared__ __align__(16) uint16_t s_p[2 * KV_CAP];  // bf16 softmax numerators
+  __shared__ float s_sc[2][KV_CAP];                    // attention scores, later the combined output
+  __shared__ float s_ao[2][HD];                        // attention output (or unnormalised partial)
+  __shared__ float s_hrow[ROWS];                       // residual rows 32j .. 32j+31 of h
+  __shared__ float s_res[ROWS];                        // stream-wave dot products for the store wave
+  __shared__ uint32_t s_cnt;                           // stream-wave results published so far
+  __shared__ const uint16_t* s_lw[MAX_LAYERS][11];    // weight pointers, copied once per launch
+  __shared__ float s_bestv[8];
+  __shared__ int s_besti[8];
   __shared__ uint32_t s_flag;
-  __shared__ const uint16_t* s_lw[MAX_LAYERS][11];  // weight pointers, copied once per launch
-  __shared__ float s_bestv[4];
-  __shared__ int s_besti[4];
+  float* s_lg = reinterpret_cast<float*>(s_kv);  // this workgroup's logits (K/V rows are dead by then)
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int w = blockIdx.x, g = w & (NXCD - 1), j = w / NXCD;
   uint32_t* ws = P.ws;
   const Buf wsb(ws);
   const uint32_t epoch = wsb.ld1(WS_EPOCH * 4u);
   const uint32_t lb = WS_LOCAL + g * LOCAL_WORDS;  // this XCD's exchange region
-
-  const int p = P.position;
-  const int n_ctx = p + 1;
-  int CH = (n_ctx + WG_PER_XCD - 1) / WG_PER_XCD;
-  CH = CH < CH_MIN ? CH_MIN : CH;
-  CH = (CH + 15) & ~15;
-  const int nsplit = (n_ctx + CH - 1) / CH;
-
-  const size_t kv_layer_stride = (size_t)NKV * P.max_seq_len * HD;
-
-  // The pointer table lives in device memory the kernel also writes to, so the
-  // compiler cannot fetch it with scalar loads; fetch it once into LDS instead of
-  // paying a dependent global round trip before every stage's weight stream.
-  for (int i = tid; i < P.num_layers * 11; i += NT)
-    s_lw[i / 11][i % 11] = reinterpret_cast<const uint16_t* const*>(P.layers)[i];
-  __syncthreads();
-
-  for (int layer = 0; layer < P.num_layers; layer++) {
-    const uint16_t* const* LW = s_lw[layer];
-    enum { W_IN = 0, W_Q, W_K, W_V, W_QN, W_KN, W_O, W_POST, W_G, W_U, W_D };
-    const uint32_t tag = tag_of(epoch, layer);
-    const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
-
-    // ============ stage 1: input RMSNorm + q/k/v rows of KV group g ============
-    // workgroup (g, j) owns rows r = 16j + 4*wave + k of [q_{2g}; q_{2g+1}; k_g; v_g].
-    {
-      const uint16_t* rows[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int r = 16 * j + 4 * wave + k;
-        const uint16_t* base;
-        if (r < 256) base = LW[W_Q] + (size_t)(256 * g + r) * H;
-        else if (r < 384) base = LW[W_K] + (size_t)(128 * g + r - 256) * H;
-        else base = LW[W_V] + (size_t)(128 * g + r - 384) * H;
-        rows[k] = base;
-      }
-      const u32x2 wln = ldw2(LW[W_IN] + tid * 4);
-      u32x4 wq[4][2];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        wq[k][0] = ldw(rows[k] + 8 * lane);
-        wq[k][1] = ldw(rows[k] + 512 + 8 * lane);
-      }
-      if (layer == 0) {
-        const uint16_t* src = (P.mode & MODE_INPUT_HIDDEN) ? P.hidden_in : P.embed + (size_t)P.token * H;
-        const u32x2 v = ldw2(src + tid * 4);
-        s_h[tid * 4 + 0] = bflo(v.x);
-        s_h[tid * 4 + 1] = bfhi(v.x);
-        s_h[tid * 4 + 2] = bflo(v.y);
-        s_h[tid * 4 + 3] = bfhi(v.y);
-        __syncthreads();
-        if (tid < ROWS) s_rh[tid] = s_h[ROWS * j + tid];
-      } else {
-        gather_local_h(wsb, ws, lb + LX_H, tag_of(epoch, layer - 1), s_h);
-      }
-      __syncthreads();
-      block_rmsnorm(s_h, wln, s_y, &s_red[0][0]);
-      float x0[8], x1[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        x0[i] = s_y[8 * lane + i];
-        x1[i] = s_y[512 + 8 * lane + i];
-      }
-      float acc[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) acc[k] = wave_sum(dot8(wq[k][0], x0) + dot8(wq[k][1], x1));
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        if (lane == k) stl1(wsb, lb + LX_QKV + 16 * j + 4 * wave + k, tagged(tag, rbf(acc[k])));
-      }
-    }
-
-    // ============ stage 2: QK-norm, RoPE, KV append, attention ============
-    if (j < nsplit) {
-      // ---- this workgroup's chunk of positions: lane group grp (16 lanes, 8 dims each)
-      // takes positions c_begin + 4*wave + grp + 16*r.
-      const int c_begin = j * CH;
-      const int c_end = min(n_ctx, c_begin + CH);
-      const int grp = lane >> 4, d0 = (lane & 15) * 8;
-      const int pos0 = c_begin + wave * 4 + grp;
-      const int nround = (c_end - c_begin + 15) >> 4;
-      const uint16_t* kc = P.k_cache + layer * kv_layer_stride + (size_t)g * P.max_seq_len * HD + d0;
-      const uint16_t* vc = P.v_cache + layer * kv_layer_stride + (size_t)g * P.max_seq_len * HD + d0;
-      // QK-norm weights and this position's cos/sin first (the in-order load queue would
-      // otherwise put them behind the K/V stream), then K/V of positions < p, which do
-      // not depend on this layer's q/k/v.
-      // (unconditional: a load merged from a branch would be waited for at the merge)
-      const uint16_t* nw = wave < 2 ? LW[W_QN] : LW[W_KN];
-      const uint16_t* ct = P.cos_tab + (size_t)p * HD;
-      const uint16_t* st = P.sin_tab + (size_t)p * HD;
-      const uint32_t rnw0 = ldraw16(nw + lane), rnw1 = ldraw16(nw + 64 + lane);
-      const uint32_t rc0 = ldraw16(ct + lane), rs0 = ldraw16(st + lane);
-      const uint32_t rc1 = ldraw16(ct + 64 + lane), rs1 = ldraw16(st + 64 + lane);
-      u32x4 KP[PF], VP[PF];
-#pragma unroll
-      for (int u = 0; u < PF; u++) {
-        const int pos = pos0 + 16 * u;
-        if (pos < c_end && pos != p) {
-          KP[u] = ldw(kc + (size_t)pos * HD);
-          VP[u] = ldw(vc + (size_t)pos * HD);
-        }
-      }
-      if (tid < 128) {
-        const u32x4 v = repoll_l4(wsb, ws, lb + LX_QKV + 4 * tid, tag, ldl4(wsb, lb + LX_QKV + 4 * tid));
-        s_qkv[4 * tid + 0] = bflo(v.x);
-        s_qkv[4 * tid + 1] = bflo(v.y);
-        s_qkv[4 * tid + 2] = bflo(v.z);
-        s_qkv[4 * tid + 3] = bflo(v.w);
-      }
-      __syncthreads();
-      if (wave < 3) {
-        // HF: q_norm/k_norm over 128 (modeling_qwen3.py:252-253), then apply_rotary_pos_emb (:147-170).
-        float a = s_qkv[wave * HD + lane], b = s_qkv[wave * HD + 64 + lane];
-        const float ss = wave_sum(a * a + b * b);
-        const float rstd = 1.0f / sqrtf(ss * (1.0f / HD) + EPS);
-        const float c0 = bf2f(rc0), s0 = bf2f(rs0), c1 = bf2f(rc1), s1 = bf2f(rs1);
-        a = rbf(bf2f(rnw0) * rbf(a * rstd));
-        b = rbf(bf2f(rnw1) * rbf(b * rstd));
-        const float ra = rbf(rbf(a * c0) - rbf(b * s0));
-        const float rb = rbf(rbf(b * c1) + rbf(a * s1));
-        s_qkv[wave * HD + lane] = ra;
-        s_qkv[wave * HD + 64 + lane] = rb;
-      }
-      __syncthreads();
-      if (j == p / CH && wave >= 2) {
-        // KV-cache append at slot p (bf16 [L][8][max_seq][128]).
-        uint16_t* dst = (wave == 2 ? P.k_cache : P.v_cache) + layer * kv_layer_stride + ((size_t)g * P.max_seq_len + p) * HD;
-        const float* src = &s_qkv[wave * HD];
-        dst[lane] = (uint16_t)f2bf(src[lane]);
-        dst[64 + lane] = (uint16_t)f2bf(src[64 + lane]);
-      }
-      float q0[8], q1[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        q0[i] = s_qkv[d0 + i];
-        q1[i] = s_qkv[HD + d0 + i];
-      }
-      float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;
-      float a0[8], a1[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) a0[i] = a1[i] = 0.f;
-      const float scale = P.attn_scale;
-      auto step = [&](int pos, const u32x4& Kw, const u32x4& Vw) {
-        float kf[8], vf[8];
-        if (pos == p) {
-#pragma unroll
-          for (int i = 0; i < 8; i++) {
-            kf[i] = s_qkv[2 * HD + d0 + i];
-            vf[i] = s_qkv[3 * HD + d0 + i];
-          }
-        } else {
-          unpack8(Kw, kf);
-          unpack8(Vw, vf);
-        }
-        float d0s = 0.f, d1s = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          d0s = fmaf(q0[i], kf[i], d0s);
-          d1s = fmaf(q1[i], kf[i], d1s);
-        }
-        const float s0 = row16_sum(d0s) * scale;
-        const float s1 = row16_sum(d1s) * scale;
-        const float n0 = fmaxf(m0, s0), n1 = fmaxf(m1, s1);
-        const float al0 = expf(m0 - n0), al1 = expf(m1 - n1);
-        const float p0 = expf(s0 - n0), p1 = expf(s1 - n1);
-        l0 = fmaf(l0, al0, p0);
-        l1 = fmaf(l1, al1, p1);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          a0[i] = fmaf(a0[i], al0, p0 * vf[i]);
-          a1[i] = fmaf(a1[i], al1, p1 * vf[i]);
-        }
-        m0 = n0;
-        m1 = n1;
-      };
-#pragma unroll
-      for (int u = 0; u < PF; u++) {
-        const int pos = pos0 + 16 * u;
-        if (pos < c_end) step(pos, KP[u], VP[u]);
-      }
-      // rounds beyond the prefetch window: two batches of 4 rounds in flight
-      auto load_batch = [&](int r0, u32x4 (&K)[4], u32x4 (&V)[4]) {
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const int pos = pos0 + 16 * (r0 + u);
-          if (pos < c_end && pos != p) {
-            K[u] = ldw(kc + (size_t)pos * HD);
-            V[u] = ldw(vc + (size_t)pos * HD);
-          }
-        }
-      };
-      auto run_batch = [&](int r0, const u32x4 (&K)[4], const u32x4 (&V)[4]) {
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const int pos = pos0 + 16 * (r0 + u);
-          if (pos < c_end) step(pos, K[u], V[u]);
-        }
-      };
-      if (nround > PF) {
-        u32x4 KA[4], VA[4], KB[4], VB[4];
-        load_batch(PF, KA, VA);
-        for (int r = PF; r < nround; r += 8) {
-          load_batch(r + 4, KB, VB);
-          run_batch(r, KA, VA);
-          load_batch(r + 8, KA, VA);
-          run_batch(r + 4, KB, VB);
-        }
-      }
-      // merge the 16 partial states (4 waves x 4 lane groups) through LDS:
-      // thread t -> (head t / 128, dim t % 128)
-      {
-        const int st = wave * 4 + grp;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          s_att[st][0][2 + d0 + i] = a0[i];
-          s_att[st][1][2 + d0 + i] = a1[i];
-        }
-        if ((lane & 15) == 0) {
-          s_att[st][0][0] = m0;
-          s_att[st][0][1] = l0;
-          s_att[st][1][0] = m1;
-          s_att[st][1][1] = l1;
-        }
-      }
-      __syncthreads();
-      const int hh = tid >> 7, dim = tid & 127;
-      float M = -INFINITY;
-#pragma unroll
-      for (int v = 0; v < 16; v++) M = fmaxf(M, s_att[v][hh][0]);
-      float L = 0.f, O = 0.f;
-#pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const float e = M == -INFINITY ? 0.f : expf(s_att[v][hh][0] - M);
-        L = fmaf(s_att[v][hh][1], e, L);
-        O = fmaf(s_att[v][hh][2 + dim], e, O);
-      }
-      const uint32_t out_word = lb + LX_ATTN + hh * HD + dim;
-      if (nsplit == 1) {
-        stl1(wsb, out_word, tagged(tag, rbf(O * (1.0f / L))));
-      } else {
-        // split partial as (fp32, tag) pairs; workgroup (g, 0) combines them
-        const uint32_t pb = lb + LX_PART + 2 * ((j * 2 + hh) * APART);
-        stl64(wsb, pb + 2 * (2 + dim), O, tag64);
-        if (dim == 0) {
-          stl64(wsb, pb + 0, M, tag64);
-          stl64(wsb, pb + 2, L, tag64);
-        }
-        if (j == 0) {
-          // thread t gathers pairs t, t + NT, ... of the nsplit * 2 * APART partial values
-          const int total = nsplit * 2 * APART;
-          constexpr int MAXL = (WG_PER_XCD * 2 * APART + NT - 1) / NT;  // 33
-          u32x2 v[MAXL];
-#pragma unroll
-          for (int k = 0; k < MAXL; k++) {
-            const int i = tid + NT * k;
-            if (i < total) v[k] = ldl64(wsb, lb + LX_PART + 2 * i);
-          }
-#pragma unroll
-          for (int k = 0; k < MAXL; k++) {
-            const int i = tid + NT * k;
-            if (i < total) s_part[i] = repoll_l64(wsb, ws, lb + LX_PART + 2 * i, tag64, v[k]);
-          }
-          __syncthreads();
-          float Mc = -INFINITY;
-          for (int c = 0; c < nsplit; c++) Mc = fmaxf(Mc, s_part[(c * 2 + hh) * APART]);
-          float Lc = 0.f, Oc = 0.f;
-          for (int c = 0; c < nsplit; c++) {
-            const float* pc = &s_part[(c * 2 + hh) * APART];
-            const float e = pc[0] == -INFINITY ? 0.f : expf(pc[0] - Mc);
-            Lc = fmaf(pc[1], e, Lc);
-            Oc = fmaf(pc[2 + dim], e, Oc);
-          }
-          stl1(wsb, out_word, tagged(tag, rbf(Oc * (1.0f / Lc))));
-        }
-      }
-    }
-
-    // ============ stage 3: o_proj columns of heads 2g, 2g+1 for rows [32j, 32j+32) ============
-    // thread t: 16-byte column chunk c = t & 31 (columns 256g + 8c ..), rows rg + 8i with
-    // rg = t >> 5 (so wave v holds rows 2v, 2v+1 (+8i)).
-    {
-      const int c = tid & 31, rg = tid >> 5;
-      const uint16_t* wo = LW[W_O] + 256 * g + 8 * c;
-      u32x4 wv[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) wv[i] = ldw(wo + (size_t)(ROWS * j + rg + 8 * i) * QS);
-      float x[8];
-      gather8_local(wsb, ws, lb + LX_ATTN + 8 * c, tag, x);
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float s = row16_sum(dot8(wv[i], x));
-        // lanes 0-31 hold row 2*wave + 8i (rows 0, 1 of the wave), lanes 32-63 row 2*wave+1 + 8i
-        const float lo = readlane(s, 0) + readlane(s, 16);
-        const float hi = readlane(s, 32) + readlane(s, 48);
-        const int r0 = 2 * wave + 8 * i;
-        if (lane == 0) stx64(wsb, WS_OPART + 2 * ((j * ROWS + r0) * NXCD + g), lo, tag64);
-        if (lane == 32) stx64(wsb, WS_OPART + 2 * ((j * ROWS + r0 + 1) * NXCD + g), hi, tag64);
-      }
-      // residual rows: h1 = bf16(h + bf16(o)), o summed over the 8 XCDs
-      if (tid < ROWS) {
-        const float h1 = reduce_rows(wsb, ws, WS_OPART, j, tid, tag64, s_rh[tid]);
-        s_rh1[tid] = h1;
-        stl1(wsb, lb + LX_H1 + ROWS * j + tid, tagged(tag, h1));
-      }
-    }
-
-    // ============ stage 4: post-attention RMSNorm, gate/up rows, SiLU * up ============
-    // units u0 + [0, 12) with u0 = 384g + 12j; threads 0-127 gate rows, 128-255 up rows.
-    {
-      const int cc = tid & 127, half = tid >> 7;
-      const int u0 = XUNITS * g + UNITS * j;
-      const uint16_t* wm = half == 0 ? LW[W_G] : LW[W_U];
-      const u32x2 wln = ldw2(LW[W_POST] + tid * 4);
-      u32x4 wv[UNITS];
-#pragma unroll
-      for (int r = 0; r < UNITS; r++) wv[r] = ldw(wm + (size_t)(u0 + r) * H + 8 * cc);
-      gather_local_h(wsb, ws, lb + LX_H1, tag, s_h);
-      __syncthreads();
-      block_rmsnorm(s_h, wln, s_y, &s_red[0][0]);
-      float x[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) x[i] = s_y[8 * cc + i];
-      float acc[UNITS];
-#pragma unroll
-      for (int r = 0; r < UNITS; r++) acc[r] = wave_sum(dot8(wv[r], x));
-      if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < UNITS; r++) s_red[wave][r] = acc[r];
-      }
-      __syncthreads();
-      if (tid < UNITS) {
-        // HF Qwen3MLP (modeling_qwen3.py:81-83): bf16(bf16(silu(gate)) * up)
-        const float gt = rbf(s_red[0][tid] + s_red[1][tid]);
-        const float up = rbf(s_red[2][tid] + s_red[3][tid]);
-        const float sl = rbf(gt / (1.0f + expf(-gt)));
-        stl1(wsb, lb + LX_M + UNITS * j + tid, tagged(tag, rbf(sl * up)));
-      }
-    }
-
-    // ============ stage 5: down_proj columns of this XCD's units for rows [32j, 32j+32) ============
-    // wave v: rows 8v + i (i < 8); lane l < 48: 16-byte column chunk l (columns 384g + 8l ..).
-    {
-      const bool act = lane < 48;
-      const uint16_t* wd = LW[W_D] + XUNITS * g + 8 * lane;
-      u32x4 wv[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        if (act) wv[i] = ldw(wd + (size_t)(ROWS * j + 8 * wave + i) * I);
-      }
-      float x[8];
-      if (act) gather8_local(wsb, ws, lb + LX_M + 8 * lane, tag, x);
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float s = wave_sum(act ? dot8(wv[i], x) : 0.f);
-        if (lane == 0) stx64(wsb, WS_DPART + 2 * ((j * ROWS + 8 * wave + i) * NXCD + g), s, tag64);
-      }
-      // residual rows: h' = bf16(h1 + bf16(d)), d summed over the 8 XCDs
-      if (tid < ROWS) {
-        const float hn = reduce_rows(wsb, ws, WS_DPART, j, tid, tag64, s_rh1[tid]);
-        s_rh[tid] = hn;
-        stl1(wsb, lb + LX_H + ROWS * j + tid, tagged(tag, hn));
-      }
-    }
-  }
-
-  // ============ final norm + tied LM head + argmax ============
-  const int last = P.num_layers - 1;
-  // The single-block entry (MODE_NO_LMHEAD) passes no final-norm weight.
+  const int L = P.num_layers;
   const bool lm = !(P.mode & MODE_NO_LMHEAD);
-  u32x2 wfn = {0u, 0u};
-  if (lm) wfn = ldw2(P.final_norm + tid * 4);
-  gather_local_h(wsb, ws, lb + LX_H, tag_of(epoch, last), s_h);
-  __syncthreads();
-  if (lm) block_rmsnorm(s_h, wfn, s_y, &s_red[0][0]);
-  if (w == 0) {
-    for (int i = tid; i < H; i += NT) {
-      P.hidden_out[i] = (uint16_t)f2bf(s_h[i]);
-      if (lm && P.normed_out) P.normed_out[i] = s_y[i];
-    }
-  }
+
+  // attention chunking: nsplit chunks of <= KV_CAP positions, chunk j on workgroup (g, j)
+  const int p = P.position, n_ctx = p + 1;
+  const int nsplit = (n_ctx + KV_CAP - 1) / KV_CAP;
+  const int CH = (n_ctx + nsplit - 1) / nsplit;
+  const bool att = j < nsplit;
+  const int c0 = j * CH;
+  const int nc = att ? min(n_ctx, c0 + CH) - c0 : 0;
+  const bool own_p = att && p >= c0 && p < c0 + nc;
+  const bool combine = att && nsplit > 1 && j == 0;
+  const uint32_t lds_kv = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)s_kv;
+
+  // LM-head rows of this workgroup: 594 for w < 128, 593 after (151936 in total)
+  const int r0 = w < 128 ? w * 594 : 128 * 594 + (w - 128) * 593;
+  const int r1 = r0 + (w < 128 ? 594 : 593);
+
   float bestv = -INFINITY;
   int besti = 0x7fffffff;
-  if (lm) {
-    const int r0 = w < 128 ? w * 594 : 128 * 594 + (w - 128) * 593;
-    const int r1 = r0 + (w < 128 ? 594 : 593);
-    float x0[8], x1[8];
+  const u32x4* x0v = reinterpret_cast<const u32x4*>(s_x0);
+  const u32x4* x1v = reinterpret_cast<const u32x4*>(s_x1);
+
+  if (wave < NSW) {
+    // ==================================================================== stream waves
+    const int s = wave, st = tid;  // st: stream thread 0..255
+    for (int i = st; i < L * 11; i += NSW * 64)
+      s_lw[i / 11][i % 11] = reinterpret_cast<const uint16_t* const*>(P.layers)[i];
+    BAR();  // P00: pointer table visible
+    // Weight pointer k of layer l; l >= L (the next-layer loads of the last layer)
+    // maps to layer 0.
+    auto wp = [&](int l, int k) -> const uint16_t* { return uniform_ptr(s_lw[l < L ? l : 0][k]); };
+    // During the last layer the registers are refilled with this wave's first LM-head rows.
+    const uint16_t* lmb = P.lm_head + (size_t)(r0 + LM_PRE * s) * H;
+    const bool lmnext = lm;
+    // o_proj: this lane's 16-byte chunk c of the group's 256 columns, rows 8s + rg + 2i
+    const int oc = lane & 31, org = lane >> 5;
+    // down_proj: lanes < 48 take chunk `lane` of the XCD's 384 columns (the others re-read chunk 47
+    // and are multiplied by zero)
+    const int dch = lane < 48 ? lane : 47;
+
+    StreamRegs R;
+    auto load_a = [&](int l) {
+      R.wln = ldw2(wp(l, W_IN) + 4 * st);
+      R.qkn = ldw1(wp(l, st < 64 ? W_QN : W_KN) + 2 * (st & 63));
+      const int r = 16 * j + 4 * s;  // this wave's 4 rows of the group's [q0; q1; k; v]
+      const uint16_t* pa = (l >= L && lmnext) ? lmb
+                           : r < 256          ? wp(l, W_Q) + (size_t)(256 * g + r) * H
+                           : r < 384          ? wp(l, W_K) + (size_t)(128 * g + r - 256) * H
+                                              : wp(l, W_V) + (size_t)(128 * g + r - 384) * H;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      x0[i] = s_y[8 * lane + i];
-      x1[i] = s_y[512 + 8 * lane + i];
+      for (int k = 0; k < 4; k++) {
+        R.a[2 * k] = ldw(pa + k * H + 8 * lane);
+        R.a[2 * k + 1] = ldw(pa + k * H + 512 + 8 * lane);
+      }
+    };
+    auto load_o = [&](int l) {
+      const bool lmr = l >= L && lmnext;
+      // LM rows 4, 5 of this wave as chunks lane, lane + 64 of two consecutive rows
+      const uint16_t* po = lmr ? lmb + 4 * H : wp(l, W_O) + (size_t)(ROWS * j + 8 * s + org) * QS + 256 * g + 8 * oc;
+#pragma unroll
+      for (int i = 0; i < 4; i++) R.o[i] = ldw(po + (lmr ? 8 * (lane + 64 * i) : (size_t)(2 * i) * QS));
+    };
+    auto load_gu = [&](int l) {
+      R.wpost = ldw2(wp(l, W_POST) + 4 * st);
+      const bool lmr = l >= L && lmnext;
+      const uint16_t* pg = lmr ? lmb + 6 * H : wp(l, W_G) + (size_t)(XUNITS * g + UNITS * j + 3 * s) * H;
+      const uint16_t* pu = lmr ? lmb + 9 * H : wp(l, W_U) + (size_t)(XUNITS * g + UNITS * j + 3 * s) * H;
+#pragma unroll
+      for (int k = 0; k < 3; k++) {
+        R.gu[2 * k] = ldw(pg + k * H + 8 * lane);
+        R.gu[2 * k + 1] = ldw(pg + k * H + 512 + 8 * lane);
+      }
+#pragma unroll
+      for (int k = 0; k < 3; k++) {
+        R.gu[6 + 2 * k] = ldw(pu + k * H + 8 * lane);
+        R.gu[7 + 2 * k] = ldw(pu + k * H + 512 + 8 * lane);
+      }
+    };
+    auto load_d = [&](int l) {
+      const bool lmr = l >= L && lmnext;
+      // LM rows 12 .. 15 of this wave as chunks lane, lane + 64 of four consecutive rows
+      const uint16_t* pd = lmr ? lmb + 12 * H : wp(l, W_D) + (size_t)(ROWS * j + 8 * s) * I + XUNITS * g + 8 * dch;
+#pragma unroll
+      for (int i = 0; i < 8; i++) R.d[i] = ldw(pd + (lmr ? 8 * (lane + 64 * i) : (size_t)i * I));
+    };
+
+    // ---- prologue: layer-0 norms to LDS, layer-0 K/V copy, layer-0 weights in flight
+    {
+      const u32x2 ln0 = ldw2(wp(0, W_IN) + 4 * st);
+      const uint32_t qk0 = ldw1(wp(0, st < 64 ? W_QN : W_KN) + 2 * (st & 63));
+      const u32x2 pn0 = ldw2(wp(0, W_POST) + 4 * st);
+      s_wln[2 * st] = ln0.x;
+      s_wln[2 * st + 1] = ln0.y;
+      s_wpost[2 * st] = pn0.x;
+      s_wpost[2 * st + 1] = pn0.y;
+      if (st < 128) s_qkn[st] = qk0;
+      if (lm) {
+        const u32x2 fn = ldw2(P.final_norm + 4 * st);
+        s_wfn[2 * st] = fn.x;
+        s_wfn[2 * st + 1] = fn.y;
+      }
     }
-    const bool want_logits = (P.mode & MODE_LOGITS) != 0;
-    // wave `wave` takes rows r0 + wave + 4*i, four rows per batch, two batches in flight
+    if (att) kv_dma(P, 0, g, c0, nc, p, lds_kv, s, lane);
+    load_a(0);
+    load_o(0);
+    load_gu(0);
+    load_d(0);
+    BAR();  // P0
+
+    for (int layer = 0; layer < L; layer++) {
+      const int nl = layer + 1;
+      // ---------------- q/k/v rows 16j + 4s .. +3 of the group's [q0; q1; k; v]
+      BAR();  // A1: normed h in s_x0
+      {
+        if (layer > 0) {
+          s_wpost[2 * st] = R.wpost.x;  // this layer's post-attention norm
+          s_wpost[2 * st + 1] = R.wpost.y;
+        }
+        const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
+        float r[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) r[k] = wave_sum(dot_chunk(R.a[2 * k], x0, dot_chunk(R.a[2 * k + 1], x1, 0.f)));
+        if (lane == 0) {
+#pragma unroll
+          for (int k = 0; k < 4; k++) s_res[4 * s + k] = r[k];
+          signal_store(&s_cnt);
+        }
+        AFTER(r[0] + r[1] + r[2] + r[3]);
+        load_a(nl);
+      }
+      if (att) {
+        // this wave's K/V copy of the layer has landed (it was issued before at least
+        // the last S_LOADS_PER_LAYER loads of this wave)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S_LOADS_PER_LAYER) : "memory");
+        BAR();  // B1: q, the new k/v row and the K/V rows are in LDS
+        attn_scores(s_kv, s_q, s_sc, nc, P.attn_scale, wave, lane);
+        BAR();  // B2
+        float M0, M1, L0, L1;
+        attn_softmax(s_sc, s_p, nc, wave, lane, M0, M1, L0, L1);
+        BAR();  // B3
+        attn_pv(s_kv, s_p, s_ao, nc, wave, lane, nsplit == 1 ? 1.0f / L0 : 1.f, nsplit == 1 ? 1.0f / L1 : 1.f);
+        BAR();  // B4: K/V rows consumed
+        if (combine) BAR();  // B5
+        if (nl < L) kv_dma(P, nl, g, c0, nc, p, lds_kv, s, lane);
+      }
+      // ---------------- o_proj partials: rows 32j + 8s + 2i + rg over the group's 256 columns
+      BAR();  // C1: attention output of the group in s_x1
+      {
+        const u32x4 xa = x1v[oc];
+        float r[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[i] = row16_sum(dot_chunk(R.o[i], xa, 0.f));
+        if (lane == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            s_res[8 * s + 2 * i] = readlane(r[i], 0) + readlane(r[i], 16);
+            s_res[8 * s + 2 * i + 1] = readlane(r[i], 32) + readlane(r[i], 48);
+          }
+          signal_store(&s_cnt);
+        }
+        AFTER(r[0] + r[1] + r[2] + r[3]);
+        load_o(nl);
+      }
+      // ---------------- gate/up rows of units 384g + 12j + 3s .. +2
+      BAR();  // D1: normed h1 in s_x0
+      {
+        s_wln[2 * st] = R.wln.x;  // the next layer's input norm and q/k norms
+        s_wln[2 * st + 1] = R.wln.y;
+        if (st < 128) s_qkn[st] = R.qkn;
+        const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
+        float r[6];
+#pragma unroll
+        for (int k = 0; k < 6; k++)
+          r[k] = wave_sum(dot_chunk(R.gu[2 * k], x0, dot_chunk(R.gu[2 * k + 1], x1, 0.f)));
+        if (lane == 0) {
+#pragma unroll
+          for (int k = 0; k < 6; k++) s_res[6 * s + k] = r[k];
+          signal_store(&s_cnt);
+        }
+        AFTER(r[0] + r[1] + r[2] + r[3] + r[4] + r[5]);
+        load_gu(nl);
+      }
+      // ---------------- down_proj partials: rows 32j + 8s + i over the XCD's 384 units
+      BAR();  // E1: m of the XCD in s_x1
+      {
+        const u32x4 xm = lane < 48 ? x1v[lane] : u32x4{0u, 0u, 0u, 0u};
+        float r[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) r[i] = wave_sum(dot_chunk(R.d[i], xm, 0.f));
+        if (lane == 0) {
+#pragma unroll
+          for (int i = 0; i < 8; i++) s_res[8 * s + i] = r[i];
+          signal_store(&s_cnt);
+        }
+        AFTER(r[0] + r[1] + r[2] + r[3] + r[4] + r[5] + r[6] + r[7]);
+        load_d(nl);
+      }
+    }
+    BAR();  // F1: final normed h in s_x0
+    if (lm) {
+      const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
+      const int rb = r0 + LM_PRE * s;
+#pragma unroll
+      for (int k = 0; k < 4; k++) lm_score(rb + k, r0, R.a[2 * k], R.a[2 * k + 1], x0, x1, s_lg, lane, bestv, besti);
+      lm_score(rb + 4, r0, R.o[0], R.o[1], x0, x1, s_lg, lane, bestv, besti);
+      lm_score(rb + 5, r0, R.o[2], R.o[3], x0, x1, s_lg, lane, bestv, besti);
+#pragma unroll
+      for (int k = 0; k < 6; k++)
+        lm_score(rb + 6 + k, r0, R.gu[2 * k], R.gu[2 * k + 1], x0, x1, s_lg, lane, bestv, besti);
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+        lm_score(rb + 12 + k, r0, R.d[2 * k], R.d[2 * k + 1], x0, x1, s_lg, lane, bestv, besti);
+    }
+  } else if (wave < NSW + NPW) {
+    // ==================================================================== poll waves
+    const int c = wave - NSW, pt = tid - NSW * 64;  // pt: poll thread 0..127
+    for (int i = pt; i < 2 * HD; i += NPW * 64) {
+      if (i < HD) s_cos[i] = bf2f(ldraw16(P.cos_tab + (size_t)p * HD + i));
+      else s_sin[i - HD] = bf2f(ldraw16(P.sin_tab + (size_t)p * HD + i - HD));
+    }
+    BAR();  // P00
+    BAR();  // P0
+
+    // RMSNorm of a gathered residual-stream vector (chunks lane + 64k, k < 4): poll wave c
+    // writes the normalised chunks k = 2c, 2c + 1 to s_x0
+    auto norm_out = [&](const u32x4 (&hv)[4], float ss, const uint32_t* wn) {
+      const float rstd = 1.0f / sqrtf(ss * (1.0f / H) + EPS);
+#pragma unroll
+      for (int q = 0; q < 2; q++) {
+        const int k = 2 * c + q;
+        float f[4];
+        unpack_tagged(pick4(hv, k), f);
+        const int ch = lane + 64 * k;
+        norm_chunk(f, rstd, wn[2 * ch], wn[2 * ch + 1], s_x0 + 2 * ch);
+      }
+    };
+    // rows 32j .. 32j+31 (chunks 8j .. 8j+7, all in block k = j / 8) for the reduce wave
+    auto keep_rows = [&](const u32x4 (&hv)[4], float* dst) {
+      const int q = lane - ((8 * j) & 63);
+      if (c == 0 && q >= 0 && q < 8) {
+        float f[4];
+        unpack_tagged(pick4(hv, j >> 3), f);
+#pragma unroll
+        for (int e = 0; e < 4; e++) dst[4 * q + e] = f[e];
+      }
+    };
+
+    u32x4 hv[4];  // the gathered residual stream, chunks lane + 64k
+    for (int layer = 0; layer < L; layer++) {
+      const uint32_t tag = tag_of(epoch, layer);
+      const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
+      MQ_TRACE(1 + layer * 16);
+      // ---------------- gather h (every poll wave reads all 1024 words), RMSNorm
+      float ss;
+      if (layer == 0) {
+        const uint16_t* src = (P.mode & MODE_INPUT_HIDDEN) ? P.hidden_in : P.embed + (size_t)P.token * H;
+        ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const u32x2 v = ldw2(src + 4 * (lane + 64 * k));
+          // widen the raw bf16 values to the tagged layout so every layer reads hv alike
+          hv[k] = u32x4{v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16};
+          float f[4];
+          unpack_tagged(hv[k], f);
+          ss += (f[0] * f[0] + f[1] * f[1]) + (f[2] * f[2] + f[3] * f[3]);
+        }
+        ss = wave_sum(ss);
+      } else {
+        ss = gather_local(wsb, ws, lb + LX_H, tag_of(epoch, layer - 1), lane, hv);
+      }
+      MQ_TRACE(2 + layer * 16);
+      norm_out(hv, ss, s_wln);
+      keep_rows(hv, s_hrow);
+      BAR();  // A1
+      MQ_TRACE(3 + layer * 16);
+      if (att) {
+        // ---------------- QK-norm, RoPE, K/V row p, attention
+        // wave 0: q heads 2g and 2g+1; wave 1: k and v; lane holds dims lane, lane + 64
+        uint32_t u[4];
+        const uint32_t wq = lb + LX_QKV + 2 * HD * c;
+#pragma unroll
+        for (int q = 0; q < 4; q++) u[q] = ldl1(wsb, wq + 64 * q + lane);
+#pragma unroll
+        for (int q = 0; q < 4; q++) u[q] = repoll_l1(wsb, ws, wq + 64 * q + lane, tag, u[q]);
+        MQ_TRACE(4 + layer * 16);
+        // HF: q_norm/k_norm over 128 (modeling_qwen3.py:252-253), then apply_rotary_pos_emb (:147-170)
+        const int nseg = c == 0 ? 2 : 1;  // segments that get QK-norm and RoPE
+        float fr[2][2];
+#pragma unroll
+        for (int sg = 0; sg < 2; sg++) {
+          float fa = bflo(u[2 * sg]), fb = bflo(u[2 * sg + 1]);
+          if (sg < nseg) {
+            const float ssq = wave_sum(fa * fa + fb * fb);
+            const float rstd = 1.0f / sqrtf(ssq * (1.0f / HD) + EPS);
+            const int nw0 = c == 1 ? 64 : 0;
+            const uint32_t na = s_qkn[nw0 + (lane >> 1)], nb = s_qkn[nw0 + 32 + (lane >> 1)];
+            const float wa = (lane & 1) ? bfhi(na) : bflo(na), wb = (lane & 1) ? bfhi(nb) : bflo(nb);
+            fa = rbf(wa * rbf(fa * rstd));
+            fb = rbf(wb * rbf(fb * rstd));
+            const float ra = rbf(rbf(fa * s_cos[lane]) - rbf(fb * s_sin[lane]));
+            const float rb = rbf(rbf(fb * s_cos[lane + 64]) + rbf(fa * s_sin[lane + 64]));
+            fa = ra;
+            fb = rb;
+          }
+          fr[sg][0] = fa;
+          fr[sg][1] = fb;
+        }
+        if (c == 0) {
+#pragma unroll
+          for (int sg = 0; sg < 2; sg++) {
+            s_q[sg * HD + lane] = (uint16_t)f2bf(fr[sg][0]);
+            s_q[sg * HD + 64 + lane] = (uint16_t)f2bf(fr[sg][1]);
+          }
+        } else if (own_p) {
+          // the new k and v rows into the LDS copy (the store wave appends them to the cache)
+          const int row = p - c0;
+          const int o0 = kv_off(row, lane >> 3) + 2 * (lane & 7), o1 = kv_off(row, 8 + (lane >> 3)) + 2 * (lane & 7);
+#pragma unroll
+          for (int sg = 0; sg < 2; sg++) {
+            uint8_t* base = s_kv + sg * (KV_CAP * 256);
+            *reinterpret_cast<uint16_t*>(base + o0) = (uint16_t)f2bf(fr[sg][0]);
+            *reinterpret_cast<uint16_t*>(base + o1) = (uint16_t)f2bf(fr[sg][1]);
+          }
+        }
+        BAR();  // B1
+        attn_scores(s_kv, s_q, s_sc, nc, P.attn_scale, wave, lane);
+        BAR();  // B2
+        float M0, M1, L0, L1;
+        attn_softmax(s_sc, s_p, nc, wave, lane, M0, M1, L0, L1);
+        BAR();  // B3
+        attn_pv(s_kv, s_p, s_ao, nc, wave, lane, nsplit == 1 ? 1.0f / L0 : 1.f, nsplit == 1 ? 1.0f / L1 : 1.f);
+        BAR();  // B4
+        MQ_TRACE(5 + layer * 16);
+        if (combine) {
+          // outputs (hh, dim) = pt, pt + 128: merge the chunk partials of the XCD's workgroups
+#pragma unroll 1
+          for (int o = pt; o < 2 * HD; o += NPW * 64) {
+            const int hh = o >> 7, dim = o & (HD - 1);
+            float Mc = -INFINITY, Lc = 0.f, Oc = 0.f;
+            for (int s0 = 0; s0 < nsplit; s0 += 8) {
+              u32x2 vm[8], vl[8], vo[8];
+#pragma unroll
+              for (int q = 0; q < 8; q++) {
+                const uint32_t b = lb + LX_PART + 2 * (((s0 + q) * 2 + hh) * APART);
+                if (s0 + q < nsplit) {
+                  vm[q] = ldl64(wsb, b);
+                  vl[q] = ldl64(wsb, b + 2);
+                  vo[q] = ldl64(wsb, b + 2 * (2 + dim));
+                }
+              }
+#pragma unroll
+              for (int q = 0; q < 8; q++) {
+                const uint32_t b = lb + LX_PART + 2 * (((s0 + q) * 2 + hh) * APART);
+                if (s0 + q < nsplit) {
+                  const float m = repoll_l64(wsb, ws, b, tag64, vm[q]);
+                  const float l = repoll_l64(wsb, ws, b + 2, tag64, vl[q]);
+                  const float ov = repoll_l64(wsb, ws, b + 2 * (2 + dim), tag64, vo[q]);
+                  const float nm = fmaxf(Mc, m);
+                  const float ea = Mc == -INFINITY ? 0.f : expf(Mc - nm), eb = expf(m - nm);
+                  Lc = Lc * ea + l * eb;
+                  Oc = Oc * ea + ov * eb;
+                  Mc = nm;
+                }
+              }
+            }
+            s_sc[hh][dim] = Oc * (1.0f / Lc);
+          }
+          BAR();  // B5
+        }
+      }
+      // ---------------- o_proj input: the group's 256 attention outputs (poll wave 0)
+      if (c == 0) {
+        u32x4 v = ldl4(wsb, lb + LX_ATT + 4 * lane);
+        v = repoll_l4(wsb, ws, lb + LX_ATT + 4 * lane, tag, v);
+        reinterpret_cast<u32x2*>(s_x1)[lane] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
+      }
+      MQ_TRACE(6 + layer * 16);
+      BAR();  // C1
+      MQ_TRACE(7 + layer * 16);
+      // ---------------- gather h1; post-attention RMSNorm
+      {
+        const float ss1 = gather_local(wsb, ws, lb + LX_H1, tag, lane, hv);
+        MQ_TRACE(8 + layer * 16);
+        norm_out(hv, ss1, s_wpost);
+      }
+      BAR();  // D1
+      MQ_TRACE(9 + layer * 16);
+      // ---------------- down_proj input: m of the XCD's 384 units (96 chunks)
+      {
+        const int q = pt;  // chunks pt, pt + 128 (< 96 only for pt < 96)
+        if (q < XUNITS / 4) {
+          u32x4 v = ldl4(wsb, lb + LX_M + 4 * q);
+          v = repoll_l4(wsb, ws, lb + LX_M + 4 * q, tag, v);
+          reinterpret_cast<u32x2*>(s_x1)[q] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
+        }
+      }
+      MQ_TRACE(10 + layer * 16);
+      BAR();  // E1
+      MQ_TRACE(11 + layer * 16);
+    }
+
+    // ---------------- final norm
+    {
+      const float ss = gather_local(wsb, ws, lb + LX_H, tag_of(epoch, L - 1), lane, hv);
+      MQ_TRACE(1000);
+      if (lm) norm_out(hv, ss, s_wfn);
+      if (w == 0) {
+        // hidden_out / normed_out chunks k = 2c, 2c + 1
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+          const int k = 2 * c + q;
+          float f[4];
+          unpack_tagged(pick4(hv, k), f);
+          const int ch = lane + 64 * k;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            P.hidden_out[4 * ch + e] = (uint16_t)f2bf(f[e]);
+            if (lm && P.normed_out) P.normed_out[4 * ch + e] = bf2f((s_x0[2 * ch + (e >> 1)] >> (16 * (e & 1))) & 0xffffu);
+          }
+        }
+      }
+    }
+    BAR();  // F1
+  } else if (wave == NSW + NPW) {
+    // ==================================================================== reduce wave
+    // Residual rows 32j .. 32j+31 from the 8 XCDs' partial sums (identical on every XCD):
+    // lane -> row lane >> 1, XCDs 4 (lane & 1) .. +3.
+    BAR();  // P00
+    BAR();  // P0
+    const int rr = lane >> 1, hx = lane & 1;
+    float h1v = 0.f;  // h1 row rr (kept for the down_proj residual)
+    // sum of the 8 partials of row rr of `part` in XCD order, identical in both lanes of the pair
+    auto reduce_row = [&](uint32_t part, uint32_t tag64) -> float {
+      const uint32_t wd = part + 2 * ((j * ROWS + rr) * NXCD + 4 * hx);
+      u32x4 a = xld4(wsb, wd), b = xld4(wsb, wd + 4);
+      a = xrepoll64x2(wsb, ws, wd, tag64, a);
+      b = xrepoll64x2(wsb, ws, wd + 4, tag64, b);
+      const float s4 = (__uint_as_float(a.x) + __uint_as_float(a.z)) + (__uint_as_float(b.x) + __uint_as_float(b.z));
+      return s4 + dpp<0xB1>(s4);  // (XCDs 0..3) + (XCDs 4..7), commutative: same bits in both lanes
+    };
+    for (int layer = 0; layer < L; layer++) {
+      const uint32_t tag = tag_of(epoch, layer);
+      const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
+      BAR();  // A1: h rows in s_hrow
+      const float hrow = s_hrow[rr];
+      if (att) {
+        BAR();  // B1
+        attn_scores(s_kv, s_q, s_sc, nc, P.attn_scale, wave, lane);
+        BAR();  // B2
+        float M0, M1, L0, L1;
+        attn_softmax(s_sc, s_p, nc, wave, lane, M0, M1, L0, L1);
+        BAR();  // B3
+        attn_pv(s_kv, s_p, s_ao, nc, wave, lane, nsplit == 1 ? 1.0f / L0 : 1.f, nsplit == 1 ? 1.0f / L1 : 1.f);
+        BAR();  // B4
+        if (combine) BAR();  // B5
+      }
+      BAR();  // C1
+      // h1 = bf16(h + bf16(o)) (modeling_qwen3.py:297-298)
+      h1v = rbf(hrow + rbf(reduce_row(X_OPART, tag64)));
+      if (hx == 0) st1_plain(ws + lb + LX_H1 + ROWS * j + rr, tagged(tag, h1v));
+      BAR();  // D1
+      BAR();  // E1
+      // h' = bf16(h1 + bf16(down)) (modeling_qwen3.py:303-304)
+      const float hn = rbf(h1v + rbf(reduce_row(X_DPART, tag64)));
+      if (hx == 0) st1_plain(ws + lb + LX_H + ROWS * j + rr, tagged(tag, hn));
+    }
+    BAR();  // F1
+  } else {
+    // ==================================================================== store wave
+    if (lane == 0) s_cnt = 0u;
+    BAR();  // P00
+    BAR();  // P0
+    uint32_t target = 0;
+    for (int layer = 0; layer < L; layer++) {
+      const uint32_t tag = tag_of(epoch, layer);
+      const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
+      BAR();  // A1
+      target += NSW;
+      wait_count(&s_cnt, target);
+      if (lane < 16) st1_plain(ws + lb + LX_QKV + 16 * j + lane, tagged(tag, rbf(s_res[lane])));
+      if (att) {
+        BAR();  // B1
+        if (own_p) {
+          // K/V-cache append at slot p (bf16 [L][8][max_seq][128]): lane -> dims 2 lane, 2 lane + 1
+          const int row = p - c0;
+          const size_t slot = ((size_t)(layer * NKV + g) * P.max_seq_len + p) * HD;
+          const uint32_t k2 = *reinterpret_cast<const uint32_t*>(s_kv + kv_off(row, lane >> 2) + 4 * (lane & 3));
+          const uint32_t v2 =
+              *reinterpret_cast<const uint32_t*>(s_kv + KV_CAP * 256 + kv_off(row, lane >> 2) + 4 * (lane & 3));
+          st1_plain(reinterpret_cast<uint32_t*>(P.k_cache + slot) + lane, k2);
+          st1_plain(reinterpret_cast<uint32_t*>(P.v_cache + slot) + lane, v2);
+        }
+        attn_scores(s_kv, s_q, s_sc, nc, P.attn_scale, wave, lane);
+        BAR();  // B2
+        float M0, M1, L0, L1;
+        attn_softmax(s_sc, s_p, nc, wave, lane, M0, M1, L0, L1);
+        BAR();  // B3
+        attn_pv(s_kv, s_p, s_ao, nc, wave, lane, nsplit == 1 ? 1.0f / L0 : 1.f, nsplit == 1 ? 1.0f / L1 : 1.f);
+        BAR();  // B4
+        // lane -> outputs 4 lane .. 4 lane + 3 of head hh = lane / 32
+        const int hh = lane >> 5, dim = 4 * (lane & 31);
+        if (nsplit == 1) {
+          st4_plain(ws + lb + LX_ATT + hh * HD + dim,
+                    u32x4{tagged(tag, rbf(s_ao[hh][dim])), tagged(tag, rbf(s_ao[hh][dim + 1])),
+                          tagged(tag, rbf(s_ao[hh][dim + 2])), tagged(tag, rbf(s_ao[hh][dim + 3]))});
+        } else {
+          // chunk partial (m, l, unnormalised acc) as (fp32, tag) pairs; workgroup (g, 0) combines
+          uint32_t* pb = ws + lb + LX_PART + 2 * ((j * 2 + hh) * APART);
+          st4_plain(pb + 2 * (2 + dim), u32x4{__float_as_uint(s_ao[hh][dim]), tag64,
+                                              __float_as_uint(s_ao[hh][dim + 1]), tag64});
+          st4_plain(pb + 2 * (4 + dim), u32x4{__float_as_uint(s_ao[hh][dim + 2]), tag64,
+                                              __float_as_uint(s_ao[hh][dim + 3]), tag64});
+          if (dim == 0)
+            st4_plain(pb, u32x4{__float_as_uint(hh ? M1 : M0), tag64, __float_as_uint(hh ? L1 : L0), tag64});
+          if (combine) {
+            BAR();  // B5: combined output in s_sc
+            st4_plain(ws + lb + LX_ATT + hh * HD + dim,
+                      u32x4{tagged(tag, rbf(s_sc[hh][dim])), tagged(tag, rbf(s_sc[hh][dim + 1])),
+                            tagged(tag, rbf(s_sc[hh][dim + 2])), tagged(tag, rbf(s_sc[hh][dim + 3]))});
+          }
+        }
+      }
+      // o_proj partials of rows 32j .. 32j+31 over this XCD's two heads
+      BAR();  // C1
+      target += NSW;
+      wait_count(&s_cnt, target);
+      if (lane < ROWS)
+        st2_dev(ws + X_OPART + 2 * ((j * ROWS + lane) * NXCD + g), u32x2{__float_as_uint(s_res[lane]), tag64});
+      // HF Qwen3MLP (modeling_qwen3.py:81-83): m = bf16(bf16(silu(gate)) * up)
+      BAR();  // D1
+      target += NSW;
+      wait_count(&s_cnt, target);
+      if (lane < UNITS) {
+        const int sw = lane / 3, u = lane - 3 * sw;  // stream wave sw holds gate / up rows 3 sw + u
+        const float gt = rbf(s_res[6 * sw + u]), up = rbf(s_res[6 * sw + 3 + u]);
+        st1_plain(ws + lb + LX_M + UNITS * j + lane, tagged(tag, rbf(rbf(gt / (1.0f + expf(-gt))) * up)));
+      }
+      // down_proj partials of rows 32j .. 32j+31 over this XCD's 384 units
+      BAR();  // E1
+      target += NSW;
+      wait_count(&s_cnt, target);
+      if (lane < ROWS)
+        st2_dev(ws + X_DPART + 2 * ((j * ROWS + lane) * NXCD + g), u32x2{__float_as_uint(s_res[lane]), tag64});
+    }
+    BAR();  // F1
+  }
+
+  // ==================================================================== LM head (all waves)
+  if (lm) {
+    const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
+    // rows r0 + NSW * LM_PRE + wave + 8i: four rows per batch, two batches in flight
     auto load_rows = [&](int rb, u32x4 (&Wr)[4][2]) {
 #pragma unroll
       for (int u = 0; u < 4; u++) {
-        const int r = rb + 4 * u;
+        const int r = rb + 8 * u;
         if (r < r1) {
           const uint16_t* row = P.lm_head + (size_t)r * H;
           Wr[u][0] = ldw(row + 8 * lane);
@@ -683,32 +1066,28 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     auto score_rows = [&](int rb, const u32x4 (&Wr)[4][2]) {
 #pragma unroll
       for (int u = 0; u < 4; u++) {
-        const int r = rb + 4 * u;
-        if (r < r1) {
-          const float v = rbf(wave_sum(dot8(Wr[u][0], x0) + dot8(Wr[u][1], x1)));
-          if (want_logits && lane == 0) P.logits_out[r] = v;
-          if (v > bestv) {
-            bestv = v;
-            besti = r;
-          }
-        }
+        const int r = rb + 8 * u;
+        if (r < r1) lm_score(r, r0, Wr[u][0], Wr[u][1], x0, x1, s_lg, lane, bestv, besti);
       }
     };
     u32x4 WA[4][2], WB[4][2];
-    load_rows(r0 + wave, WA);
-    for (int rb = r0 + wave; rb < r1; rb += 32) {
-      load_rows(rb + 16, WB);
+    const int rs = r0 + NSW * LM_PRE + wave;
+    load_rows(rs, WA);
+    for (int rb = rs; rb < r1; rb += 64) {
+      load_rows(rb + 32, WB);
       score_rows(rb, WA);
-      load_rows(rb + 32, WA);
-      score_rows(rb + 16, WB);
+      load_rows(rb + 64, WA);
+      score_rows(rb + 32, WB);
     }
     if (lane == 0) {
       s_bestv[wave] = bestv;
       s_besti[wave] = besti;
     }
-    __syncthreads();
+  }
+  BAR();  // F2
+  if (lm) {
     if (tid == 0) {
-      for (int v = 1; v < 4; v++) {
+      for (int v = 1; v < 8; v++) {
         if (s_bestv[v] > bestv || (s_bestv[v] == bestv && s_besti[v] < besti)) {
           bestv = s_bestv[v];
           besti = s_besti[v];
@@ -717,21 +1096,28 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       wsb.st1(__float_as_uint(bestv), (WS_LMPART + 2 * w) * 4u);
       wsb.st1((uint32_t)besti, (WS_LMPART + 2 * w + 1) * 4u);
     }
+    if (P.mode & MODE_LOGITS)
+      for (int i = tid; i < r1 - r0; i += NT) P.logits_out[r0 + i] = s_lg[i];
   }
+
   // ---- completion ticket: the last workgroup reduces and resets the workspace
   wait_vmem();
-  __syncthreads();
+  BAR();
   if (tid == 0) {
     const uint32_t old =
         __hip_atomic_fetch_add(ws + WS_FINAL_TICKET, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_flag = (old == (uint32_t)(NWG - 1)) ? 1u : 0u;
   }
-  __syncthreads();
+  BAR();
   if (!s_flag) return;
   int tok = 0;
   if (lm) {
-    float v = __uint_as_float(wsb.ld1((WS_LMPART + 2 * tid) * 4u));
-    int i = (int)wsb.ld1((WS_LMPART + 2 * tid + 1) * 4u);
+    float v = -INFINITY;
+    int i = 0x7fffffff;
+    if (tid < NWG) {
+      v = __uint_as_float(wsb.ld1((WS_LMPART + 2 * tid) * 4u));
+      i = (int)wsb.ld1((WS_LMPART + 2 * tid + 1) * 4u);
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
       const float ov = __shfl_xor(v, off, 64);
@@ -745,10 +1131,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       s_bestv[wave] = v;
       s_besti[wave] = i;
     }
-    __syncthreads();
+    BAR();
     float bv = s_bestv[0];
     int bi = s_besti[0];
-    for (int q = 1; q < 4; q++) {
+    for (int q = 1; q < 8; q++) {
       if (s_bestv[q] > bv || (s_bestv[q] == bv && s_besti[q] < bi)) {
         bv = s_bestv[q];
         bi = s_besti[q];
@@ -830,7 +1216,7 @@ extern "C" int launch_ldg_decode_with_logits(int input_token_id, int* output_tok
       !sin_table || !k_cache || !v_cache || !hidden_buffer)
     return MQ_ERR_ARG;
   if (num_layers < 1 || num_layers > MAX_LAYERS || max_seq_len < 1 || position < 0 || position >= max_seq_len ||
-      cache_len != position + 1 || input_token_id < 0 || input_token_id >= VOCAB || bad_scale(attn_scale))
+      position >= MAX_CTX || cache_len != position + 1 || input_token_id < 0 || input_token_id >= VOCAB || bad_scale(attn_scale))
     return MQ_ERR_ARG;
   DecodeParams P{};
   P.layers = layer_weights;
@@ -874,7 +1260,8 @@ extern "C" int mq_decode_layer(const void* hidden_in, void* hidden_out, const LD
                                int position, int max_seq_len, float attn_scale, hipStream_t stream) {
   if (!hidden_in || !hidden_out || !layer_weights || !cos_table || !sin_table || !k_cache || !v_cache)
     return MQ_ERR_ARG;
-  if (max_seq_len < 1 || position < 0 || position >= max_seq_len || bad_scale(attn_scale)) return MQ_ERR_ARG;
+  if (max_seq_len < 1 || position < 0 || position >= max_seq_len || position >= MAX_CTX || bad_scale(attn_scale))
+    return MQ_ERR_ARG;
   DecodeParams P{};
   P.layers = layer_weights;
   P.cos_tab = static_cast<const uint16_t*>(cos_table);
