@@ -69,11 +69,10 @@ constexpr int UNITS = I / NWG;                // MLP units per workgroup: 12
 constexpr int XUNITS = I / NXCD;              // MLP units per XCD: 384
 constexpr int KV_CAP = 256;                   // positions per attention workgroup
 constexpr int MAX_CTX = WG_PER_XCD * KV_CAP;  // 8192
-constexpr int LM_PRE = 16;                    // LM-head rows each stream wave loads during the last layer
-// Vector-memory instructions a stream wave issues per layer (q/k/v 8 + input norm 1
-// + q/k norm 1, o_proj 4, gate/up 12 + post norm 1, down 8); the K/V copy of a layer
-// is followed by at least this many before it is needed.
-constexpr int S_LOADS_PER_LAYER = 35;
+constexpr int LM_PRE = 4;                     // LM-head rows each stream wave loads during the last layer
+// A layer's K/V copy is issued just before the previous layer's down_proj weights;
+// the next layer's q/k/v (8) and o_proj (4) loads follow it before attention.
+constexpr int S_LOADS_AFTER_KV = 12;
 
 // Workspace layout, in 32-bit words.
 constexpr uint32_t WS_EPOCH = 0;
@@ -311,10 +310,14 @@ __device__ __forceinline__ void wait_count(uint32_t* cnt, uint32_t target) {
 }
 
 // ---- attention of one chunk for the two query heads of a KV group (all 8 waves)
-// scores s_sc[h][r] = (q_h . k_r) * scale for rows r < nc, -inf for rows nc..255.
-// Rows at or past nc hold stale LDS contents; they are masked by selects only.
-__device__ __forceinline__ void attn_scores(const uint8_t* s_kv, const uint16_t* s_q, float (*s_sc)[KV_CAP], int nc,
-                                            float scale, int v, int lane) {
+// The K/V rows of the chunk sit in LDS (rows 0..nc-1; rows nc..255 are zero for the
+// whole launch: the LDS copy is cleared once and the copies only ever fill rows < nc).
+//
+// Scores s_sc[h][r] = (q_h . k_r) * scale for r < nc (-inf past nc), from MFMA tiles
+// of 16 rows: wave v takes row blocks v and v + 8. Each wave also leaves the maximum
+// of its scores per head in s_mx[v].
+__device__ __forceinline__ void attn_scores(const uint8_t* s_kv, const uint16_t* s_q, float (*s_sc)[KV_CAP],
+                                            float (*s_mx)[2], int nc, float scale, int v, int lane) {
   const int r16 = lane & 15, kg = lane >> 4;
   u32x4 qb[4];
 #pragma unroll
@@ -322,92 +325,91 @@ __device__ __forceinline__ void attn_scores(const uint8_t* s_kv, const uint16_t*
     const u32x4 t = *reinterpret_cast<const u32x4*>(s_q + (r16 & 1) * HD + 32 * s4 + 8 * kg);
     qb[s4] = r16 < 2 ? t : u32x4{0u, 0u, 0u, 0u};
   }
-  // wave v: row blocks v and v + 8 (16 rows each); a block's K operands are read before its MFMAs
+  const int nb = (nc + 15) >> 4;
+  float mx = -INFINITY;
 #pragma unroll 1
-  for (int bb = 0; bb < 2; bb++) {
-    const int row = 16 * (v + 8 * bb) + r16;
+  for (int b = v; b < nb; b += 8) {
+    const int row = 16 * b + r16;
     u32x4 ka[4];
 #pragma unroll
     for (int s4 = 0; s4 < 4; s4++) ka[s4] = *reinterpret_cast<const u32x4*>(s_kv + kv_off(row, 4 * s4 + kg));
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s4 = 0; s4 < 4; s4++) acc = mfma_16x16x32(ka[s4], qb[s4], acc);
-    if (r16 < 2) {
+    // lane (column r16 = head, rows 4kg + e)
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int r = 16 * (v + 8 * bb) + 4 * kg + e;
-        s_sc[r16][r] = r < nc ? acc[e] * scale : -INFINITY;
-      }
+    for (int e = 0; e < 4; e++) {
+      const int r = 16 * b + 4 * kg + e;
+      const float val = r < nc ? acc[e] * scale : -INFINITY;
+      if (r16 < 2) s_sc[r16][r] = val;
+      mx = fmaxf(mx, val);
     }
+  }
+  // per-head maximum over the lanes of column 0 (head 0) and column 1 (head 1)
+  const float m0 = fmaxf(fmaxf(readlane(mx, 0), readlane(mx, 16)), fmaxf(readlane(mx, 32), readlane(mx, 48)));
+  const float m1 = fmaxf(fmaxf(readlane(mx, 1), readlane(mx, 17)), fmaxf(readlane(mx, 33), readlane(mx, 49)));
+  if (lane == 0) {
+    s_mx[v][0] = m0;
+    s_mx[v][1] = m1;
   }
 }
 
-// Softmax statistics of both heads (every wave computes them); wave 0 also
-// stores the bf16 numerators exp(s - max) for the P.V product (0 past nc).
-__device__ __forceinline__ void attn_softmax(float (*s_sc)[KV_CAP], uint16_t* s_p, int nc, int v, int lane,
-                                             float& M0, float& M1, float& L0, float& L1) {
-  float a[4], b[4];
-  float m0 = -INFINITY, m1 = -INFINITY;
+// Softmax numerators of this wave's 32 rows (blocks v and v + 8) for both heads:
+// lane -> head lane / 32, row 16 (v + 8 ((lane >> 4) & 1)) + (lane & 15). Stores
+// bf16(exp(s - max)) in s_p (0 past nc; torch's CPU flash kernel feeds bf16 p to P.V)
+// and this wave's unrounded sums in s_l[v]; returns the per-head maxima.
+__device__ __forceinline__ void attn_softmax(const float (*s_sc)[KV_CAP], uint16_t* s_p, const float (*s_mx)[2],
+                                             float (*s_l)[2], int nc, int v, int lane, float& M0, float& M1) {
+  M0 = s_mx[0][0];
+  M1 = s_mx[0][1];
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int r = lane + 64 * k;
-    a[k] = r < nc ? s_sc[0][r] : -INFINITY;
-    b[k] = r < nc ? s_sc[1][r] : -INFINITY;
-    m0 = fmaxf(m0, a[k]);
-    m1 = fmaxf(m1, b[k]);
+  for (int k = 1; k < 8; k++) {
+    M0 = fmaxf(M0, s_mx[k][0]);
+    M1 = fmaxf(M1, s_mx[k][1]);
   }
-  M0 = wave_max(m0);
-  M1 = wave_max(m1);
-  float l0 = 0.f, l1 = 0.f;
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int r = lane + 64 * k;
-    const float e0 = r < nc ? expf(a[k] - M0) : 0.f;
-    const float e1 = r < nc ? expf(b[k] - M1) : 0.f;
-    l0 += e0;
-    l1 += e1;
-    if (v == 0) {
-      s_p[r] = (uint16_t)f2bf(e0);
-      s_p[KV_CAP + r] = (uint16_t)f2bf(e1);
-    }
+  const int h = lane >> 5, r = 16 * (v + 8 * ((lane >> 4) & 1)) + (lane & 15);
+  const float e = r < nc ? expf(s_sc[h][r] - (h ? M1 : M0)) : 0.f;
+  s_p[h * KV_CAP + r] = (uint16_t)f2bf(e);
+  const float t = row16_sum(e);
+  const float l0 = readlane(t, 0) + readlane(t, 16), l1 = readlane(t, 32) + readlane(t, 48);
+  if (lane == 0) {
+    s_l[v][0] = l0;
+    s_l[v][1] = l1;
   }
-  L0 = wave_sum(l0);
-  L1 = wave_sum(l1);
 }
 
-// acc[h][d] = sum_r bf16(p_h[r]) * v_r[d] for this wave's 16 dims d = 16v + (lane & 15),
-// scaled by inv0 / inv1 into s_ao. All 8 blocks of 32 rows are processed: past nc
-// both operands are zero (P by the softmax, V by select), so no branch is needed
-// and every LDS read can be issued ahead of the MFMAs.
-__device__ __forceinline__ void attn_pv(const uint8_t* s_kv, const uint16_t* s_p, float (*s_ao)[HD], int nc, int v,
-                                        int lane, float inv0, float inv1) {
+// acc[h][d] = sum_r bf16(p_h[r]) * v_r[d] for this wave's 16 dims d = 16v + (lane & 15)
+// over the 32-row blocks that hold rows < nc; the rows past nc are zero in both
+// operands. Writes acc / l (fin) or the raw acc (a split-K partial) to s_ao and
+// returns the per-head sums l.
+__device__ __forceinline__ void attn_pv(const uint8_t* s_kv, const uint16_t* s_p, const float (*s_l)[2],
+                                        float (*s_ao)[HD], int nc, int v, int lane, bool fin, float& L0, float& L1) {
   const int r16 = lane & 15, kg = lane >> 4;
   const int dim = 16 * v + r16, ch = dim >> 3, within = 2 * (dim & 7);
   const uint8_t* vbase = s_kv + KV_CAP * 256;
+  const int nb = (nc + 31) >> 5;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-  for (int t0 = 0; t0 < 8; t0 += 2) {
-    u32x4 pa[2], vb[2];
+  for (int t = 0; t < nb; t++) {
+    const int rr = 32 * t + 8 * kg;
+    const u32x4 pt = *reinterpret_cast<const u32x4*>(s_p + (r16 & 1) * KV_CAP + rr);
+    const u32x4 pa = r16 < 2 ? pt : u32x4{0u, 0u, 0u, 0u};
+    uint32_t h16[8];
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const int rr = 32 * (t0 + u) + 8 * kg;
-      const u32x4 pt = *reinterpret_cast<const u32x4*>(s_p + (r16 & 1) * KV_CAP + rr);
-      pa[u] = r16 < 2 ? pt : u32x4{0u, 0u, 0u, 0u};
-      uint32_t h16[8];
+    for (int e = 0; e < 8; e++) h16[e] = *reinterpret_cast<const uint16_t*>(vbase + kv_off(rr + e, ch) + within);
+    const u32x4 vb = {h16[0] | (h16[1] << 16), h16[2] | (h16[3] << 16), h16[4] | (h16[5] << 16),
+                      h16[6] | (h16[7] << 16)};
+    acc = mfma_16x16x32(pa, vb, acc);
+  }
+  L0 = 0.f;
+  L1 = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; e++) h16[e] = *reinterpret_cast<const uint16_t*>(vbase + kv_off(rr + e, ch) + within);
-      uint32_t vw[4];
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        vw[e] = (rr + 2 * e < nc ? h16[2 * e] : 0u) | ((rr + 2 * e + 1 < nc ? h16[2 * e + 1] : 0u) << 16);
-      vb[u] = u32x4{vw[0], vw[1], vw[2], vw[3]};
-    }
-#pragma unroll
-    for (int u = 0; u < 2; u++) acc = mfma_16x16x32(pa[u], vb[u], acc);
+  for (int k = 0; k < 8; k++) {
+    L0 += s_l[k][0];
+    L1 += s_l[k][1];
   }
   if (kg == 0) {
-    s_ao[0][dim] = acc[0] * inv0;
-    s_ao[1][dim] = acc[1] * inv1;
+    s_ao[0][dim] = fin ? acc[0] * (1.0f / L0) : acc[0];
+    s_ao[1][dim] = fin ? acc[1] * (1.0f / L1) : acc[1];
   }
 }
 
@@ -484,6 +486,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ __align__(16) uint16_t s_p[2 * KV_CAP];  // bf16 softmax numerators
   __shared__ float s_sc[2][KV_CAP];                    // attention scores, later the combined output
   __shared__ float s_ao[2][HD];                        // attention output (or unnormalised partial)
+  __shared__ float s_mx[8][2], s_l[8][2];              // per-wave score maxima and softmax sums
   __shared__ float s_hrow[ROWS];                       // residual rows 32j .. 32j+31 of h
   __shared__ float s_res[ROWS];                        // stream-wave dot products for the store wave
   __shared__ uint32_t s_cnt;                           // stream-wave results published so far
@@ -523,6 +526,9 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   const u32x4* x0v = reinterpret_cast<const u32x4*>(s_x0);
   const u32x4* x1v = reinterpret_cast<const u32x4*>(s_x1);
 
+  // rows past the chunk length must read as zeros in every layer
+  for (int i = tid; i < 2 * KV_CAP * HD * 2 / 16; i += NT) reinterpret_cast<u32x4*>(s_kv)[i] = u32x4{0u, 0u, 0u, 0u};
+
   if (wave < NSW) {
     // ==================================================================== stream waves
     const int s = wave, st = tid;  // st: stream thread 0..255
@@ -543,8 +549,6 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
 
     StreamRegs R;
     auto load_a = [&](int l) {
-      R.wln = ldw2(wp(l, W_IN) + 4 * st);
-      R.qkn = ldw1(wp(l, st < 64 ? W_QN : W_KN) + 2 * (st & 63));
       const int r = 16 * j + 4 * s;  // this wave's 4 rows of the group's [q0; q1; k; v]
       const uint16_t* pa = (l >= L && lmnext) ? lmb
                            : r < 256          ? wp(l, W_Q) + (size_t)(256 * g + r) * H
@@ -564,7 +568,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       for (int i = 0; i < 4; i++) R.o[i] = ldw(po + (lmr ? 8 * (lane + 64 * i) : (size_t)(2 * i) * QS));
     };
     auto load_gu = [&](int l) {
-      R.wpost = ldw2(wp(l, W_POST) + 4 * st);
+      R.wln = ldw2(wp(l + 1, W_IN) + 4 * st);  // the next layer's input norm and q/k norms
+      R.qkn = ldw1(wp(l + 1, st < 64 ? W_QN : W_KN) + 2 * (st & 63));
       const bool lmr = l >= L && lmnext;
       const uint16_t* pg = lmr ? lmb + 6 * H : wp(l, W_G) + (size_t)(XUNITS * g + UNITS * j + 3 * s) * H;
       const uint16_t* pu = lmr ? lmb + 9 * H : wp(l, W_U) + (size_t)(XUNITS * g + UNITS * j + 3 * s) * H;
@@ -580,6 +585,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       }
     };
     auto load_d = [&](int l) {
+      R.wpost = ldw2(wp(l + 1, W_POST) + 4 * st);  // the next layer's post-attention norm
       const bool lmr = l >= L && lmnext;
       // LM rows 12 .. 15 of this wave as chunks lane, lane + 64 of four consecutive rows
       const uint16_t* pd = lmr ? lmb + 12 * H : wp(l, W_D) + (size_t)(ROWS * j + 8 * s) * I + XUNITS * g + 8 * dch;
@@ -605,9 +611,6 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     }
     if (att) kv_dma(P, 0, g, c0, nc, p, lds_kv, s, lane);
     load_a(0);
-    load_o(0);
-    load_gu(0);
-    load_d(0);
     BAR();  // P0
 
     for (int layer = 0; layer < L; layer++) {
@@ -629,22 +632,20 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           signal_store(&s_cnt);
         }
         AFTER(r[0] + r[1] + r[2] + r[3]);
-        load_a(nl);
+        load_o(layer);
       }
       if (att) {
-        // this wave's K/V copy of the layer has landed (it was issued before at least
-        // the last S_LOADS_PER_LAYER loads of this wave)
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S_LOADS_PER_LAYER) : "memory");
+        // this wave's K/V copy of the layer has landed (S_LOADS_AFTER_KV loads followed it)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S_LOADS_AFTER_KV) : "memory");
         BAR();  // B1: q, the new k/v row and the K/V rows are in LDS
-        attn_scores(s_kv, s_q, s_sc, nc, P.attn_scale, wave, lane);
+        attn_scores(s_kv, s_q, s_sc, s_mx, nc, P.attn_scale, wave, lane);
         BAR();  // B2
         float M0, M1, L0, L1;
-        attn_softmax(s_sc, s_p, nc, wave, lane, M0, M1, L0, L1);
+        attn_softmax(s_sc, s_p, s_mx, s_l, nc, wave, lane, M0, M1);
         BAR();  // B3
-        attn_pv(s_kv, s_p, s_ao, nc, wave, lane, nsplit == 1 ? 1.0f / L0 : 1.f, nsplit == 1 ? 1.0f / L1 : 1.f);
+        attn_pv(s_kv, s_p, s_l, s_ao, nc, wave, lane, nsplit == 1, L0, L1);
         BAR();  // B4: K/V rows consumed
         if (combine) BAR();  // B5
-        if (nl < L) kv_dma(P, nl, g, c0, nc, p, lds_kv, s, lane);
       }
       // ---------------- o_proj partials: rows 32j + 8s + 2i + rg over the group's 256 columns
       BAR();  // C1: attention output of the group in s_x1
@@ -662,7 +663,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           signal_store(&s_cnt);
         }
         AFTER(r[0] + r[1] + r[2] + r[3]);
-        load_o(nl);
+        load_gu(layer);
       }
       // ---------------- gate/up rows of units 384g + 12j + 3s .. +2
       BAR();  // D1: normed h1 in s_x0
@@ -681,7 +682,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           signal_store(&s_cnt);
         }
         AFTER(r[0] + r[1] + r[2] + r[3] + r[4] + r[5]);
-        load_gu(nl);
+        load_d(layer);
+        // the next layer's K/V rows: the LDS copy is free since B4, and its completion is
+        // first needed behind the next layer's q/k/v weights
+        if (att && nl < L) kv_dma(P, nl, g, c0, nc, p, lds_kv, s, lane);
       }
       // ---------------- down_proj partials: rows 32j + 8s + i over the XCD's 384 units
       BAR();  // E1: m of the XCD in s_x1
@@ -696,7 +700,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           signal_store(&s_cnt);
         }
         AFTER(r[0] + r[1] + r[2] + r[3] + r[4] + r[5] + r[6] + r[7]);
-        load_d(nl);
+        load_a(nl);
       }
     }
     BAR();  // F1: final normed h in s_x0
@@ -705,14 +709,6 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       const int rb = r0 + LM_PRE * s;
 #pragma unroll
       for (int k = 0; k < 4; k++) lm_score(rb + k, r0, R.a[2 * k], R.a[2 * k + 1], x0, x1, s_lg, lane, bestv, besti);
-      lm_score(rb + 4, r0, R.o[0], R.o[1], x0, x1, s_lg, lane, bestv, besti);
-      lm_score(rb + 5, r0, R.o[2], R.o[3], x0, x1, s_lg, lane, bestv, besti);
-#pragma unroll
-      for (int k = 0; k < 6; k++)
-        lm_score(rb + 6 + k, r0, R.gu[2 * k], R.gu[2 * k + 1], x0, x1, s_lg, lane, bestv, besti);
-#pragma unroll
-      for (int k = 0; k < 4; k++)
-        lm_score(rb + 12 + k, r0, R.d[2 * k], R.d[2 * k + 1], x0, x1, s_lg, lane, bestv, besti);
     }
   } else if (wave < NSW + NPW) {
     // ==================================================================== poll waves
@@ -826,12 +822,12 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           }
         }
         BAR();  // B1
-        attn_scores(s_kv, s_q, s_sc, nc, P.attn_scale, wave, lane);
+        attn_scores(s_kv, s_q, s_sc, s_mx, nc, P.attn_scale, wave, lane);
         BAR();  // B2
         float M0, M1, L0, L1;
-        attn_softmax(s_sc, s_p, nc, wave, lane, M0, M1, L0, L1);
+        attn_softmax(s_sc, s_p, s_mx, s_l, nc, wave, lane, M0, M1);
         BAR();  // B3
-        attn_pv(s_kv, s_p, s_ao, nc, wave, lane, nsplit == 1 ? 1.0f / L0 : 1.f, nsplit == 1 ? 1.0f / L1 : 1.f);
+        attn_pv(s_kv, s_p, s_l, s_ao, nc, wave, lane, nsplit == 1, L0, L1);
         BAR();  // B4
         MQ_TRACE(5 + layer * 16);
         if (combine) {
@@ -948,12 +944,12 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       const float hrow = s_hrow[rr];
       if (att) {
         BAR();  // B1
-        attn_scores(s_kv, s_q, s_sc, nc, P.attn_scale, wave, lane);
+        attn_scores(s_kv, s_q, s_sc, s_mx, nc, P.attn_scale, wave, lane);
         BAR();  // B2
         float M0, M1, L0, L1;
-        attn_softmax(s_sc, s_p, nc, wave, lane, M0, M1, L0, L1);
+        attn_softmax(s_sc, s_p, s_mx, s_l, nc, wave, lane, M0, M1);
         BAR();  // B3
-        attn_pv(s_kv, s_p, s_ao, nc, wave, lane, nsplit == 1 ? 1.0f / L0 : 1.f, nsplit == 1 ? 1.0f / L1 : 1.f);
+        attn_pv(s_kv, s_p, s_l, s_ao, nc, wave, lane, nsplit == 1, L0, L1);
         BAR();  // B4
         if (combine) BAR();  // B5
       }
@@ -993,12 +989,12 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           st1_plain(reinterpret_cast<uint32_t*>(P.k_cache + slot) + lane, k2);
           st1_plain(reinterpret_cast<uint32_t*>(P.v_cache + slot) + lane, v2);
         }
-        attn_scores(s_kv, s_q, s_sc, nc, P.attn_scale, wave, lane);
+        attn_scores(s_kv, s_q, s_sc, s_mx, nc, P.attn_scale, wave, lane);
         BAR();  // B2
         float M0, M1, L0, L1;
-        attn_softmax(s_sc, s_p, nc, wave, lane, M0, M1, L0, L1);
+        attn_softmax(s_sc, s_p, s_mx, s_l, nc, wave, lane, M0, M1);
         BAR();  // B3
-        attn_pv(s_kv, s_p, s_ao, nc, wave, lane, nsplit == 1 ? 1.0f / L0 : 1.f, nsplit == 1 ? 1.0f / L1 : 1.f);
+        attn_pv(s_kv, s_p, s_l, s_ao, nc, wave, lane, nsplit == 1, L0, L1);
         BAR();  // B4
         // lane -> outputs 4 lane .. 4 lane + 3 of head hh = lane / 32
         const int hh = lane >> 5, dim = 4 * (lane & 31);
