@@ -97,6 +97,7 @@ constexpr size_t WS_BYTES = ((WS_WORDS * 4 + 4 + 65535) / 65536) * 65536;
 
 constexpr uint32_t POLL_LIMIT = 1u << 21;  // ~1 s of polling before the watchdog fires
 constexpr uint32_t ERR_POLL = 1u;
+constexpr uint32_t ERR_XCD = 2u;  // a workgroup did not run on XCD blockIdx % 8
 
 constexpr int NT_LD = 2;  // non-temporal cache policy: bypasses the CU's L1, served by the XCD's L2
 
@@ -502,6 +503,13 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   uint32_t* ws = P.ws;
   const Buf wsb(ws);
   const uint32_t epoch = wsb.ld1(WS_EPOCH * 4u);
+  // The XCD-local exchange (plain stores, L2-coherent loads) assumes that the
+  // dispatcher placed workgroup w on XCD w % 8; check it on the hardware.
+  if (tid == 0) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    if ((xcc & 15u) != (uint32_t)g) raise_error(ws, ERR_XCD);
+  }
   const uint32_t lb = WS_LOCAL + g * LOCAL_WORDS;  // this XCD's exchange region
   const int L = P.num_layers;
   const bool lm = !(P.mode & MODE_NO_LMHEAD);
@@ -1185,9 +1193,14 @@ static int launch(DecodeParams& P, hipStream_t stream) {
   if (st != MQ_OK) return st;
   P.ws = g_dev[dev].ws;
   if (!P.out_token) P.out_token = reinterpret_cast<int*>(g_dev[dev].ws + WS_WORDS);
+  // All NWG workgroups must be resident at once. Each one needs a whole CU
+  // (its LDS use exceeds half a CU's), ensure_device() checked that the GPU has
+  // NWG such slots, and every inter-workgroup wait in the kernel ends in an
+  // error after a bounded spin, so an ordinary launch is used: a cooperative
+  // launch adds about 18 us of queue synchronisation per token on this stack.
   void* args[] = {&P};
-  const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mq_decode_kernel), dim3(NWG),
-                                                  dim3(NT), args, 0, stream);
+  const hipError_t e =
+      hipLaunchKernel(reinterpret_cast<const void*>(mq_decode_kernel), dim3(NWG), dim3(NT), args, 0, stream);
   return e == hipSuccess ? MQ_OK : MQ_ERR_HIP;
 }
 
