@@ -1,32 +1,38 @@
-// Persistent cooperative decode kernel for Qwen3-0.6B on MI355X (gfx950).
+// Persistent decode kernel for Qwen3-0.6B on MI355X (gfx950).
 //
 // One launch = one greedy decode step of the whole model (embedding, 28
 // decoder layers, final norm, tied LM head, argmax), the role of the
 // reference's ldg_decode_kernel + ldg_lm_head_phase1/2
 // (csrc/megakernel/fused_decode_ldg.cu:617-887).
 //
-// Chip layout: 256 workgroups (one per CU; a cooperative launch puts workgroup
-// w on XCD g = w % 8 as its j = w / 8 -th member) of 512 threads. Each
-// workgroup runs two kinds of waves:
-//   * 4 stream waves hold the workgroup's slice of the NEXT layer's weights in
-//     registers: right after a stage consumes its weight registers they are
-//     reloaded with the same stage of the following layer (the LM-head rows
-//     after the last layer), so every weight byte is requested one full layer
-//     before it is needed and HBM latency is off the critical path. Stream
+// Chip layout: 256 workgroups of 512 threads, one per CU; workgroup w runs on
+// XCD g = w % 8 (checked against the hardware XCC id) as that XCD's member
+// j = w / 8. XCD g owns KV group g: the 512 q/k/v rows of query heads 2g, 2g+1
+// and KV head g, the attention of those heads, the o_proj columns of those
+// heads (a K-split of o_proj across XCDs) and MLP units 384g .. 384g+383 (a
+// K-split of down_proj). Every workgroup runs four roles, one per wave kind:
+//   * stream waves 0-3 hold the workgroup's weight slice of the next stage in
+//     registers: as soon as a stage's dot products are done the registers are
+//     refilled with the following stage (the first LM-head rows after the last
+//     layer), so each weight byte is requested one stage before it is used.
+//     They also copy the next layer's K/V rows into LDS (LDS DMA). Stream
 //     waves only ever issue loads, so the compiler's in-order vmcnt bookkeeping
 //     stays exact across the layer loop.
-//   * 4 exchange waves poll the inter-workgroup exchanges, normalise, apply
-//     residuals and publish results. They never have a weight load queued
-//     ahead of a poll (vector-memory loads retire in order within a wave).
-// Per layer and workgroup w:
-//   q/k/v : 16 rows of KV group g (XCD g owns the group's 512 q/k/v rows)
-//   attn  : workgroup (g, j < nsplit) attends over a chunk of <= 256 positions
-//           for the group's two query heads; K/V rows are copied to LDS by the
-//           stream waves (LDS DMA) one layer ahead; QK^T and PV run on MFMA
-//   o_proj: residual rows 4w..4w+3 over all 2048 attention outputs
-//   MLP   : units 12w..12w+11 (gate and up rows), then down_proj rows 4w..4w+3
-// Every output row is complete inside one workgroup, so each exchange is a
-// single all-gather: a consumer reads the whole (<= 12 KB) vector directly.
+//   * poll waves 4-5 gather the XCD-local exchanges (h, q/k/v, attention
+//     output, h1, m), normalise, apply QK-norm and RoPE, and combine attention
+//     chunks.
+//   * reduce wave 6 sums the eight XCDs' o_proj and down_proj partials of the
+//     workgroup's 32 residual rows and applies the residual adds.
+//   * store wave 7 publishes the stream waves' dot products (handed over
+//     through LDS) and the K/V append.
+// Per layer and workgroup (g, j):
+//   q/k/v : rows 16j .. 16j+15 of the group's [q0; q1; k; v]
+//   attn  : workgroups j < nsplit attend over chunk j (<= 256 positions) for the
+//           group's two query heads; QK^T and PV run on MFMA from LDS
+//   o_proj: partial sums of rows 32j .. 32j+31 over the group's 256 columns
+//   MLP   : gate and up rows of units 384g + 12j .. +11, then down_proj
+//           partial sums of rows 32j .. 32j+31 over the XCD's 384 units
+// so a layer has five XCD-local all-gathers and two cross-XCD reductions.
 //
 // Exchanges use "tagged words": a bf16 value in the low half of a 32-bit word
 // and a 16-bit tag (launch epoch x 32 + layer) in the high half, or an fp32
