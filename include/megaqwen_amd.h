@@ -87,6 +87,32 @@ int mq_decode_layer(const void* hidden_in, void* hidden_out, const LDGLayerWeigh
                     const void* cos_table, const void* sin_table, void* k_cache, void* v_cache, int position,
                     int max_seq_len, float attn_scale, hipStream_t stream);
 
+/* Prefill of a whole prompt, then the greedy next token.
+ * Replaces `launch_prefill_float` (csrc/megakernel/fused_prefill.cu:601-636) with the
+ * same arguments minus the cuBLAS handle (the GEMMs are hand-written MFMA kernels).
+ *   input_token_ids: device int32 [seq_len]; 1 <= seq_len <= max_seq_len.
+ *   layer_weights  : HOST array of num_layers structs (as in the reference,
+ *                    csrc/megakernel/megakernel_decode.py:516).
+ *   k_cache/v_cache: bf16 [num_layers, 8, max_seq_len, 128]; slots 0..seq_len-1 are written.
+ *   Scratch (bf16, device, caller-owned, as the reference sizes them):
+ *     hidden_bf16 [seq_len, 1024], normalized [seq_len, 1024], q_proj [seq_len, 2048],
+ *     k_proj / v_proj [seq_len, 1024], attn_out [seq_len, 2048], mlp_norm [seq_len, 1024],
+ *     mlp_intermediate [seq_len, 3072], final_hidden [1024] (final-norm output of the
+ *     last row), block_max_vals f32 [1184], block_max_idxs i32 [1184].
+ *     residual, o_proj_out, gate_out, up_out and down_out are accepted and unused
+ *     (the epilogues fuse those steps); they may be NULL.
+ *   hidden_bf16_out [1024]: the last row's final hidden state (before the final norm).
+ *   On return (stream-ordered): *output_token_id = argmax of the last row's bf16
+ *   logits (lowest index on ties), or -2 if an input id was outside [0, 151936). */
+int launch_prefill_float(const int* input_token_ids, int* output_token_id, int seq_len, const void* embed_weight,
+                         const PrefillLayerWeights* layer_weights, const void* final_norm_weight,
+                         const void* lm_head_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                         void* v_cache, void* hidden_bf16, void* residual, void* normalized, void* q_proj,
+                         void* k_proj, void* v_proj, void* attn_out, void* o_proj_out, void* mlp_norm,
+                         void* gate_out, void* up_out, void* mlp_intermediate, void* down_out, void* final_hidden,
+                         void* block_max_vals, void* block_max_idxs, void* hidden_bf16_out, int num_layers,
+                         int max_seq_len, float attn_scale, hipStream_t stream);
+
 /* Zero this device's workspace (exchange buffers and counters). Needed only
  * after a launch reported a watchdog error. Synchronous. */
 int mq_reset_workspace(int device);

@@ -50,6 +50,9 @@ SIGNATURES = {
     "launch_ldg_decode": _DECODE_ARGS,
     "launch_ldg_decode_with_logits": _DECODE_ARGS[:2] + [_vp] + _DECODE_ARGS[2:],
     "mq_decode_layer": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _f, _vp],
+    # ids, out, seq_len, embed, layers (host array), final norm, lm head, cos, sin, k, v, 17 scratch,
+    # num_layers, max_seq_len, scale, stream
+    "launch_prefill_float": [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_vp] * 17 + [_i, _i, _f, _vp],
     "mq_reset_workspace": [_i],
     "mq_strerror": [_i],
 }

@@ -19,6 +19,10 @@ constexpr int VOCAB = 151936;
 constexpr int MAX_LAYERS = 32;
 constexpr float EPS = 1e-6f;
 
+// Word of the per-device library workspace where the prefill kernels flag an
+// invalid input (the decode kernel's words sit below it, its exchange buffers above).
+constexpr uint32_t WS_PREFILL_ERR = 96;
+
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x3 __attribute__((ext_vector_type(3)));

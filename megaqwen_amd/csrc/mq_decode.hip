@@ -84,6 +84,7 @@ constexpr int S_LOADS_AFTER_KV = 12;
 constexpr uint32_t WS_EPOCH = 0;
 constexpr uint32_t WS_ERR = 32;
 constexpr uint32_t WS_FINAL_TICKET = 64;
+// word WS_PREFILL_ERR (96) belongs to the prefill kernels
 // per-XCD regions of tagged bf16 words, written and read only by that XCD's workgroups
 constexpr uint32_t WS_LOCAL = 1024;
 constexpr uint32_t LOCAL_WORDS = 32768;
@@ -1208,6 +1209,17 @@ static int launch(DecodeParams& P, hipStream_t stream) {
   const hipError_t e =
       hipLaunchKernel(reinterpret_cast<const void*>(mq_decode_kernel), dim3(NWG), dim3(NT), args, 0, stream);
   return e == hipSuccess ? MQ_OK : MQ_ERR_HIP;
+}
+
+// The calling thread's current device's workspace, allocated on first use
+// (shared with the prefill kernels, which use word WS_PREFILL_ERR).
+int current_workspace(uint32_t** ws) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return MQ_ERR_HIP;
+  const int st = ensure_device(dev);
+  if (st != MQ_OK) return st;
+  *ws = g_dev[dev].ws;
+  return MQ_OK;
 }
 
 static bool bad_scale(float s) { return !(s > 0.f) || !isfinite(s); }

@@ -1,0 +1,572 @@
+// Prefill of S prompt tokens for Qwen3-0.6B on MI355X (gfx950).
+//
+// Replaces launch_prefill_float (csrc/megakernel/fused_prefill.cu:601-867): the
+// prompt's hidden states go through every layer as [S, *] bf16 matrices, K/V
+// slots 0..S-1 of every layer are written, and the greedy next token is taken
+// from the last row. Per layer:
+//   rmsnorm_rows -> gemm_nt (q, k, v in one launch) -> qk_rope_kv (QK-norm,
+//   RoPE, K/V append) -> attn_prefill (causal, MFMA) -> gemm_nt (o_proj + residual)
+//   -> rmsnorm_rows -> gemm_nt (gate and up, SiLU(gate) * up epilogue)
+//   -> gemm_nt (down_proj + residual)
+// then lm_partial (final norm of the last row, tied LM head, per-block argmax) and
+// argmax_final. The GEMMs run on v_mfma_f32_16x16x32_bf16 with fp32 accumulation.
+//
+// The intermediates live in the caller's scratch buffers (the reference's own
+// argument list), so a launch allocates nothing.
+//
+// Numerics are HF Qwen3's bf16 rounding points, as in the decode kernel. The
+// attention reproduces torch's CPU flash kernel (the sdpa path HF runs on the
+// CPU): scores in fp32, keys in blocks of 512 with a running maximum, exp in
+// fp32 summed unrounded, probabilities rounded to bf16 before P.V, output
+// bf16(acc * (1 / sum)).
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "megaqwen_amd.h"
+#include "mq_common.h"
+
+namespace mq {
+
+int current_workspace(uint32_t** ws);  // mq_decode.hip: this device's library workspace
+
+namespace pf {
+
+// ------------------------------------------------------------------ GEMM
+// C[m, n] = sum_k A[m, k] * W[n, k] (both operands k-contiguous, HF nn.Linear
+// layout), one 64 x 64 output tile per workgroup, k in steps of 64 staged
+// through LDS (double-buffered). Wave w computes rows 16w .. 16w+15 of the tile
+// against all 64 columns: four 16x16 MFMA blocks sharing one A fragment.
+constexpr int TM = 64, TN = 64, TK = 64, GT = 256;
+
+enum : int { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2 };
+
+struct GemmSeg {
+  const uint16_t* w;   // weight rows [n, k]; EPI_SILU: gate_proj rows
+  const uint16_t* w2;  // EPI_SILU: up_proj rows
+  uint16_t* out;       // [m, ldo] bf16
+  int ntiles;          // column tiles of this segment (EPI_SILU: 32 units each)
+  int ldo;
+};
+struct GemmArgs {
+  const uint16_t* a;  // [m, lda] bf16
+  int lda, m, k, nseg;
+  GemmSeg seg[3];
+};
+
+// LDS slot (in 16-byte chunks) of chunk kc (0..7) of tile row r. The chunks of a
+// row are XOR-swizzled with the row so that the 8 rows a quarter-wave reads in
+// one fragment load fall in distinct banks.
+__device__ __forceinline__ int tslot(int r, int kc) { return r * 8 + (kc ^ (r & 7)); }
+
+template <int EPI>
+__global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
+  __shared__ u32x4 sa[2][TM * 8];
+  __shared__ u32x4 sb[2][TN * 8];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  int nt = blockIdx.x, si = 0;
+  while (si + 1 < G.nseg && nt >= G.seg[si].ntiles) nt -= G.seg[si++].ntiles;
+  const GemmSeg S = G.seg[si];
+  const int m0 = blockIdx.y * TM;
+
+  // this thread's two A chunks and two B chunks of every k tile
+  const uint16_t* ga[2];
+  const uint16_t* gb[2];
+  bool va[2];
+  int slot[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int c = tid + GT * i, r = c >> 3, kc = c & 7;
+    slot[i] = tslot(r, kc);
+    va[i] = m0 + r < G.m;
+    ga[i] = G.a + (size_t)(va[i] ? m0 + r : 0) * G.lda + 8 * kc;
+    if (EPI == EPI_SILU)
+      gb[i] = (r < 32 ? S.w + (size_t)(32 * nt + r) * G.k : S.w2 + (size_t)(32 * nt + r - 32) * G.k) + 8 * kc;
+    else
+      gb[i] = S.w + (size_t)(TN * nt + r) * G.k + 8 * kc;
+  }
+  u32x4 ra[2], rb[2];
+  auto gload = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const u32x4 t = ldw(ga[i] + kt * TK);
+      ra[i] = va[i] ? t : u32x4{0u, 0u, 0u, 0u};
+      rb[i] = ldw(gb[i] + kt * TK);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      sa[buf][slot[i]] = ra[i];
+      sb[buf][slot[i]] = rb[i];
+    }
+  };
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int KT = G.k / TK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; kt++) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) gload(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      const int kc = 4 * ks + (lane >> 4), r = lane & 15;
+      const u32x4 af = sa[buf][tslot(16 * wv + r, kc)];
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[j] = mfma_16x16x32(af, sb[buf][tslot(16 * j + r, kc)], acc[j]);
+    }
+    if (kt + 1 < KT) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // lane holds rows 4 * (lane / 16) + e of column lane % 16 of each block
+  const int col = lane & 15, rq = 4 * (lane >> 4);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int row = m0 + 16 * wv + rq + e;
+    if (row >= G.m) continue;
+    uint16_t* orow = S.out + (size_t)row * S.ldo;
+    if (EPI == EPI_SILU) {
+      // HF Qwen3MLP (modeling_qwen3.py:81-83): down(bf16(silu(bf16 gate)) * bf16 up)
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const float g = rbf(acc[j][e]), u = rbf(acc[j + 2][e]);
+        const float sg = rbf(g / (1.0f + expf(-g)));
+        orow[32 * nt + 16 * j + col] = (uint16_t)f2bf(sg * u);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int c = TN * nt + 16 * j + col;
+        float v = rbf(acc[j][e]);
+        if (EPI == EPI_RESID) v = bf2f(orow[c]) + v;  // residual add, rounded once more
+        orow[c] = (uint16_t)f2bf(v);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ row-wise kernels
+// Embedding rows of the prompt. An id outside the vocabulary sets the error word
+// (reported as a negative token) and reads row 0.
+__global__ void __launch_bounds__(128) embed_rows(const int* ids, const uint16_t* emb, uint16_t* h, uint32_t* err) {
+  const int s = blockIdx.x;
+  int id = ids[s];
+  if (id < 0 || id >= VOCAB) {
+    if (threadIdx.x == 0) __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    id = 0;
+  }
+  reinterpret_cast<u32x4*>(h + (size_t)s * H)[threadIdx.x] = ldw(emb + (size_t)id * H + 8 * threadIdx.x);
+}
+
+// HF Qwen3RMSNorm (modeling_qwen3.py:59-64) of each row: y = bf16(w * bf16(x * rstd)),
+// rstd = 1 / sqrt(mean(x^2) + eps) in fp32. One wave per row.
+__global__ void __launch_bounds__(256) rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* y, int m) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= m) return;
+  const uint16_t* xr = x + (size_t)row * H;
+  const u32x4 c[2] = {ldw(xr + 8 * lane), ldw(xr + 512 + 8 * lane)};
+  const u32x4 wc[2] = {ldw(w + 8 * lane), ldw(w + 512 + 8 * lane)};
+  float f[2][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    unpack8(c[h], f[h]);
+#pragma unroll
+    for (int i = 0; i < 8; i++) ss = fmaf(f[h][i], f[h][i], ss);
+  }
+  ss = wave_sum(ss);
+  const float rstd = 1.0f / sqrtf(ss * (1.0f / H) + EPS);
+  uint16_t* yr = y + (size_t)row * H;
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    float wf[8];
+    unpack8(wc[h], wf);
+    u32x4 o;
+    o.x = pack_bf2(rbf(wf[0] * rbf(f[h][0] * rstd)), rbf(wf[1] * rbf(f[h][1] * rstd)));
+    o.y = pack_bf2(rbf(wf[2] * rbf(f[h][2] * rstd)), rbf(wf[3] * rbf(f[h][3] * rstd)));
+    o.z = pack_bf2(rbf(wf[4] * rbf(f[h][4] * rstd)), rbf(wf[5] * rbf(f[h][5] * rstd)));
+    o.w = pack_bf2(rbf(wf[6] * rbf(f[h][6] * rstd)), rbf(wf[7] * rbf(f[h][7] * rstd)));
+    reinterpret_cast<u32x4*>(yr + 512 * h)[lane] = o;
+  }
+}
+
+// Per token (one workgroup): QK-norm (per head over 128, weights q_norm/k_norm) and
+// RoPE (modeling_qwen3.py:247-257, rotate_half form, three bf16 ops) of the 16 q and
+// 8 k heads; q is rewritten in place, k goes to the K cache and v is copied to the V
+// cache at slot s (the reference's ldg_qk_norm_rope_cache, fused_decode_ldg.cu:166-276,
+// for a whole prompt). Lane l handles dims l and l + 64, the two halves RoPE pairs.
+__global__ void __launch_bounds__(256) qk_rope_kv(uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                                  const uint16_t* qn, const uint16_t* kn, const uint16_t* cos_t,
+                                                  const uint16_t* sin_t, uint16_t* kc, uint16_t* vc, int max_seq) {
+  const int s = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const float c1 = bf2f(cos_t[(size_t)s * HD + lane]), c2 = bf2f(cos_t[(size_t)s * HD + 64 + lane]);
+  const float s1 = bf2f(sin_t[(size_t)s * HD + lane]), s2 = bf2f(sin_t[(size_t)s * HD + 64 + lane]);
+  for (int hh = wv; hh < NQ + 2 * NKV; hh += 4) {
+    if (hh < NQ + NKV) {
+      const bool isq = hh < NQ;
+      const int h = isq ? hh : hh - NQ;
+      const uint16_t* src = isq ? q + (size_t)s * QS + HD * h : k + (size_t)s * KVS + HD * h;
+      const float x1 = bf2f(src[lane]), x2 = bf2f(src[64 + lane]);
+      const float ss = wave_sum(x1 * x1 + x2 * x2);
+      const float rstd = 1.0f / sqrtf(ss * (1.0f / HD) + EPS);
+      const uint16_t* nw = isq ? qn : kn;
+      const float n1 = rbf(bf2f(nw[lane]) * rbf(x1 * rstd)), n2 = rbf(bf2f(nw[64 + lane]) * rbf(x2 * rstd));
+      const float o1 = rbf(rbf(n1 * c1) - rbf(n2 * s1));
+      const float o2 = rbf(rbf(n2 * c2) + rbf(n1 * s2));
+      uint16_t* dst = isq ? q + (size_t)s * QS + HD * h : kc + ((size_t)h * max_seq + s) * HD;
+      dst[lane] = (uint16_t)f2bf(o1);
+      dst[64 + lane] = (uint16_t)f2bf(o2);
+    } else {
+      const int h = hh - NQ - NKV;
+      const uint16_t* src = v + (size_t)s * KVS + HD * h;
+      uint16_t* dst = vc + ((size_t)h * max_seq + s) * HD;
+      dst[lane] = src[lane];
+      dst[64 + lane] = src[64 + lane];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ causal attention
+// Workgroup (q block, head h): query rows r0 .. r0+31 of head h against keys
+// 0 .. min(S, r0 + 32) - 1 of KV head h / 2, in blocks of 512 keys. Per block:
+// scores (MFMA, K fragments straight from the cache) -> LDS; per-row max, exp and
+// sum with the running maximum -> bf16 probabilities in LDS; P.V on MFMA with the
+// accumulator rescaled by exp(m_old - m_new).
+constexpr int AQ = 32;
+constexpr int AKB = 512;
+
+__global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                                                    uint16_t* out, int S, int max_seq, float scale) {
+  __shared__ float s_sc[AQ][AKB];
+  __shared__ __align__(16) uint16_t s_p[AQ][AKB];
+  __shared__ float s_m[AQ], s_l[AQ], s_a[AQ];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int r0 = blockIdx.x * AQ, h = blockIdx.y, g = h >> 1;
+  const uint16_t* K = kc + (size_t)g * max_seq * HD;
+  const uint16_t* V = vc + (size_t)g * max_seq * HD;
+  const int nkey = min(S, r0 + AQ);
+  const int r16 = lane & 15, kg = lane >> 4;
+
+  u32x4 qf[2][4];
+#pragma unroll
+  for (int rb = 0; rb < 2; rb++) {
+    const int row = r0 + 16 * rb + r16;
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+      qf[rb][ks] = row < S ? ldw(q + (size_t)row * QS + HD * h + 32 * ks + 8 * kg) : u32x4{0u, 0u, 0u, 0u};
+  }
+  if (tid < AQ) {
+    s_m[tid] = -INFINITY;
+    s_l[tid] = 0.f;
+  }
+  f32x4 oacc[2][2];
+#pragma unroll
+  for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+    for (int db = 0; db < 2; db++) oacc[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb0 = 0; kb0 < nkey; kb0 += AKB) {
+    const int kb1 = min(nkey, kb0 + AKB), nk = kb1 - kb0, nk32 = (nk + 31) & ~31;
+    // ---- scores of 16-key blocks b = wv, wv + 4, ...
+    for (int b = wv; b < (nk + 15) >> 4; b += 4) {
+      const int key = kb0 + 16 * b + r16;
+      u32x4 kf[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++)
+        kf[ks] = key < kb1 ? ldw(K + (size_t)key * HD + 32 * ks + 8 * kg) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int rb = 0; rb < 2; rb++) {
+        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) a = mfma_16x16x32(qf[rb][ks], kf[ks], a);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int rl = 16 * rb + 4 * kg + e;
+          s_sc[rl][16 * b + r16] = (key <= r0 + rl && key < kb1) ? a[e] * scale : -INFINITY;
+        }
+      }
+    }
+    __syncthreads();
+    // ---- softmax rows 8 wv .. 8 wv + 7
+    for (int i = 0; i < 8; i++) {
+      const int rl = 8 * wv + i;
+      float mx = -INFINITY;
+      for (int c = lane; c < nk; c += 64) mx = fmaxf(mx, s_sc[rl][c]);
+      mx = wave_max(mx);
+      const float mo = s_m[rl];
+      const float mn = fmaxf(mo, mx);
+      const float base = mn == -INFINITY ? 0.f : mn;
+      float sum = 0.f;
+      for (int c = lane; c < nk32; c += 64) {
+        const float e = c < nk ? expf(s_sc[rl][c] - base) : 0.f;
+        sum += e;
+        s_p[rl][c] = (uint16_t)f2bf(e);
+      }
+      sum = wave_sum(sum);
+      const float al = mo == -INFINITY ? 0.f : expf(mo - base);
+      if (lane == 0) {
+        s_m[rl] = mn;
+        s_l[rl] = sum + al * s_l[rl];
+        s_a[rl] = al;
+      }
+    }
+    __syncthreads();
+    // ---- P.V: wave wv owns dims 32 wv .. 32 wv + 31
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float al = s_a[16 * rb + 4 * kg + e];
+        oacc[rb][0][e] *= al;
+        oacc[rb][1][e] *= al;
+      }
+    for (int kk = 0; kk < nk32 >> 5; kk++) {
+      const int kbase = kb0 + 32 * kk + 8 * kg;
+      u32x4 vf[2];
+#pragma unroll
+      for (int db = 0; db < 2; db++) {
+        const uint16_t* vp = V + 32 * wv + 16 * db + r16;
+        uint32_t t[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) t[u] = kbase + u < kb1 ? (uint32_t)ldraw16(vp + (size_t)(kbase + u) * HD) : 0u;
+        vf[db] = u32x4{t[0] | (t[1] << 16), t[2] | (t[3] << 16), t[4] | (t[5] << 16), t[6] | (t[7] << 16)};
+      }
+#pragma unroll
+      for (int rb = 0; rb < 2; rb++) {
+        const u32x4 pfr = *reinterpret_cast<const u32x4*>(&s_p[16 * rb + r16][32 * kk + 8 * kg]);
+        oacc[rb][0] = mfma_16x16x32(pfr, vf[0], oacc[rb][0]);
+        oacc[rb][1] = mfma_16x16x32(pfr, vf[1], oacc[rb][1]);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int rl = 16 * rb + 4 * kg + e, row = r0 + rl;
+      if (row >= S) continue;
+      const float inv = 1.0f / s_l[rl];
+      uint16_t* o = out + (size_t)row * QS + HD * h + 32 * wv + r16;
+      o[0] = (uint16_t)f2bf(oacc[rb][0][e] * inv);
+      o[16] = (uint16_t)f2bf(oacc[rb][1][e] * inv);
+    }
+}
+
+// ------------------------------------------------------------------ LM head
+constexpr int LMB = 1184;  // partial-argmax blocks (the length of the reference's block_max_* buffers)
+
+// Final norm of the last hidden row (every workgroup computes it; workgroup 0 also
+// writes it to final_hidden and the raw row to hidden_out), then the bf16 logits of
+// rows [VOCAB * b / LMB, VOCAB * (b+1) / LMB) of the tied LM head and their argmax
+// (lowest index on ties).
+__global__ void __launch_bounds__(256) lm_partial(const uint16_t* hlast, const uint16_t* fnw, const uint16_t* lm,
+                                                  uint16_t* final_hidden, uint16_t* hidden_out, float* bmv, int* bmi) {
+  __shared__ __align__(16) uint32_t s_x[H / 2];
+  __shared__ float s_ss[4], s_bv[4];
+  __shared__ int s_bi[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, b = blockIdx.x;
+  const u32x2 xw = ldw2(hlast + 4 * tid), ww = ldw2(fnw + 4 * tid);
+  const float x[4] = {bflo(xw.x), bfhi(xw.x), bflo(xw.y), bfhi(xw.y)};
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) ss = fmaf(x[i], x[i], ss);
+  ss = wave_sum(ss);
+  if (lane == 0) s_ss[wv] = ss;
+  __syncthreads();
+  const float rstd = 1.0f / sqrtf(((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3])) * (1.0f / H) + EPS);
+  const uint32_t n0 = pack_bf2(rbf(bflo(ww.x) * rbf(x[0] * rstd)), rbf(bfhi(ww.x) * rbf(x[1] * rstd)));
+  const uint32_t n1 = pack_bf2(rbf(bflo(ww.y) * rbf(x[2] * rstd)), rbf(bfhi(ww.y) * rbf(x[3] * rstd)));
+  s_x[2 * tid] = n0;
+  s_x[2 * tid + 1] = n1;
+  if (b == 0) {
+    reinterpret_cast<u32x2*>(final_hidden)[tid] = u32x2{n0, n1};
+    reinterpret_cast<u32x2*>(hidden_out)[tid] = xw;
+  }
+  __syncthreads();
+  const u32x4 xa = reinterpret_cast<const u32x4*>(s_x)[lane], xb = reinterpret_cast<const u32x4*>(s_x)[64 + lane];
+  const int r0 = (int)((long long)VOCAB * b / LMB), r1 = (int)((long long)VOCAB * (b + 1) / LMB);
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int r = r0 + wv; r < r1; r += 16) {
+    u32x4 wa[4], wb[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int rr = min(r + 4 * u, r1 - 1);
+      wa[u] = ldw(lm + (size_t)rr * H + 8 * lane);
+      wb[u] = ldw(lm + (size_t)rr * H + 512 + 8 * lane);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const float lg = rbf(wave_sum(dot_chunk(wa[u], xa, dot_chunk(wb[u], xb, 0.f))));
+      if (r + 4 * u < r1 && lg > bv) {
+        bv = lg;
+        bi = r + 4 * u;
+      }
+    }
+  }
+  if (lane == 0) {
+    s_bv[wv] = bv;
+    s_bi[wv] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int i = 1; i < 4; i++)
+      if (s_bv[i] > bv || (s_bv[i] == bv && s_bi[i] < bi)) {
+        bv = s_bv[i];
+        bi = s_bi[i];
+      }
+    bmv[b] = bv;
+    bmi[b] = bi;
+  }
+}
+
+__global__ void __launch_bounds__(256) argmax_final(const float* bmv, const int* bmi, int* out, uint32_t* err) {
+  __shared__ float s_bv[4];
+  __shared__ int s_bi[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  float v = -INFINITY;
+  int i = 0x7fffffff;
+  for (int b = tid; b < LMB; b += 256) {
+    const float bv = bmv[b];
+    const int bi = bmi[b];
+    if (bv > v || (bv == v && bi < i)) {
+      v = bv;
+      i = bi;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(v, off, 64);
+    const int oi = __shfl_xor(i, off, 64);
+    if (ov > v || (ov == v && oi < i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+  if (lane == 0) {
+    s_bv[wv] = v;
+    s_bi[wv] = i;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; w++)
+      if (s_bv[w] > v || (s_bv[w] == v && s_bi[w] < i)) {
+        v = s_bv[w];
+        i = s_bi[w];
+      }
+    const uint32_t e = *err;
+    *out = e ? -(int)(1u + e) : i;
+    if (e) *err = 0u;
+  }
+}
+
+}  // namespace pf
+}  // namespace mq
+
+using namespace mq;
+using namespace mq::pf;
+
+extern "C" int launch_prefill_float(const int* input_token_ids, int* output_token_id, int seq_len,
+                                    const void* embed_weight, const PrefillLayerWeights* layer_weights,
+                                    const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
+                                    const void* sin_table, void* k_cache, void* v_cache, void* hidden_bf16,
+                                    void* residual, void* normalized, void* q_proj, void* k_proj, void* v_proj,
+                                    void* attn_out, void* o_proj_out, void* mlp_norm, void* gate_out, void* up_out,
+                                    void* mlp_intermediate, void* down_out, void* final_hidden, void* block_max_vals,
+                                    void* block_max_idxs, void* hidden_bf16_out, int num_layers, int max_seq_len,
+                                    float attn_scale, hipStream_t stream) {
+  (void)residual; (void)o_proj_out; (void)gate_out; (void)up_out; (void)down_out;
+  if (!input_token_ids || !output_token_id || !embed_weight || !layer_weights || !final_norm_weight ||
+      !lm_head_weight || !cos_table || !sin_table || !k_cache || !v_cache || !hidden_bf16 || !normalized ||
+      !q_proj || !k_proj || !v_proj || !attn_out || !mlp_norm || !mlp_intermediate || !final_hidden ||
+      !block_max_vals || !block_max_idxs || !hidden_bf16_out)
+    return MQ_ERR_ARG;
+  if (seq_len < 1 || max_seq_len < 1 || seq_len > max_seq_len || num_layers < 1 || num_layers > MAX_LAYERS ||
+      !(attn_scale > 0.f) || !isfinite(attn_scale))
+    return MQ_ERR_ARG;
+  for (int l = 0; l < num_layers; l++) {
+    const PrefillLayerWeights& w = layer_weights[l];
+    if (!w.input_layernorm_weight || !w.q_proj_weight || !w.k_proj_weight || !w.v_proj_weight ||
+        !w.q_norm_weight || !w.k_norm_weight || !w.o_proj_weight || !w.post_attn_layernorm_weight ||
+        !w.gate_proj_weight || !w.up_proj_weight || !w.down_proj_weight)
+      return MQ_ERR_ARG;
+  }
+  uint32_t* ws = nullptr;
+  const int st = current_workspace(&ws);
+  if (st != MQ_OK) return st;
+  uint32_t* err = ws + WS_PREFILL_ERR;
+
+  const int S = seq_len;
+  auto bf = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  auto bfm = [](void* p) { return static_cast<uint16_t*>(p); };
+  uint16_t* h = bfm(hidden_bf16);
+  uint16_t* nrm = bfm(normalized);
+  uint16_t* qp = bfm(q_proj);
+  uint16_t* kp = bfm(k_proj);
+  uint16_t* vp = bfm(v_proj);
+  uint16_t* att = bfm(attn_out);
+  uint16_t* mln = bfm(mlp_norm);
+  uint16_t* mid = bfm(mlp_intermediate);
+  const size_t kv_layer = (size_t)NKV * max_seq_len * HD;
+  const int mt = (S + TM - 1) / TM;
+
+  hipError_t launch_err = hipSuccess;
+  auto chk = [&]() {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess && launch_err == hipSuccess) launch_err = e;
+  };
+  (void)hipGetLastError();  // clear an error left by an unrelated earlier call
+  embed_rows<<<S, 128, 0, stream>>>(input_token_ids, bf(embed_weight), h, err);
+  chk();
+  for (int l = 0; l < num_layers; l++) {
+    const PrefillLayerWeights& w = layer_weights[l];
+    uint16_t* kcl = bfm(k_cache) + l * kv_layer;
+    uint16_t* vcl = bfm(v_cache) + l * kv_layer;
+    rmsnorm_rows<<<(S + 3) / 4, 256, 0, stream>>>(h, bf(w.input_layernorm_weight), nrm, S);
+    chk();
+    GemmArgs g{};
+    g.a = nrm; g.lda = H; g.m = S; g.k = H; g.nseg = 3;
+    g.seg[0] = GemmSeg{bf(w.q_proj_weight), nullptr, qp, QS / TN, QS};
+    g.seg[1] = GemmSeg{bf(w.k_proj_weight), nullptr, kp, KVS / TN, KVS};
+    g.seg[2] = GemmSeg{bf(w.v_proj_weight), nullptr, vp, KVS / TN, KVS};
+    gemm_nt<EPI_STORE><<<dim3((QS + 2 * KVS) / TN, mt), GT, 0, stream>>>(g);
+    chk();
+    qk_rope_kv<<<S, 256, 0, stream>>>(qp, kp, vp, bf(w.q_norm_weight), bf(w.k_norm_weight), bf(cos_table),
+                                      bf(sin_table), kcl, vcl, max_seq_len);
+    chk();
+    attn_prefill<<<dim3((S + AQ - 1) / AQ, NQ), 256, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
+    chk();
+    GemmArgs go{};
+    go.a = att; go.lda = QS; go.m = S; go.k = QS; go.nseg = 1;
+    go.seg[0] = GemmSeg{bf(w.o_proj_weight), nullptr, h, H / TN, H};
+    gemm_nt<EPI_RESID><<<dim3(H / TN, mt), GT, 0, stream>>>(go);
+    chk();
+    rmsnorm_rows<<<(S + 3) / 4, 256, 0, stream>>>(h, bf(w.post_attn_layernorm_weight), mln, S);
+    chk();
+    GemmArgs gu{};
+    gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
+    gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, I / 32, I};
+    gemm_nt<EPI_SILU><<<dim3(I / 32, mt), GT, 0, stream>>>(gu);
+    chk();
+    GemmArgs gd{};
+    gd.a = mid; gd.lda = I; gd.m = S; gd.k = I; gd.nseg = 1;
+    gd.seg[0] = GemmSeg{bf(w.down_proj_weight), nullptr, h, H / TN, H};
+    gemm_nt<EPI_RESID><<<dim3(H / TN, mt), GT, 0, stream>>>(gd);
+    chk();
+  }
+  lm_partial<<<LMB, 256, 0, stream>>>(h + (size_t)(S - 1) * H, bf(final_norm_weight), bf(lm_head_weight),
+                                      bfm(final_hidden), bfm(hidden_bf16_out), static_cast<float*>(block_max_vals),
+                                      static_cast<int*>(block_max_idxs));
+  chk();
+  argmax_final<<<1, 256, 0, stream>>>(static_cast<const float*>(block_max_vals),
+                                      static_cast<const int*>(block_max_idxs), output_token_id, err);
+  chk();
+  return launch_err == hipSuccess ? MQ_OK : MQ_ERR_HIP;
+}

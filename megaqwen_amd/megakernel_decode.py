@@ -128,7 +128,8 @@ class MegakernelDecoder:
         tok = int(self.output_token_.item())
         if tok < 0:
             _abi.lib().mq_reset_workspace(self.embed_weight_.device.index or 0)
-            raise _abi.MegakernelError(f"decode kernel watchdog fired (code {-tok - 1}); workspace reset")
+            raise _abi.MegakernelError(f"kernel reported error flags {-tok - 1} (decode watchdog, or a prompt id "
+                                       f"out of range in prefill); workspace reset")
         return tok
 
     # -- reference API ---------------------------------------------------------
@@ -176,6 +177,77 @@ class MegakernelDecoder:
     def normalized_state(self) -> torch.Tensor:
         """Final-norm output (fp32 [1024]) of the last step."""
         return self.g_normalized_
+
+
+def make_layer_struct_host(layer_weights_flat, num_layers):
+    """HOST array of PrefillLayerWeights, as the reference passes to the prefill
+    launcher (megakernel_decode.py:516); the caller keeps it alive."""
+    arr = (_abi.LDGLayerWeights * num_layers)()
+    for i in range(num_layers):
+        for f, name in enumerate(_abi.LAYER_FIELDS):
+            setattr(arr[i], name, layer_weights_flat[i * 11 + f].data_ptr())
+    return arr
+
+
+class MegakernelPrefillDecoder(MegakernelDecoder):
+    """Prompt prefill + greedy decode (reference `MegakernelPrefillDecoder`,
+    megakernel_decode.py:375-660).
+
+    `prefill_step(ids)` runs the whole prompt through the MFMA prefill kernels,
+    writes KV slots 0..S-1, sets the position to S and returns the greedy next
+    token; `decode_step` then continues one token at a time. Raises for an empty
+    prompt or one longer than `max_prefill_len` (the reference's checks, :499-504).
+    """
+
+    def __init__(self, embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight, cos_table, sin_table,
+                 num_layers: int, max_seq_len: int, max_prefill_len: int = 512):
+        super().__init__(embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight, cos_table, sin_table,
+                         num_layers, max_seq_len)
+        if not 1 <= max_prefill_len <= max_seq_len:
+            raise ValueError("max_prefill_len must be in [1, max_seq_len]")
+        self.max_prefill_len_ = max_prefill_len
+        self.h_layer_weights_ = make_layer_struct_host(self.layer_weights_tensors_, num_layers)
+        dev = embed_weight.device
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        P = max_prefill_len
+        # Prefill scratch in the reference's shapes (megakernel_decode.py:453-466); the ones
+        # this build fuses away are not allocated and are passed as NULL.
+        self.hidden_float_ = torch.empty(P, HIDDEN_SIZE, **bf)
+        self.normalized_ = torch.empty(P, HIDDEN_SIZE, **bf)
+        self.q_proj_ = torch.empty(P, Q_SIZE, **bf)
+        self.k_proj_ = torch.empty(P, KV_SIZE, **bf)
+        self.v_proj_ = torch.empty(P, KV_SIZE, **bf)
+        self.attn_out_ = torch.empty(P, Q_SIZE, **bf)
+        self.mlp_norm_ = torch.empty(P, HIDDEN_SIZE, **bf)
+        self.mlp_intermediate_ = torch.empty(P, INTERMEDIATE_SIZE, **bf)
+        self.final_hidden_ = torch.empty(HIDDEN_SIZE, **bf)
+        self.input_tokens_ = torch.empty(P, dtype=torch.int32, device=dev)
+
+    def prefill_step_async(self, input_token_ids) -> torch.Tensor:
+        """Launch the prefill without the device->host read; returns the device token tensor."""
+        ids = torch.as_tensor(input_token_ids, dtype=torch.int32).reshape(-1)
+        n = int(ids.numel())
+        if n == 0:
+            raise RuntimeError("Empty input sequence")
+        if n > self.max_prefill_len_:
+            raise RuntimeError("Prefill sequence length exceeds maximum")
+        self.input_tokens_[:n].copy_(ids.to(self.input_tokens_.device), non_blocking=False)
+        st = _abi.lib().launch_prefill_float(
+            _ptr(self.input_tokens_), _ptr(self.output_token_), n, _ptr(self.embed_weight_),
+            ctypes.addressof(self.h_layer_weights_), _ptr(self.final_norm_weight_), _ptr(self.lm_head_weight_),
+            _ptr(self.cos_table_), _ptr(self.sin_table_), _ptr(self.k_cache_), _ptr(self.v_cache_),
+            _ptr(self.hidden_float_), None, _ptr(self.normalized_), _ptr(self.q_proj_), _ptr(self.k_proj_),
+            _ptr(self.v_proj_), _ptr(self.attn_out_), None, _ptr(self.mlp_norm_), None, None,
+            _ptr(self.mlp_intermediate_), None, _ptr(self.final_hidden_), _ptr(self.block_max_vals_),
+            _ptr(self.block_max_idxs_), _ptr(self.hidden_buffer_), self.num_layers_, self.max_seq_len_,
+            self.attn_scale_, _stream())
+        _abi.check(st, "launch_prefill_float")
+        self.position_ = n
+        return self.output_token_
+
+    def prefill_step(self, input_token_ids) -> int:
+        self.prefill_step_async(input_token_ids)
+        return self._read_token()
 
 
 def decode_layer(hidden_in: torch.Tensor, layer_weights: list, cos_table, sin_table, k_cache, v_cache,
@@ -283,3 +355,63 @@ class MegakernelGenerator:
             cur = nxt
             if self.decoder.position() >= self.max_seq_len - 1:
                 break
+
+
+class MegakernelPrefillGenerator:
+    """Generator using the prefill kernels for the prompt and the decode kernel after
+    it (reference megakernel_decode.py:1214-1307). Prompts are token-id lists."""
+
+    def __init__(self, model_name=None, max_seq_len: int = 2048, max_prefill_len: int = 512, seed: int = 0,
+                 weights_dict=None):
+        w = weights_dict or load_qwen3_weights(model_name, seed=seed, max_seq_len=max_seq_len)
+        self.weights = w
+        self.decoder = MegakernelPrefillDecoder(w["embed_weight"], w["layer_weights"], w["final_norm_weight"],
+                                                w["lm_head_weight"], w["cos_table"], w["sin_table"],
+                                                len(w["layer_weights"]) // 11, max_seq_len, max_prefill_len)
+        self.tokenizer = w.get("tokenizer")
+        self.max_seq_len = max_seq_len
+        self.max_prefill_len = max_prefill_len
+
+    def _ids(self, prompt):
+        if isinstance(prompt, str):
+            if self.tokenizer is None:
+                raise ValueError("string prompts need a tokenizer; pass a list of token ids")
+            prompt = self.tokenizer.encode(prompt, add_special_tokens=True)
+        ids = [int(t) for t in prompt]
+        if len(ids) > self.max_prefill_len:
+            raise ValueError(f"Prompt length {len(ids)} exceeds max prefill length {self.max_prefill_len}")
+        return ids
+
+    def generate_ids(self, prompt, max_new_tokens: int = 100, stop_tokens=None):
+        self.decoder.reset()
+        nxt = self.decoder.prefill_step(torch.tensor(self._ids(prompt), dtype=torch.int32))
+        out, stop = [], set(stop_tokens or [])
+        for _ in range(max_new_tokens):
+            if nxt in stop:
+                break
+            out.append(nxt)
+            if self.decoder.position() >= self.max_seq_len - 1:
+                break
+            nxt = self.decoder.decode_step(nxt)
+        return out
+
+    def generate(self, prompt, max_new_tokens: int = 100, stop_tokens=None):
+        ids = self.generate_ids(prompt, max_new_tokens, stop_tokens)
+        return self.tokenizer.decode(ids, skip_special_tokens=True) if self.tokenizer else ids
+
+    def generate_stream(self, prompt, max_new_tokens: int = 100, stop_tokens=None):
+        self.decoder.reset()
+        nxt = self.decoder.prefill_step(torch.tensor(self._ids(prompt), dtype=torch.int32))
+        stop = set(stop_tokens or [])
+        for _ in range(max_new_tokens):
+            if nxt in stop:
+                break
+            yield self.tokenizer.decode([nxt]) if self.tokenizer else nxt
+            if self.decoder.position() >= self.max_seq_len - 1:
+                break
+            nxt = self.decoder.decode_step(nxt)
+
+    def prefill_only(self, prompt):
+        self.decoder.reset()
+        nxt = self.decoder.prefill_step(torch.tensor(self._ids(prompt), dtype=torch.int32))
+        return nxt, self.decoder.position()

@@ -26,7 +26,7 @@ def declared_functions():
 
 def test_header_declares_expected_entry_points():
     names = declared_functions()
-    for n in ("launch_ldg_decode", "launch_ldg_decode_with_logits", "mq_decode_layer",
+    for n in ("launch_ldg_decode", "launch_ldg_decode_with_logits", "mq_decode_layer", "launch_prefill_float",
               "mq_reset_workspace", "mq_strerror"):
         assert n in names, n
 
@@ -72,6 +72,35 @@ def test_decode_layer_rejects_invalid_arguments():
     assert L.mq_decode_layer(None, 1, 1, 1, 1, 1, 1, 0, 16, 0.088, None) == _abi.MQ_ERR_ARG
     assert L.mq_decode_layer(1, 1, 1, 1, 1, 1, 1, 16, 16, 0.088, None) == _abi.MQ_ERR_ARG
     assert L.mq_decode_layer(1, 1, 1, 1, 1, 1, 1, 0, 16, -1.0, None) == _abi.MQ_ERR_ARG
+
+
+def _prefill_args(**over):
+    layers = (_abi.LDGLayerWeights * 2)()
+    for i in range(2):
+        for name in _abi.LAYER_FIELDS:
+            setattr(layers[i], name, 1)
+    if over.pop("null_layer_field", False):
+        layers[1].down_proj_weight = None
+    a = dict(ids=1, out=1, seq_len=8, embed=1, layers=ctypes.addressof(layers), norm=1, lm=1, cos=1, sin=1, k=1,
+             v=1, num_layers=2, max_seq_len=16, scale=0.088)
+    a.update(over)
+    scratch = [1] * 17
+    scratch[1] = scratch[7] = scratch[9] = scratch[10] = scratch[12] = None  # unused by this build
+    if a.pop("null_scratch", False):
+        scratch[3] = None  # q_proj
+    return layers, [a["ids"], a["out"], a["seq_len"], a["embed"], a["layers"], a["norm"], a["lm"], a["cos"],
+                    a["sin"], a["k"], a["v"]] + scratch + [a["num_layers"], a["max_seq_len"], a["scale"], None]
+
+
+@pytest.mark.parametrize("bad", [
+    dict(ids=None), dict(out=None), dict(layers=None), dict(k=None), dict(null_scratch=True),
+    dict(null_layer_field=True), dict(seq_len=0), dict(seq_len=17), dict(num_layers=0), dict(num_layers=33),
+    dict(max_seq_len=0), dict(scale=0.0), dict(scale=float("inf")),
+])
+def test_prefill_rejects_invalid_arguments(bad):
+    keep, args = _prefill_args(**bad)
+    assert _abi.lib().launch_prefill_float(*args) == _abi.MQ_ERR_ARG
+    del keep
 
 
 def test_strerror():

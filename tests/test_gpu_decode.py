@@ -14,31 +14,9 @@ from conftest import load_npz
 from megaqwen_amd import megakernel_decode as MK
 from megaqwen_amd import rope, weights
 from oracle import qwen3_oracle as O
+from parity_helpers import LOGIT_MAX_ABS, LOGIT_MEAN_ABS, TIE_TOL, f32, hf_tie_set, ulp_close
 
 pytestmark = pytest.mark.gpu
-
-LOGIT_MAX_ABS = 0.0625
-LOGIT_MEAN_ABS = 0.01
-
-
-def u16(t):
-    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
-
-
-def f32(t):
-    return O.u16_to_f32(u16(t))
-
-
-def ulp_close(a, b, max_ulps=1, max_frac=0.05, floor=2.0 ** -8):
-    """bf16 arrays a, b (fp32-held) differ by <= max_ulps bf16 ulps of max(|b|, floor-scale),
-    in <= max_frac of the elements. The floor covers values that cancel to near
-    zero (e.g. h + o), whose absolute error is set by the operands' ulps."""
-    a = np.asarray(a, np.float32)
-    b = np.asarray(b, np.float32)
-    ulp = np.maximum(np.abs(b), 1e-30).view(np.uint32) & 0x7F800000
-    ulp = np.maximum((ulp.view(np.float32) * 2.0 ** -7).astype(np.float32), floor)
-    d = np.abs(a - b)
-    return bool(np.all(d <= max_ulps * ulp) and (d > 0).mean() <= max_frac), float(d.max()), float((d > 0).mean())
 
 
 @pytest.fixture(scope="module")
@@ -123,16 +101,6 @@ def decoder(gpu_weights):
     w = gpu_weights
     return MK.MegakernelDecoder(w["embed_weight"], w["layer_weights"], w["final_norm_weight"], w["lm_head_weight"],
                                 w["cos_table"], w["sin_table"], 28, 2048)
-
-
-# Near-tie tolerance for argmax comparisons: two candidates whose bf16 logits
-# differ by less than this are a tie under the logit tolerance.
-TIE_TOL = LOGIT_MAX_ABS
-
-
-def hf_tie_set(fx, step):
-    vals, ids = fx["topk_vals"][step], fx["topk_ids"][step]
-    return set(ids[vals >= vals[0] - TIE_TOL].tolist())
 
 
 def test_greedy_config1_teacher_forced_vs_hf(decoder):
