@@ -26,6 +26,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode tok/s batch=1 Qwen3-0.6B at pos 1/200/2048; achieved HBM GB/s"
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
 
 
 def log(*a):
@@ -43,6 +44,8 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (for rocprofv3 counter scaling)")
     ap.add_argument("--cpu-decode-tokens", type=int, default=32)
+    ap.add_argument("--prefill-len", type=int, default=512, help="prompt length of the prefill timing (config 4)")
+    ap.add_argument("--no-prefill", action="store_true")
     return ap.parse_args()
 
 
@@ -82,6 +85,26 @@ def time_decode(dec, position: int, steps: int, warmup: int, token: int = 1234):
     tok = int(dec.output_token_.item())
     assert tok >= 0, f"decode kernel reported an error ({tok})"
     return ms, wall / steps * 1e3
+
+
+def time_prefill(dec, ids, steps: int, warmup: int):
+    """Average device time of one prefill of `ids` over `steps` back-to-back launches
+    (each prefill rewrites KV slots 0..S-1 with the same values)."""
+    import torch
+
+    t = torch.tensor(ids, dtype=torch.int32, device="cuda")  # resident: no host copy in the timed region
+    for _ in range(warmup):
+        dec.prefill_step_async(t)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        dec.prefill_step_async(t)
+    end.record()
+    torch.cuda.synchronize()
+    tok = int(dec.output_token_.item())
+    assert tok >= 0, f"prefill reported an error ({tok})"
+    return start.elapsed_time(end) / steps
 
 
 def e2e_generate(dec, prompt, n_new):
@@ -174,8 +197,9 @@ def main():
     max_seq = 2048 + 16
     w = MK.load_qwen3_weights(seed=0, max_seq_len=max_seq)
     log(f"weights ready in {time.perf_counter() - t0:.1f}s")
-    dec = MK.MegakernelDecoder(w["embed_weight"], w["layer_weights"], w["final_norm_weight"], w["lm_head_weight"],
-                               w["cos_table"], w["sin_table"], C.NUM_LAYERS, max_seq)
+    dec = MK.MegakernelPrefillDecoder(w["embed_weight"], w["layer_weights"], w["final_norm_weight"],
+                                      w["lm_head_weight"], w["cos_table"], w["sin_table"], C.NUM_LAYERS, max_seq,
+                                      max(args.prefill_len, 1))
     positions = [int(p) for p in args.positions.split(",")]
     per_pos = {}
     for p in positions:
@@ -186,6 +210,16 @@ def main():
                       "wall_ms": wall_ms}
         log(f"pos {p}: {ms * 1e3:.1f} us/step, {1e3 / ms:.0f} tok/s, "
             f"{per_pos[p]['hbm_gbs']:.0f} GB/s algorithmic ({per_pos[p]['hbm_gbs'] / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+    prefill = None
+    if not args.no_prefill:
+        S = args.prefill_len
+        pms = time_prefill(dec, weights.random_prompt(S, seed=1), steps=10, warmup=2)
+        fl = C.prefill_flops(S)
+        prefill = {"seq_len": S, "ms": round(pms, 4), "tok_s": round(S / (pms * 1e-3), 1),
+                   "tflops": round(fl / (pms * 1e-3) / 1e12, 2), "flops": fl,
+                   "mfma_frac": round(fl / (pms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)}
+        log(f"prefill S={S}: {pms:.3f} ms, {prefill['tok_s']:.0f} tok/s, {prefill['tflops']:.1f} TFLOP/s "
+            f"({prefill['mfma_frac']:.1%} of {MFMA_PEAK_TFLOPS:.0f} dense bf16)")
     main_p = 200
     ms = per_pos[main_p]["ms"]
     e2e = None
@@ -222,6 +256,7 @@ def main():
                                "roofline_frac": round(v["hbm_gbs"] / HBM_PEAK_GBS, 4), "us_per_step": round(v["ms"] * 1e3, 2)}
                       for p, v in per_pos.items()},
         "e2e_generate_tok_s": None if e2e is None else round(e2e, 1),
+        "prefill": prefill,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -69,3 +69,18 @@ def decode_bytes(position: int) -> int:
     positions 0..position + KV write of slot `position`.
     """
     return WEIGHT_BYTES_PER_TOKEN + KV_BYTES_PER_POSITION * (position + 1) + KV_BYTES_PER_POSITION
+
+
+# Matrix-product flops of one prefill of S tokens (the MFMA work).
+LINEAR_PARAMS = NUM_LAYERS * sum(_numel(s) for n, s in LAYER_WEIGHT_SHAPES.items() if len(s) == 2)
+
+
+def prefill_flops(seq_len: int) -> int:
+    """2 flops per multiply-add: the 7 linear layers of every layer for all S rows,
+    causal attention (QK^T and PV over keys 0..s for row s, 16 query heads of 128),
+    and the tied LM head for the last row."""
+    S = seq_len
+    linear = 2 * S * LINEAR_PARAMS
+    attention = NUM_LAYERS * NUM_Q_HEADS * 2 * 2 * HEAD_DIM * S * (S + 1) // 2
+    lm_head = 2 * VOCAB_SIZE * HIDDEN_SIZE
+    return linear + attention + lm_head

@@ -35,10 +35,13 @@ namespace pf {
 
 // ------------------------------------------------------------------ GEMM
 // C[m, n] = sum_k A[m, k] * W[n, k] (both operands k-contiguous, HF nn.Linear
-// layout), one 64 x 64 output tile per workgroup, k in steps of 64 staged
-// through LDS (double-buffered). Wave w computes rows 16w .. 16w+15 of the tile
-// against all 64 columns: four 16x16 MFMA blocks sharing one A fragment.
-constexpr int TM = 64, TN = 64, TK = 64, GT = 256;
+// layout), one TM x 64 output tile per workgroup, k in steps of 64 staged
+// through LDS (double-buffered). The four waves form a 2 x 2 grid: wave (wm, wn)
+// owns rows 32wm.. (TM = 64) or 16wm.. (TM = 32) of the tile and two 16-column
+// blocks, so every 16-byte fragment read from LDS feeds one or two MFMAs.
+// TM = 32 is used for the N = 1024 products (o_proj, down_proj) so that a
+// 512-row prompt still gives 256 workgroups.
+constexpr int TN = 64, TK = 64, GT = 256;
 
 enum : int { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2 };
 
@@ -60,52 +63,60 @@ struct GemmArgs {
 // one fragment load fall in distinct banks.
 __device__ __forceinline__ int tslot(int r, int kc) { return r * 8 + (kc ^ (r & 7)); }
 
-template <int EPI>
+template <int EPI, int TM>
 __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
+  constexpr int RB = TM / 32;            // 16-row blocks per wave: 2 (TM 64) or 1 (TM 32)
+  constexpr int AC = TM * 8 / GT;        // A chunks per thread per k tile: 2 or 1
   __shared__ u32x4 sa[2][TM * 8];
   __shared__ u32x4 sb[2][TN * 8];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv >> 1, wn = wv & 1;
   int nt = blockIdx.x, si = 0;
   while (si + 1 < G.nseg && nt >= G.seg[si].ntiles) nt -= G.seg[si++].ntiles;
   const GemmSeg S = G.seg[si];
   const int m0 = blockIdx.y * TM;
+  // the wave's two column blocks; EPI_SILU pairs gate block wn with up block wn + 2
+  const int jb0 = EPI == EPI_SILU ? wn : 2 * wn, jb1 = EPI == EPI_SILU ? wn + 2 : 2 * wn + 1;
 
-  // this thread's two A chunks and two B chunks of every k tile
-  const uint16_t* ga[2];
+  const uint16_t* ga[AC];
   const uint16_t* gb[2];
-  bool va[2];
-  int slot[2];
+  bool va[AC];
+  int sla[AC], slb[2];
+#pragma unroll
+  for (int i = 0; i < AC; i++) {
+    const int c = tid + GT * i, r = c >> 3, kc = c & 7;
+    sla[i] = tslot(r, kc);
+    va[i] = m0 + r < G.m;
+    ga[i] = G.a + (size_t)(va[i] ? m0 + r : 0) * G.lda + 8 * kc;
+  }
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     const int c = tid + GT * i, r = c >> 3, kc = c & 7;
-    slot[i] = tslot(r, kc);
-    va[i] = m0 + r < G.m;
-    ga[i] = G.a + (size_t)(va[i] ? m0 + r : 0) * G.lda + 8 * kc;
+    slb[i] = tslot(r, kc);
     if (EPI == EPI_SILU)
       gb[i] = (r < 32 ? S.w + (size_t)(32 * nt + r) * G.k : S.w2 + (size_t)(32 * nt + r - 32) * G.k) + 8 * kc;
     else
       gb[i] = S.w + (size_t)(TN * nt + r) * G.k + 8 * kc;
   }
-  u32x4 ra[2], rb[2];
+  u32x4 ra[AC], rb[2];
   auto gload = [&](int kt) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < AC; i++) {
       const u32x4 t = ldw(ga[i] + kt * TK);
       ra[i] = va[i] ? t : u32x4{0u, 0u, 0u, 0u};
-      rb[i] = ldw(gb[i] + kt * TK);
     }
+#pragma unroll
+    for (int i = 0; i < 2; i++) rb[i] = ldw(gb[i] + kt * TK);
   };
   auto lstore = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      sa[buf][slot[i]] = ra[i];
-      sb[buf][slot[i]] = rb[i];
-    }
+    for (int i = 0; i < AC; i++) sa[buf][sla[i]] = ra[i];
+#pragma unroll
+    for (int i = 0; i < 2; i++) sb[buf][slb[i]] = rb[i];
   };
 
-  f32x4 acc[4];
+  f32x4 acc[RB][2];
 #pragma unroll
-  for (int j = 0; j < 4; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < RB; i++) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int KT = G.k / TK;
   gload(0);
   lstore(0);
@@ -116,9 +127,13 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
       const int kc = 4 * ks + (lane >> 4), r = lane & 15;
-      const u32x4 af = sa[buf][tslot(16 * wv + r, kc)];
+      const u32x4 b0 = sb[buf][tslot(16 * jb0 + r, kc)], b1 = sb[buf][tslot(16 * jb1 + r, kc)];
 #pragma unroll
-      for (int j = 0; j < 4; j++) acc[j] = mfma_16x16x32(af, sb[buf][tslot(16 * j + r, kc)], acc[j]);
+      for (int i = 0; i < RB; i++) {
+        const u32x4 af = sa[buf][tslot(16 * (RB * wm + i) + r, kc)];
+        acc[i][0] = mfma_16x16x32(af, b0, acc[i][0]);
+        acc[i][1] = mfma_16x16x32(af, b1, acc[i][1]);
+      }
     }
     if (kt + 1 < KT) lstore(buf ^ 1);
     __syncthreads();
@@ -127,28 +142,27 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
   // lane holds rows 4 * (lane / 16) + e of column lane % 16 of each block
   const int col = lane & 15, rq = 4 * (lane >> 4);
 #pragma unroll
-  for (int e = 0; e < 4; e++) {
-    const int row = m0 + 16 * wv + rq + e;
-    if (row >= G.m) continue;
-    uint16_t* orow = S.out + (size_t)row * S.ldo;
-    if (EPI == EPI_SILU) {
-      // HF Qwen3MLP (modeling_qwen3.py:81-83): down(bf16(silu(bf16 gate)) * bf16 up)
+  for (int i = 0; i < RB; i++)
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const float g = rbf(acc[j][e]), u = rbf(acc[j + 2][e]);
+    for (int e = 0; e < 4; e++) {
+      const int row = m0 + 16 * (RB * wm + i) + rq + e;
+      if (row >= G.m) continue;
+      uint16_t* orow = S.out + (size_t)row * S.ldo;
+      if (EPI == EPI_SILU) {
+        // HF Qwen3MLP (modeling_qwen3.py:81-83): down(bf16(silu(bf16 gate)) * bf16 up)
+        const float g = rbf(acc[i][0][e]), u = rbf(acc[i][1][e]);
         const float sg = rbf(g / (1.0f + expf(-g)));
-        orow[32 * nt + 16 * j + col] = (uint16_t)f2bf(sg * u);
-      }
-    } else {
+        orow[32 * nt + 16 * wn + col] = (uint16_t)f2bf(sg * u);
+      } else {
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int c = TN * nt + 16 * j + col;
-        float v = rbf(acc[j][e]);
-        if (EPI == EPI_RESID) v = bf2f(orow[c]) + v;  // residual add, rounded once more
-        orow[c] = (uint16_t)f2bf(v);
+        for (int j = 0; j < 2; j++) {
+          const int c = TN * nt + 16 * (j ? jb1 : jb0) + col;
+          float v = rbf(acc[i][j][e]);
+          if (EPI == EPI_RESID) v = bf2f(orow[c]) + v;  // residual add, rounded once more
+          orow[c] = (uint16_t)f2bf(v);
+        }
       }
     }
-  }
 }
 
 // ------------------------------------------------------------------ row-wise kernels
@@ -240,11 +254,14 @@ __global__ void __launch_bounds__(256) qk_rope_kv(uint16_t* q, const uint16_t* k
 // accumulator rescaled by exp(m_old - m_new).
 constexpr int AQ = 32;
 constexpr int AKB = 512;
+constexpr int VT_STRIDE = 72;  // keys per row of the transposed V stage: 64 + 8 (144-byte rows keep
+                               // 16-byte alignment and spread 8 consecutive dims over the banks)
 
 __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                                                     uint16_t* out, int S, int max_seq, float scale) {
   __shared__ float s_sc[AQ][AKB];
   __shared__ __align__(16) uint16_t s_p[AQ][AKB];
+  __shared__ __align__(16) uint16_t s_vt[HD][VT_STRIDE];
   __shared__ float s_m[AQ], s_l[AQ], s_a[AQ];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r0 = blockIdx.x * AQ, h = blockIdx.y, g = h >> 1;
@@ -317,7 +334,9 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
       }
     }
     __syncthreads();
-    // ---- P.V: wave wv owns dims 32 wv .. 32 wv + 31
+    // ---- P.V: wave wv owns dims 32 wv .. 32 wv + 31. V rows are staged through LDS
+    // transposed ([dim][key], 64 keys at a time) so that an MFMA operand (8 keys of
+    // one dim) is one 16-byte read.
 #pragma unroll
     for (int rb = 0; rb < 2; rb++)
 #pragma unroll
@@ -326,23 +345,32 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
         oacc[rb][0][e] *= al;
         oacc[rb][1][e] *= al;
       }
-    for (int kk = 0; kk < nk32 >> 5; kk++) {
-      const int kbase = kb0 + 32 * kk + 8 * kg;
-      u32x4 vf[2];
+    for (int c0 = 0; c0 < nk32; c0 += 64) {
 #pragma unroll
-      for (int db = 0; db < 2; db++) {
-        const uint16_t* vp = V + 32 * wv + 16 * db + r16;
-        uint32_t t[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) t[u] = kbase + u < kb1 ? (uint32_t)ldraw16(vp + (size_t)(kbase + u) * HD) : 0u;
-        vf[db] = u32x4{t[0] | (t[1] << 16), t[2] | (t[3] << 16), t[4] | (t[5] << 16), t[6] | (t[7] << 16)};
+      for (int it = 0; it < 4; it++) {
+        const int dc = 4 * it + wv, key = kb0 + c0 + lane;  // lane: key, dc: 8-dim chunk
+        const u32x4 v = key < kb1 ? ldw(V + (size_t)key * HD + 8 * dc) : u32x4{0u, 0u, 0u, 0u};
+        s_vt[8 * dc + 0][lane] = (uint16_t)v.x;
+        s_vt[8 * dc + 1][lane] = (uint16_t)(v.x >> 16);
+        s_vt[8 * dc + 2][lane] = (uint16_t)v.y;
+        s_vt[8 * dc + 3][lane] = (uint16_t)(v.y >> 16);
+        s_vt[8 * dc + 4][lane] = (uint16_t)v.z;
+        s_vt[8 * dc + 5][lane] = (uint16_t)(v.z >> 16);
+        s_vt[8 * dc + 6][lane] = (uint16_t)v.w;
+        s_vt[8 * dc + 7][lane] = (uint16_t)(v.w >> 16);
       }
+      __syncthreads();
+      for (int kk = 0; kk < 2 && c0 + 32 * kk < nk32; kk++) {
+        const u32x4 vf0 = *reinterpret_cast<const u32x4*>(&s_vt[32 * wv + r16][32 * kk + 8 * kg]);
+        const u32x4 vf1 = *reinterpret_cast<const u32x4*>(&s_vt[32 * wv + 16 + r16][32 * kk + 8 * kg]);
 #pragma unroll
-      for (int rb = 0; rb < 2; rb++) {
-        const u32x4 pfr = *reinterpret_cast<const u32x4*>(&s_p[16 * rb + r16][32 * kk + 8 * kg]);
-        oacc[rb][0] = mfma_16x16x32(pfr, vf[0], oacc[rb][0]);
-        oacc[rb][1] = mfma_16x16x32(pfr, vf[1], oacc[rb][1]);
+        for (int rb = 0; rb < 2; rb++) {
+          const u32x4 pfr = *reinterpret_cast<const u32x4*>(&s_p[16 * rb + r16][c0 + 32 * kk + 8 * kg]);
+          oacc[rb][0] = mfma_16x16x32(pfr, vf0, oacc[rb][0]);
+          oacc[rb][1] = mfma_16x16x32(pfr, vf1, oacc[rb][1]);
+        }
       }
+      __syncthreads();
     }
     __syncthreads();
   }
@@ -515,7 +543,7 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
   uint16_t* mln = bfm(mlp_norm);
   uint16_t* mid = bfm(mlp_intermediate);
   const size_t kv_layer = (size_t)NKV * max_seq_len * HD;
-  const int mt = (S + TM - 1) / TM;
+  const int mt64 = (S + 63) / 64, mt32 = (S + 31) / 32;
 
   hipError_t launch_err = hipSuccess;
   auto chk = [&]() {
@@ -536,7 +564,7 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     g.seg[0] = GemmSeg{bf(w.q_proj_weight), nullptr, qp, QS / TN, QS};
     g.seg[1] = GemmSeg{bf(w.k_proj_weight), nullptr, kp, KVS / TN, KVS};
     g.seg[2] = GemmSeg{bf(w.v_proj_weight), nullptr, vp, KVS / TN, KVS};
-    gemm_nt<EPI_STORE><<<dim3((QS + 2 * KVS) / TN, mt), GT, 0, stream>>>(g);
+    gemm_nt<EPI_STORE, 64><<<dim3((QS + 2 * KVS) / TN, mt64), GT, 0, stream>>>(g);
     chk();
     qk_rope_kv<<<S, 256, 0, stream>>>(qp, kp, vp, bf(w.q_norm_weight), bf(w.k_norm_weight), bf(cos_table),
                                       bf(sin_table), kcl, vcl, max_seq_len);
@@ -546,19 +574,19 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     GemmArgs go{};
     go.a = att; go.lda = QS; go.m = S; go.k = QS; go.nseg = 1;
     go.seg[0] = GemmSeg{bf(w.o_proj_weight), nullptr, h, H / TN, H};
-    gemm_nt<EPI_RESID><<<dim3(H / TN, mt), GT, 0, stream>>>(go);
+    gemm_nt<EPI_RESID, 32><<<dim3(H / TN, mt32), GT, 0, stream>>>(go);
     chk();
     rmsnorm_rows<<<(S + 3) / 4, 256, 0, stream>>>(h, bf(w.post_attn_layernorm_weight), mln, S);
     chk();
     GemmArgs gu{};
     gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
     gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, I / 32, I};
-    gemm_nt<EPI_SILU><<<dim3(I / 32, mt), GT, 0, stream>>>(gu);
+    gemm_nt<EPI_SILU, 64><<<dim3(I / 32, mt64), GT, 0, stream>>>(gu);
     chk();
     GemmArgs gd{};
     gd.a = mid; gd.lda = I; gd.m = S; gd.k = I; gd.nseg = 1;
     gd.seg[0] = GemmSeg{bf(w.down_proj_weight), nullptr, h, H / TN, H};
-    gemm_nt<EPI_RESID><<<dim3(H / TN, mt), GT, 0, stream>>>(gd);
+    gemm_nt<EPI_RESID, 32><<<dim3(H / TN, mt32), GT, 0, stream>>>(gd);
     chk();
   }
   lm_partial<<<LMB, 256, 0, stream>>>(h + (size_t)(S - 1) * H, bf(final_norm_weight), bf(lm_head_weight),
