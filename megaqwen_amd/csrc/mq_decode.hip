@@ -73,8 +73,8 @@ constexpr int WG_PER_XCD = NWG / NXCD;        // 32
 constexpr int ROWS = H / WG_PER_XCD;          // residual-stream rows owned per workgroup: 32
 constexpr int UNITS = I / NWG;                // MLP units per workgroup: 12
 constexpr int XUNITS = I / NXCD;              // MLP units per XCD: 384
-constexpr int KV_CAP = 256;                   // positions per attention workgroup
-constexpr int MAX_CTX = WG_PER_XCD * KV_CAP;  // 8192
+constexpr int KV_CAP = 256;                       // positions per LDS pass of an attention workgroup
+constexpr int MAX_CTX = 2 * WG_PER_XCD * KV_CAP;  // 16384: at most two passes per workgroup
 constexpr int LM_PRE = 4;                     // LM-head rows each stream wave loads during the last layer
 // A layer's K/V copy is issued just before the previous layer's down_proj weights;
 // the next layer's q/k/v (8) and o_proj (4) loads follow it before attention.
@@ -494,6 +494,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ __align__(16) uint16_t s_p[2 * KV_CAP];  // bf16 softmax numerators
   __shared__ float s_sc[2][KV_CAP];                    // attention scores, later the combined output
   __shared__ float s_ao[2][HD];                        // attention output (or unnormalised partial)
+  __shared__ float s_ao1[2][HD];                       // second LDS pass's unnormalised partial
   __shared__ float s_mx[8][2], s_l[8][2];              // per-wave score maxima and softmax sums
   __shared__ float s_hrow[ROWS];                       // residual rows 32j .. 32j+31 of h
   __shared__ float s_res[ROWS];                        // stream-wave dot products for the store wave
@@ -521,14 +522,18 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   const int L = P.num_layers;
   const bool lm = !(P.mode & MODE_NO_LMHEAD);
 
-  // attention chunking: nsplit chunks of <= KV_CAP positions, chunk j on workgroup (g, j)
+  // attention chunking: nsplit chunks of <= 2 KV_CAP positions, chunk j on workgroup (g, j),
+  // attended in npass LDS passes of <= KV_CAP positions (rows KV_CAP.. in the second)
   const int p = P.position, n_ctx = p + 1;
-  const int nsplit = (n_ctx + KV_CAP - 1) / KV_CAP;
+  const int nsplit = min(WG_PER_XCD, (n_ctx + KV_CAP - 1) / KV_CAP);
   const int CH = (n_ctx + nsplit - 1) / nsplit;
   const bool att = j < nsplit;
   const int c0 = j * CH;
   const int nc = att ? min(n_ctx, c0 + CH) - c0 : 0;
-  const bool own_p = att && p >= c0 && p < c0 + nc;
+  const int npass = (nc + KV_CAP - 1) / KV_CAP;
+  const int nc0 = min(nc, KV_CAP);
+  const bool own_p = att && p >= c0 && p < c0 + nc;  // p is always in the last pass
+  const int prow = p - c0 - KV_CAP * (npass - 1);     // its LDS row there
   const bool combine = att && nsplit > 1 && j == 0;
   const uint32_t lds_kv = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)s_kv;
 
@@ -624,7 +629,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         s_wfn[2 * st + 1] = fn.y;
       }
     }
-    if (att) kv_dma(P, 0, g, c0, nc, p, lds_kv, s, lane);
+    if (att) kv_dma(P, 0, g, c0, nc0, p, lds_kv, s, lane);
     load_a(0);
     BAR();  // P0
 
@@ -652,14 +657,22 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       if (att) {
         // this wave's K/V copy of the layer has landed (S_LOADS_AFTER_KV loads followed it)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S_LOADS_AFTER_KV) : "memory");
-        BAR();  // B1: q, the new k/v row and the K/V rows are in LDS
-        attn_scores(s_kv, s_q, s_sc, s_mx, nc, P.attn_scale, wave, lane);
-        BAR();  // B2
-        float M0, M1, L0, L1;
-        attn_softmax(s_sc, s_p, s_mx, s_l, nc, wave, lane, M0, M1);
-        BAR();  // B3
-        attn_pv(s_kv, s_p, s_l, s_ao, nc, wave, lane, nsplit == 1, L0, L1);
-        BAR();  // B4: K/V rows consumed
+        for (int ps = 0; ps < npass; ps++) {
+          if (ps == 1) {
+            // second pass: rows KV_CAP .. nc-1 of the chunk replace the first pass's rows
+            kv_dma(P, layer, g, c0 + KV_CAP, nc - KV_CAP, p, lds_kv, s, lane);
+            wait_vmem();
+          }
+          const int ncp = ps ? nc - KV_CAP : nc0;
+          BAR();  // B1: q, the new k/v row and the K/V rows are in LDS
+          attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
+          BAR();  // B2
+          float M0, M1, L0, L1;
+          attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
+          BAR();  // B3
+          attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+          BAR();  // B4: K/V rows consumed
+        }
         if (combine) BAR();  // B5
       }
       // ---------------- o_proj partials: rows 32j + 8s + 2i + rg over the group's 256 columns
@@ -700,7 +713,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         load_d(layer);
         // the next layer's K/V rows: the LDS copy is free since B4, and its completion is
         // first needed behind the next layer's q/k/v weights
-        if (att && nl < L) kv_dma(P, nl, g, c0, nc, p, lds_kv, s, lane);
+        if (att && nl < L) kv_dma(P, nl, g, c0, nc0, p, lds_kv, s, lane);
       }
       // ---------------- down_proj partials: rows 32j + 8s + i over the XCD's 384 units
       BAR();  // E1: m of the XCD in s_x1
@@ -825,25 +838,30 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             s_q[sg * HD + lane] = (uint16_t)f2bf(fr[sg][0]);
             s_q[sg * HD + 64 + lane] = (uint16_t)f2bf(fr[sg][1]);
           }
-        } else if (own_p) {
-          // the new k and v rows into the LDS copy (the store wave appends them to the cache)
-          const int row = p - c0;
-          const int o0 = kv_off(row, lane >> 3) + 2 * (lane & 7), o1 = kv_off(row, 8 + (lane >> 3)) + 2 * (lane & 7);
-#pragma unroll
-          for (int sg = 0; sg < 2; sg++) {
-            uint8_t* base = s_kv + sg * (KV_CAP * 256);
-            *reinterpret_cast<uint16_t*>(base + o0) = (uint16_t)f2bf(fr[sg][0]);
-            *reinterpret_cast<uint16_t*>(base + o1) = (uint16_t)f2bf(fr[sg][1]);
-          }
         }
-        BAR();  // B1
-        attn_scores(s_kv, s_q, s_sc, s_mx, nc, P.attn_scale, wave, lane);
-        BAR();  // B2
-        float M0, M1, L0, L1;
-        attn_softmax(s_sc, s_p, s_mx, s_l, nc, wave, lane, M0, M1);
-        BAR();  // B3
-        attn_pv(s_kv, s_p, s_l, s_ao, nc, wave, lane, nsplit == 1, L0, L1);
-        BAR();  // B4
+        for (int ps = 0; ps < npass; ps++) {
+          if (c == 1 && own_p && ps == npass - 1) {
+            // the new k and v rows into the LDS copy of the pass that holds position p (the
+            // store wave appends them to the cache); a second pass's copy excludes that row
+            const int o0 = kv_off(prow, lane >> 3) + 2 * (lane & 7);
+            const int o1 = kv_off(prow, 8 + (lane >> 3)) + 2 * (lane & 7);
+#pragma unroll
+            for (int sg = 0; sg < 2; sg++) {
+              uint8_t* base = s_kv + sg * (KV_CAP * 256);
+              *reinterpret_cast<uint16_t*>(base + o0) = (uint16_t)f2bf(fr[sg][0]);
+              *reinterpret_cast<uint16_t*>(base + o1) = (uint16_t)f2bf(fr[sg][1]);
+            }
+          }
+          const int ncp = ps ? nc - KV_CAP : nc0;
+          BAR();  // B1
+          attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
+          BAR();  // B2
+          float M0, M1, L0, L1;
+          attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
+          BAR();  // B3
+          attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+          BAR();  // B4
+        }
         MQ_TRACE(5 + layer * 16);
         if (combine) {
           // outputs (hh, dim) = pt, pt + 128: merge the chunk partials of the XCD's workgroups
@@ -958,14 +976,17 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       BAR();  // A1: h rows in s_hrow
       const float hrow = s_hrow[rr];
       if (att) {
-        BAR();  // B1
-        attn_scores(s_kv, s_q, s_sc, s_mx, nc, P.attn_scale, wave, lane);
-        BAR();  // B2
-        float M0, M1, L0, L1;
-        attn_softmax(s_sc, s_p, s_mx, s_l, nc, wave, lane, M0, M1);
-        BAR();  // B3
-        attn_pv(s_kv, s_p, s_l, s_ao, nc, wave, lane, nsplit == 1, L0, L1);
-        BAR();  // B4
+        for (int ps = 0; ps < npass; ps++) {
+          const int ncp = ps ? nc - KV_CAP : nc0;
+          BAR();  // B1
+          attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
+          BAR();  // B2
+          float M0, M1, L0, L1;
+          attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
+          BAR();  // B3
+          attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+          BAR();  // B4
+        }
         if (combine) BAR();  // B5
       }
       BAR();  // C1
@@ -993,26 +1014,53 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       wait_count(&s_cnt, target);
       if (lane < 16) st1_plain(ws + lb + LX_QKV + 16 * j + lane, tagged(tag, rbf(s_res[lane])));
       if (att) {
-        BAR();  // B1
-        if (own_p) {
-          // K/V-cache append at slot p (bf16 [L][8][max_seq][128]): lane -> dims 2 lane, 2 lane + 1
-          const int row = p - c0;
-          const size_t slot = ((size_t)(layer * NKV + g) * P.max_seq_len + p) * HD;
-          const uint32_t k2 = *reinterpret_cast<const uint32_t*>(s_kv + kv_off(row, lane >> 2) + 4 * (lane & 3));
-          const uint32_t v2 =
-              *reinterpret_cast<const uint32_t*>(s_kv + KV_CAP * 256 + kv_off(row, lane >> 2) + 4 * (lane & 3));
-          st1_plain(reinterpret_cast<uint32_t*>(P.k_cache + slot) + lane, k2);
-          st1_plain(reinterpret_cast<uint32_t*>(P.v_cache + slot) + lane, v2);
+        float M0 = 0.f, M1 = 0.f, L0 = 0.f, L1 = 0.f, Ma0 = 0.f, Ma1 = 0.f, La0 = 0.f, La1 = 0.f;
+        for (int ps = 0; ps < npass; ps++) {
+          const int ncp = ps ? nc - KV_CAP : nc0;
+          BAR();  // B1
+          if (own_p && ps == npass - 1) {
+            // K/V-cache append at slot p (bf16 [L][8][max_seq][128]): lane -> dims 2 lane, 2 lane + 1
+            const size_t slot = ((size_t)(layer * NKV + g) * P.max_seq_len + p) * HD;
+            const uint32_t k2 = *reinterpret_cast<const uint32_t*>(s_kv + kv_off(prow, lane >> 2) + 4 * (lane & 3));
+            const uint32_t v2 =
+                *reinterpret_cast<const uint32_t*>(s_kv + KV_CAP * 256 + kv_off(prow, lane >> 2) + 4 * (lane & 3));
+            st1_plain(reinterpret_cast<uint32_t*>(P.k_cache + slot) + lane, k2);
+            st1_plain(reinterpret_cast<uint32_t*>(P.v_cache + slot) + lane, v2);
+          }
+          attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
+          BAR();  // B2
+          attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
+          BAR();  // B3
+          attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+          BAR();  // B4
+          if (ps == 0) {
+            Ma0 = M0;
+            Ma1 = M1;
+            La0 = L0;
+            La1 = L1;
+          }
         }
-        attn_scores(s_kv, s_q, s_sc, s_mx, nc, P.attn_scale, wave, lane);
-        BAR();  // B2
-        float M0, M1, L0, L1;
-        attn_softmax(s_sc, s_p, s_mx, s_l, nc, wave, lane, M0, M1);
-        BAR();  // B3
-        attn_pv(s_kv, s_p, s_l, s_ao, nc, wave, lane, nsplit == 1, L0, L1);
-        BAR();  // B4
         // lane -> outputs 4 lane .. 4 lane + 3 of head hh = lane / 32
         const int hh = lane >> 5, dim = 4 * (lane & 31);
+        if (npass == 2) {
+          // merge the two passes exactly: rescale both to the larger maximum
+#pragma unroll
+          for (int h2 = 0; h2 < 2; h2++) {
+            const float ma = h2 ? Ma1 : Ma0, mb = h2 ? M1 : M0, mm = fmaxf(ma, mb);
+            const float ea = expf(ma - mm), eb = expf(mb - mm);
+            if (h2 == hh)
+#pragma unroll
+              for (int e = 0; e < 4; e++) s_ao[hh][dim + e] = s_ao[hh][dim + e] * ea + s_ao1[hh][dim + e] * eb;
+            const float lm2 = (h2 ? La1 : La0) * ea + (h2 ? L1 : L0) * eb;
+            if (h2) {
+              M1 = mm;
+              L1 = lm2;
+            } else {
+              M0 = mm;
+              L0 = lm2;
+            }
+          }
+        }
         if (nsplit == 1) {
           st4_plain(ws + lb + LX_ATT + hh * HD + dim,
                     u32x4{tagged(tag, rbf(s_ao[hh][dim])), tagged(tag, rbf(s_ao[hh][dim + 1])),

@@ -51,7 +51,7 @@ def gpu_weights(state_dict):
     dev = "cuda"
     flat = [t.to(dev) for t in weights.layer_weights_flat(state_dict)]
     embed = state_dict["model.embed_tokens.weight"].to(dev)
-    cos, sin = rope.rope_tables(8448)
+    cos, sin = rope.rope_tables(16384)
     return {
         "embed_weight": embed,
         "layer_weights": flat,

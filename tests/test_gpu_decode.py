@@ -73,11 +73,13 @@ def test_block_config2_matches_hf(gpu_weights, layer0, state_dict):
     assert np.array_equal(vg[:, :200], vc[:, :200]) and np.array_equal(vg[:, 201:], vc[:, 201:])
 
 
-@pytest.mark.parametrize("pos", [0, 1, 31, 32, 33, 200, 1023, 1024, 2047, 4097, 8191])
+@pytest.mark.parametrize("pos", [0, 1, 31, 32, 33, 200, 1023, 1024, 2047, 4097, 8191, 8192, 8447, 12000, 16383])
 def test_block_attention_splits_vs_oracle(gpu_weights, layer0, state_dict, pos):
-    """Split-K attention over every split count: random N(0,1) cache, query at `pos`."""
+    """Split-K attention over every split count, and past 8192 positions the two LDS
+    passes per workgroup: random N(0,1) cache, query at `pos`."""
+    print(f"block pos {pos}", flush=True)
     g = torch.Generator().manual_seed(100 + pos)
-    max_seq = 8192
+    max_seq = 16384
     hidden = torch.randn(1024, generator=g).to(torch.bfloat16)
     kc = np.zeros((8, max_seq, 128), np.float32)
     vc = np.zeros_like(kc)
@@ -207,3 +209,26 @@ def test_watchdog_never_fires_and_position_cap(decoder):
     with pytest.raises(RuntimeError):
         decoder.decode_step(tok)
     decoder.reset()
+
+
+def test_config3_2048_steps_teacher_forced_vs_hf(gpu_weights):
+    """Config 3: 16-token prompt, then 2048 greedy decode steps on HF's own token
+    stream (positions up to 2062); ids equal HF's where HF's top-2 margin exceeds
+    TIE_TOL and lie in HF's tie set otherwise."""
+    fx = load_npz("greedy_c3.npz")
+    prompt, hf_ids = fx["prompt"].tolist(), fx["ids"].tolist()
+    w = gpu_weights
+    dec = MK.MegakernelDecoder(w["embed_weight"], w["layer_weights"], w["final_norm_weight"], w["lm_head_weight"],
+                               w["cos_table"], w["sin_table"], 28, 2048 + 16)
+    for t in prompt[:-1]:
+        dec.decode_step(t)
+    stream = [prompt[-1]] + hf_ids[:-1]
+    exact = 0
+    for step, t in enumerate(stream):
+        g = dec.decode_step(t)
+        if fx["margins"][step] > TIE_TOL:
+            assert g == hf_ids[step], (step, g, hf_ids[step])
+        else:
+            assert g in hf_tie_set(fx, step), (step, g)
+        exact += g == hf_ids[step]
+    print(f"config 3 teacher-forced: {exact}/{len(hf_ids)} ids identical to HF")

@@ -193,3 +193,28 @@ def test_config4_free_running(prefill_decoder):
     match = next((i for i, (a, b) in enumerate(zip(ids, hf_ids)) if a != b), len(hf_ids))
     print(f"config 4 free-running: identical for {match}/{len(hf_ids)}; first HF near-tie at {first_tie}")
     assert ids[:first_tie] == hf_ids[:first_tie]
+
+
+def test_config5_long_context_vs_hf(gpu_weights):
+    """Config 5: an 8192-token prompt through the prefill kernels, then 256 greedy
+    decode steps at positions 8192..8447 (every attention workgroup takes two LDS
+    passes) on HF's own token stream; ids equal HF's where HF's top-2 margin exceeds
+    TIE_TOL and lie in HF's tie set otherwise."""
+    fx = load_npz("greedy_c5.npz")
+    prompt, hf_ids = fx["prompt"].tolist(), fx["ids"].tolist()
+    w = gpu_weights
+    dec = MK.MegakernelPrefillDecoder(w["embed_weight"], w["layer_weights"], w["final_norm_weight"],
+                                      w["lm_head_weight"], w["cos_table"], w["sin_table"], 28, 8448, 8192)
+    print("config 5 prefill", flush=True)
+    got = [dec.prefill_step(prompt)]
+    print("config 5 decode", flush=True)
+    for step in range(1, len(hf_ids)):
+        got.append(dec.decode_step(hf_ids[step - 1]))
+    exact = 0
+    for step, (g, r) in enumerate(zip(got, hf_ids)):
+        if fx["margins"][step] > TIE_TOL:
+            assert g == r, (step, g, r)
+        else:
+            assert g in hf_tie_set(fx, step), (step, g)
+        exact += g == r
+    print(f"config 5 teacher-forced: {exact}/{len(hf_ids)} ids identical to HF")
