@@ -57,9 +57,15 @@
 
 #include "../../include/megaqwen_amd.h"
 
-// Instrumentation hook (per-stage timestamps); compiles to nothing by default.
-#ifndef MQ_TRACE
-#define MQ_TRACE(i) ((void)0)
+// Instrumentation hooks: MQ_STAMP(slot) marks a point of a layer's timeline
+// (slot = layer * 40 + event; stream events 0..9, poll 12..24, reduce 28..32,
+// store 34..38), MQ_STAMP_DUMP() runs once at the end of the kernel. Both compile
+// to nothing unless a tracing build defines them before including this file.
+#ifndef MQ_STAMP
+#define MQ_STAMP(i) ((void)0)
+#endif
+#ifndef MQ_STAMP_DUMP
+#define MQ_STAMP_DUMP() ((void)0)
 #endif
 
 namespace mq {
@@ -76,9 +82,9 @@ constexpr int XUNITS = I / NXCD;              // MLP units per XCD: 384
 constexpr int KV_CAP = 256;                       // positions per LDS pass of an attention workgroup
 constexpr int MAX_CTX = 2 * WG_PER_XCD * KV_CAP;  // 16384: at most two passes per workgroup
 constexpr int LM_PRE = 4;                     // LM-head rows each stream wave loads during the last layer
-// A layer's K/V copy is issued just before the previous layer's down_proj weights;
-// the next layer's q/k/v (8) and o_proj (4) loads follow it before attention.
-constexpr int S_LOADS_AFTER_KV = 12;
+// Attention workgroups issue a layer's K/V copy in the previous layer's gate/up stage;
+// only the layer's o_proj loads (4) follow it before attention.
+constexpr int S_LOADS_AFTER_KV = 4;
 
 // Workspace layout, in 32-bit words.
 constexpr uint32_t WS_EPOCH = 0;
@@ -462,10 +468,18 @@ __device__ __forceinline__ float gather_local(const Buf& b, uint32_t* ws, uint32
                                               u32x4 (&v)[4]) {
 #pragma unroll
   for (int k = 0; k < 4; k++) v[k] = ldl4(b, base + 4 * (lane + 64 * k));
+  // re-poll every stale chunk at once (one memory round trip per iteration)
+  uint32_t spins = 0;
+  while (!(tags_ok(v[0], tag) & tags_ok(v[1], tag) & tags_ok(v[2], tag) & tags_ok(v[3], tag))) {
+    if (watchdog(b, ws, ++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (!tags_ok(v[k], tag)) v[k] = ldl4(b, base + 4 * (lane + 64 * k));
+  }
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    v[k] = repoll_l4(b, ws, base + 4 * (lane + 64 * k), tag, v[k]);
     float f[4];
     unpack_tagged(v[k], f);
     ss += (f[0] * f[0] + f[1] * f[1]) + (f[2] * f[2] + f[3] * f[3]);
@@ -613,6 +627,13 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       for (int i = 0; i < 8; i++) R.d[i] = ldw(pd + (lmr ? 8 * (lane + 64 * i) : (size_t)i * I));
     };
 
+    auto burst = [&](int l) {
+      load_o(l);
+      load_gu(l);
+      load_d(l);
+      load_a(l + 1);
+    };
+
     // ---- prologue: layer-0 norms to LDS, layer-0 K/V copy, layer-0 weights in flight
     {
       const u32x2 ln0 = ldw2(wp(0, W_IN) + 4 * st);
@@ -631,12 +652,14 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     }
     if (att) kv_dma(P, 0, g, c0, nc0, p, lds_kv, s, lane);
     load_a(0);
+    if (att) load_o(0);
     BAR();  // P0
 
     for (int layer = 0; layer < L; layer++) {
       const int nl = layer + 1;
       // ---------------- q/k/v rows 16j + 4s .. +3 of the group's [q0; q1; k; v]
       BAR();  // A1: normed h in s_x0
+      MQ_STAMP(layer * 40 + 0);
       {
         if (layer > 0) {
           s_wpost[2 * st] = R.wpost.x;  // this layer's post-attention norm
@@ -652,7 +675,14 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           signal_store(&s_cnt);
         }
         AFTER(r[0] + r[1] + r[2] + r[3]);
-        load_o(layer);
+        MQ_STAMP(layer * 40 + 1);
+        // Workgroups without attention load the rest of the layer's weights and the next
+        // layer's q/k/v in one burst: it drains while attention runs elsewhere, so the
+        // exchanges after attention find this CU's vector-memory pipeline idle (a poll queued
+        // behind in-flight HBM loads waits for them). Attention workgroups poll q/k/v right
+        // after this stage: they load o_proj at the end of the previous layer and the rest
+        // once attention is done.
+        if (!att) burst(layer);
       }
       if (att) {
         // this wave's K/V copy of the layer has landed (S_LOADS_AFTER_KV loads followed it)
@@ -665,6 +695,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           }
           const int ncp = ps ? nc - KV_CAP : nc0;
           BAR();  // B1: q, the new k/v row and the K/V rows are in LDS
+          MQ_STAMP(layer * 40 + 2);
           attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
           BAR();  // B2
           float M0, M1, L0, L1;
@@ -672,11 +703,16 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           BAR();  // B3
           attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
           BAR();  // B4: K/V rows consumed
+          MQ_STAMP(layer * 40 + 3);
         }
+        load_gu(layer);
+        load_d(layer);
+        load_a(nl);
         if (combine) BAR();  // B5
       }
       // ---------------- o_proj partials: rows 32j + 8s + 2i + rg over the group's 256 columns
       BAR();  // C1: attention output of the group in s_x1
+      MQ_STAMP(layer * 40 + 4);
       {
         const u32x4 xa = x1v[oc];
         float r[4];
@@ -691,10 +727,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           signal_store(&s_cnt);
         }
         AFTER(r[0] + r[1] + r[2] + r[3]);
-        load_gu(layer);
+        MQ_STAMP(layer * 40 + 5);
       }
       // ---------------- gate/up rows of units 384g + 12j + 3s .. +2
       BAR();  // D1: normed h1 in s_x0
+      MQ_STAMP(layer * 40 + 6);
       {
         s_wln[2 * st] = R.wln.x;  // the next layer's input norm and q/k norms
         s_wln[2 * st + 1] = R.wln.y;
@@ -710,13 +747,14 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           signal_store(&s_cnt);
         }
         AFTER(r[0] + r[1] + r[2] + r[3] + r[4] + r[5]);
-        load_d(layer);
+        MQ_STAMP(layer * 40 + 7);
         // the next layer's K/V rows: the LDS copy is free since B4, and its completion is
         // first needed behind the next layer's q/k/v weights
         if (att && nl < L) kv_dma(P, nl, g, c0, nc0, p, lds_kv, s, lane);
       }
       // ---------------- down_proj partials: rows 32j + 8s + i over the XCD's 384 units
       BAR();  // E1: m of the XCD in s_x1
+      MQ_STAMP(layer * 40 + 8);
       {
         const u32x4 xm = lane < 48 ? x1v[lane] : u32x4{0u, 0u, 0u, 0u};
         float r[8];
@@ -728,7 +766,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           signal_store(&s_cnt);
         }
         AFTER(r[0] + r[1] + r[2] + r[3] + r[4] + r[5] + r[6] + r[7]);
-        load_a(nl);
+        MQ_STAMP(layer * 40 + 9);
+        if (att && nl < L) load_o(nl);
       }
     }
     BAR();  // F1: final normed h in s_x0
@@ -776,7 +815,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     for (int layer = 0; layer < L; layer++) {
       const uint32_t tag = tag_of(epoch, layer);
       const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
-      MQ_TRACE(1 + layer * 16);
+      MQ_STAMP(layer * 40 + 12);
       // ---------------- gather h (every poll wave reads all 1024 words), RMSNorm
       float ss;
       if (layer == 0) {
@@ -795,11 +834,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       } else {
         ss = gather_local(wsb, ws, lb + LX_H, tag_of(epoch, layer - 1), lane, hv);
       }
-      MQ_TRACE(2 + layer * 16);
+      MQ_STAMP(layer * 40 + 13);
       norm_out(hv, ss, s_wln);
       keep_rows(hv, s_hrow);
       BAR();  // A1
-      MQ_TRACE(3 + layer * 16);
+      MQ_STAMP(layer * 40 + 14);
       if (att) {
         // ---------------- QK-norm, RoPE, K/V row p, attention
         // wave 0: q heads 2g and 2g+1; wave 1: k and v; lane holds dims lane, lane + 64
@@ -807,9 +846,17 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         const uint32_t wq = lb + LX_QKV + 2 * HD * c;
 #pragma unroll
         for (int q = 0; q < 4; q++) u[q] = ldl1(wsb, wq + 64 * q + lane);
+        {
+          uint32_t spins = 0;
+          while (((u[0] >> 16) != tag) | ((u[1] >> 16) != tag) | ((u[2] >> 16) != tag) | ((u[3] >> 16) != tag)) {
+            if (watchdog(wsb, ws, ++spins)) break;
+            __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-        for (int q = 0; q < 4; q++) u[q] = repoll_l1(wsb, ws, wq + 64 * q + lane, tag, u[q]);
-        MQ_TRACE(4 + layer * 16);
+            for (int q = 0; q < 4; q++)
+              if ((u[q] >> 16) != tag) u[q] = ldl1(wsb, wq + 64 * q + lane);
+          }
+        }
+        MQ_STAMP(layer * 40 + 15);
         // HF: q_norm/k_norm over 128 (modeling_qwen3.py:252-253), then apply_rotary_pos_emb (:147-170)
         const int nseg = c == 0 ? 2 : 1;  // segments that get QK-norm and RoPE
         float fr[2][2];
@@ -854,6 +901,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           }
           const int ncp = ps ? nc - KV_CAP : nc0;
           BAR();  // B1
+          MQ_STAMP(layer * 40 + 16);
           attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
           BAR();  // B2
           float M0, M1, L0, L1;
@@ -862,7 +910,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
           BAR();  // B4
         }
-        MQ_TRACE(5 + layer * 16);
+        MQ_STAMP(layer * 40 + 17);
         if (combine) {
           // outputs (hh, dim) = pt, pt + 128: merge the chunk partials of the XCD's workgroups
 #pragma unroll 1
@@ -898,6 +946,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             s_sc[hh][dim] = Oc * (1.0f / Lc);
           }
           BAR();  // B5
+          MQ_STAMP(layer * 40 + 18);
         }
       }
       // ---------------- o_proj input: the group's 256 attention outputs (poll wave 0)
@@ -906,17 +955,17 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         v = repoll_l4(wsb, ws, lb + LX_ATT + 4 * lane, tag, v);
         reinterpret_cast<u32x2*>(s_x1)[lane] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
       }
-      MQ_TRACE(6 + layer * 16);
+      MQ_STAMP(layer * 40 + 19);
       BAR();  // C1
-      MQ_TRACE(7 + layer * 16);
+      MQ_STAMP(layer * 40 + 20);
       // ---------------- gather h1; post-attention RMSNorm
       {
         const float ss1 = gather_local(wsb, ws, lb + LX_H1, tag, lane, hv);
-        MQ_TRACE(8 + layer * 16);
+        MQ_STAMP(layer * 40 + 21);
         norm_out(hv, ss1, s_wpost);
       }
       BAR();  // D1
-      MQ_TRACE(9 + layer * 16);
+      MQ_STAMP(layer * 40 + 22);
       // ---------------- down_proj input: m of the XCD's 384 units (96 chunks)
       {
         const int q = pt;  // chunks pt, pt + 128 (< 96 only for pt < 96)
@@ -926,15 +975,15 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           reinterpret_cast<u32x2*>(s_x1)[q] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
         }
       }
-      MQ_TRACE(10 + layer * 16);
+      MQ_STAMP(layer * 40 + 23);
       BAR();  // E1
-      MQ_TRACE(11 + layer * 16);
+      MQ_STAMP(layer * 40 + 24);
     }
 
     // ---------------- final norm
     {
       const float ss = gather_local(wsb, ws, lb + LX_H, tag_of(epoch, L - 1), lane, hv);
-      MQ_TRACE(1000);
+      MQ_STAMP(32 * 40);
       if (lm) norm_out(hv, ss, s_wfn);
       if (w == 0) {
         // hidden_out / normed_out chunks k = 2c, 2c + 1
@@ -974,6 +1023,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       const uint32_t tag = tag_of(epoch, layer);
       const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
       BAR();  // A1: h rows in s_hrow
+      MQ_STAMP(layer * 40 + 28);
       const float hrow = s_hrow[rr];
       if (att) {
         for (int ps = 0; ps < npass; ps++) {
@@ -990,14 +1040,18 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         if (combine) BAR();  // B5
       }
       BAR();  // C1
+      MQ_STAMP(layer * 40 + 29);
       // h1 = bf16(h + bf16(o)) (modeling_qwen3.py:297-298)
       h1v = rbf(hrow + rbf(reduce_row(X_OPART, tag64)));
       if (hx == 0) st1_plain(ws + lb + LX_H1 + ROWS * j + rr, tagged(tag, h1v));
+      MQ_STAMP(layer * 40 + 30);
       BAR();  // D1
       BAR();  // E1
+      MQ_STAMP(layer * 40 + 31);
       // h' = bf16(h1 + bf16(down)) (modeling_qwen3.py:303-304)
       const float hn = rbf(h1v + rbf(reduce_row(X_DPART, tag64)));
       if (hx == 0) st1_plain(ws + lb + LX_H + ROWS * j + rr, tagged(tag, hn));
+      MQ_STAMP(layer * 40 + 32);
     }
     BAR();  // F1
   } else {
@@ -1013,6 +1067,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       target += NSW;
       wait_count(&s_cnt, target);
       if (lane < 16) st1_plain(ws + lb + LX_QKV + 16 * j + lane, tagged(tag, rbf(s_res[lane])));
+      MQ_STAMP(layer * 40 + 34);
       if (att) {
         float M0 = 0.f, M1 = 0.f, L0 = 0.f, L1 = 0.f, Ma0 = 0.f, Ma1 = 0.f, La0 = 0.f, La1 = 0.f;
         for (int ps = 0; ps < npass; ps++) {
@@ -1082,12 +1137,14 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           }
         }
       }
+      MQ_STAMP(layer * 40 + 35);
       // o_proj partials of rows 32j .. 32j+31 over this XCD's two heads
       BAR();  // C1
       target += NSW;
       wait_count(&s_cnt, target);
       if (lane < ROWS)
         st2_dev(ws + X_OPART + 2 * ((j * ROWS + lane) * NXCD + g), u32x2{__float_as_uint(s_res[lane]), tag64});
+        MQ_STAMP(layer * 40 + 36);
       // HF Qwen3MLP (modeling_qwen3.py:81-83): m = bf16(bf16(silu(gate)) * up)
       BAR();  // D1
       target += NSW;
@@ -1097,12 +1154,14 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         const float gt = rbf(s_res[6 * sw + u]), up = rbf(s_res[6 * sw + 3 + u]);
         st1_plain(ws + lb + LX_M + UNITS * j + lane, tagged(tag, rbf(rbf(gt / (1.0f + expf(-gt))) * up)));
       }
+      MQ_STAMP(layer * 40 + 37);
       // down_proj partials of rows 32j .. 32j+31 over this XCD's 384 units
       BAR();  // E1
       target += NSW;
       wait_count(&s_cnt, target);
       if (lane < ROWS)
         st2_dev(ws + X_DPART + 2 * ((j * ROWS + lane) * NXCD + g), u32x2{__float_as_uint(s_res[lane]), tag64});
+        MQ_STAMP(layer * 40 + 38);
     }
     BAR();  // F1
   }
@@ -1144,6 +1203,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     }
   }
   BAR();  // F2
+  MQ_STAMP_DUMP();
   if (lm) {
     if (tid == 0) {
       for (int v = 1; v < 8; v++) {
