@@ -949,11 +949,19 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           MQ_STAMP(layer * 40 + 18);
         }
       }
-      // ---------------- o_proj input: the group's 256 attention outputs (poll wave 0)
+      // ---------------- o_proj input: the group's 256 attention outputs (poll wave 0); the
+      // workgroup that finished them (one chunk, or the combining workgroup) has them in LDS
       if (c == 0) {
-        u32x4 v = ldl4(wsb, lb + LX_ATT + 4 * lane);
-        v = repoll_l4(wsb, ws, lb + LX_ATT + 4 * lane, tag, v);
-        reinterpret_cast<u32x2*>(s_x1)[lane] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
+        if (att && (nsplit == 1 || combine)) {
+          const int hh = lane >> 5, dim = 4 * (lane & 31);
+          const float* src = nsplit == 1 ? &s_ao[hh][dim] : &s_sc[hh][dim];
+          reinterpret_cast<u32x2*>(s_x1)[lane] =
+              u32x2{pack_bf2(rbf(src[0]), rbf(src[1])), pack_bf2(rbf(src[2]), rbf(src[3]))};
+        } else {
+          u32x4 v = ldl4(wsb, lb + LX_ATT + 4 * lane);
+          v = repoll_l4(wsb, ws, lb + LX_ATT + 4 * lane, tag, v);
+          reinterpret_cast<u32x2*>(s_x1)[lane] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
+        }
       }
       MQ_STAMP(layer * 40 + 19);
       BAR();  // C1
