@@ -706,8 +706,6 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           MQ_STAMP(layer * 40 + 3);
         }
         load_gu(layer);
-        load_d(layer);
-        load_a(nl);
         if (combine) BAR();  // B5
       }
       // ---------------- o_proj partials: rows 32j + 8s + 2i + rg over the group's 256 columns
@@ -728,6 +726,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         }
         AFTER(r[0] + r[1] + r[2] + r[3]);
         MQ_STAMP(layer * 40 + 5);
+        if (att) load_d(layer);
       }
       // ---------------- gate/up rows of units 384g + 12j + 3s .. +2
       BAR();  // D1: normed h1 in s_x0
@@ -748,6 +747,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         }
         AFTER(r[0] + r[1] + r[2] + r[3] + r[4] + r[5]);
         MQ_STAMP(layer * 40 + 7);
+        if (att) load_a(nl);
         // the next layer's K/V rows: the LDS copy is free since B4, and its completion is
         // first needed behind the next layer's q/k/v weights
         if (att && nl < L) kv_dma(P, nl, g, c0, nc0, p, lds_kv, s, lane);
