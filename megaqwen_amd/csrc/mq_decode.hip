@@ -1022,8 +1022,15 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     auto reduce_row = [&](uint32_t part, uint32_t tag64) -> float {
       const uint32_t wd = part + 2 * ((j * ROWS + rr) * NXCD + 4 * hx);
       u32x4 a = xld4(wsb, wd), b = xld4(wsb, wd + 4);
-      a = xrepoll64x2(wsb, ws, wd, tag64, a);
-      b = xrepoll64x2(wsb, ws, wd + 4, tag64, b);
+      // re-poll both stale halves at once (one round trip per iteration)
+      uint32_t spins = 0;
+      auto ok = [&](const u32x4& v) { return (v.y == tag64) & (v.w == tag64); };
+      while (!(ok(a) & ok(b))) {
+        if (watchdog(wsb, ws, ++spins)) break;
+        __builtin_amdgcn_s_sleep(1);
+        if (!ok(a)) a = xld4(wsb, wd);
+        if (!ok(b)) b = xld4(wsb, wd + 4);
+      }
       const float s4 = (__uint_as_float(a.x) + __uint_as_float(a.z)) + (__uint_as_float(b.x) + __uint_as_float(b.z));
       return s4 + dpp<0xB1>(s4);  // (XCDs 0..3) + (XCDs 4..7), commutative: same bits in both lanes
     };
