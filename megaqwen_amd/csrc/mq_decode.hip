@@ -393,26 +393,33 @@ __device__ __forceinline__ void attn_softmax(const float (*s_sc)[KV_CAP], uint16
 }
 
 // acc[h][d] = sum_r bf16(p_h[r]) * v_r[d] for this wave's 16 dims d = 16v + (lane & 15)
-// over the 32-row blocks that hold rows < nc; the rows past nc are zero in both
-// operands. Writes acc / l (fin) or the raw acc (a split-K partial) to s_ao and
-// returns the per-head sums l.
+// over the 32-row blocks that hold rows < nc (rows past nc have p = 0 and finite V).
+// The MFMA operand (8 rows of one dim per lane) comes from two LDS transpose reads:
+// within each 16-lane group, lane j addresses row base + j / 4, dims 4 (j % 4) .. +3 of
+// the wave's 16, and lane i receives that column's 4 rows (ds_read_b64_tr_b16).
+// Writes acc / l (fin) or the raw acc (a split-K partial) to s_ao and returns the
+// per-head sums l.
 __device__ __forceinline__ void attn_pv(const uint8_t* s_kv, const uint16_t* s_p, const float (*s_l)[2],
                                         float (*s_ao)[HD], int nc, int v, int lane, bool fin, float& L0, float& L1) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
   const int r16 = lane & 15, kg = lane >> 4;
-  const int dim = 16 * v + r16, ch = dim >> 3, within = 2 * (dim & 7);
-  const uint8_t* vbase = s_kv + KV_CAP * 256;
+  const int dim = 16 * v + r16;
+  const int dq = 16 * v + 4 * (r16 & 3);                // this lane's 4 dims in the transpose reads
+  const uint32_t vb0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(s_kv + KV_CAP * 256);
   const int nb = (nc + 31) >> 5;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int t = 0; t < nb; t++) {
     const int rr = 32 * t + 8 * kg;
     const u32x4 pt = *reinterpret_cast<const u32x4*>(s_p + (r16 & 1) * KV_CAP + rr);
     const u32x4 pa = r16 < 2 ? pt : u32x4{0u, 0u, 0u, 0u};
-    uint32_t h16[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) h16[e] = *reinterpret_cast<const uint16_t*>(vbase + kv_off(rr + e, ch) + within);
-    const u32x4 vb = {h16[0] | (h16[1] << 16), h16[2] | (h16[3] << 16), h16[4] | (h16[5] << 16),
-                      h16[6] | (h16[7] << 16)};
-    acc = mfma_16x16x32(pa, vb, acc);
+    const int ra = rr + (r16 >> 2), rb = ra + 4;
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4s*)(uintptr_t)(vb0 + kv_off(ra, dq >> 3) + 2 * (dq & 7)));
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4s*)(uintptr_t)(vb0 + kv_off(rb, dq >> 3) + 2 * (dq & 7)));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+    acc = mfma_16x16x32(pa, u32x4{l2.x, l2.y, h2.x, h2.y}, acc);
   }
   L0 = 0.f;
   L1 = 0.f;
@@ -698,9 +705,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           MQ_STAMP(layer * 40 + 2);
           attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
           BAR();  // B2
+          MQ_STAMP(layer * 40 + 10);
           float M0, M1, L0, L1;
           attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
           BAR();  // B3
+          MQ_STAMP(layer * 40 + 11);
           attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
           BAR();  // B4: K/V rows consumed
           MQ_STAMP(layer * 40 + 3);
@@ -886,6 +895,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             s_q[sg * HD + 64 + lane] = (uint16_t)f2bf(fr[sg][1]);
           }
         }
+        MQ_STAMP(layer * 40 + 25);
         for (int ps = 0; ps < npass; ps++) {
           if (c == 1 && own_p && ps == npass - 1) {
             // the new k and v rows into the LDS copy of the pass that holds position p (the
