@@ -108,6 +108,34 @@ __device__ __forceinline__ float wave_sum(float v) {
   v = row16_sum(v);
   return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
 }
+// wave_sum of N independent values, step by step across the values so that the DPP and
+// readlane latencies of one overlap the others (same operations and order as wave_sum,
+// so the results are bitwise identical).
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0xB1>(v[k]);
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0x4E>(v[k]);
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0x141>(v[k]);
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0x140>(v[k]);
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] = (readlane(v[k], 0) + readlane(v[k], 16)) + (readlane(v[k], 32) + readlane(v[k], 48));
+}
+// row16_sum of N independent values, interleaved the same way
+template <int N>
+__device__ __forceinline__ void row16_sum_n(float (&v)[N]) {
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0xB1>(v[k]);
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0x4E>(v[k]);
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0x141>(v[k]);
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0x140>(v[k]);
+}
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<0xB1>(v));
   v = fmaxf(v, dpp<0x4E>(v));

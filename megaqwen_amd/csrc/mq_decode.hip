@@ -675,7 +675,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
         float r[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) r[k] = wave_sum(dot_chunk(R.a[2 * k], x0, dot_chunk(R.a[2 * k + 1], x1, 0.f)));
+        for (int k = 0; k < 4; k++) r[k] = dot_chunk(R.a[2 * k], x0, dot_chunk(R.a[2 * k + 1], x1, 0.f));
+        wave_sum_n(r);
         if (lane == 0) {
 #pragma unroll
           for (int k = 0; k < 4; k++) s_res[4 * s + k] = r[k];
@@ -724,7 +725,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         const u32x4 xa = x1v[oc];
         float r[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) r[i] = row16_sum(dot_chunk(R.o[i], xa, 0.f));
+        for (int i = 0; i < 4; i++) r[i] = dot_chunk(R.o[i], xa, 0.f);
+        row16_sum_n(r);
         if (lane == 0) {
 #pragma unroll
           for (int i = 0; i < 4; i++) {
@@ -747,8 +749,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
         float r[6];
 #pragma unroll
-        for (int k = 0; k < 6; k++)
-          r[k] = wave_sum(dot_chunk(R.gu[2 * k], x0, dot_chunk(R.gu[2 * k + 1], x1, 0.f)));
+        for (int k = 0; k < 6; k++) r[k] = dot_chunk(R.gu[2 * k], x0, dot_chunk(R.gu[2 * k + 1], x1, 0.f));
+        wave_sum_n(r);
         if (lane == 0) {
 #pragma unroll
           for (int k = 0; k < 6; k++) s_res[6 * s + k] = r[k];
@@ -768,7 +770,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         const u32x4 xm = lane < 48 ? x1v[lane] : u32x4{0u, 0u, 0u, 0u};
         float r[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) r[i] = wave_sum(dot_chunk(R.d[i], xm, 0.f));
+        for (int i = 0; i < 8; i++) r[i] = dot_chunk(R.d[i], xm, 0.f);
+        wave_sum_n(r);
         if (lane == 0) {
 #pragma unroll
           for (int i = 0; i < 8; i++) s_res[8 * s + i] = r[i];
@@ -845,6 +848,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       }
       MQ_STAMP(layer * 40 + 13);
       norm_out(hv, ss, s_wln);
+      MQ_STAMP(layer * 40 + 26);
       keep_rows(hv, s_hrow);
       BAR();  // A1
       MQ_STAMP(layer * 40 + 14);
@@ -981,6 +985,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         const float ss1 = gather_local(wsb, ws, lb + LX_H1, tag, lane, hv);
         MQ_STAMP(layer * 40 + 21);
         norm_out(hv, ss1, s_wpost);
+        MQ_STAMP(layer * 40 + 27);
       }
       BAR();  // D1
       MQ_STAMP(layer * 40 + 22);
@@ -1192,6 +1197,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   }
 
   // ==================================================================== LM head (all waves)
+  MQ_STAMP(32 * 40 + 1);
   if (lm) {
     const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
     // rows r0 + NSW * LM_PRE + wave + 8i: four rows per batch, two batches in flight
@@ -1227,7 +1233,9 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       s_besti[wave] = besti;
     }
   }
+  MQ_STAMP(32 * 40 + 2);
   BAR();  // F2
+  MQ_STAMP(32 * 40 + 3);
   MQ_STAMP_DUMP();
   if (lm) {
     if (tid == 0) {
