@@ -1212,11 +1212,24 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         }
       }
     };
+    // bf16 logits of the batch's rows (the four reductions interleaved), best kept with the
+    // lowest index on ties (rows are visited in increasing order within a wave)
     auto score_rows = [&](int rb, const u32x4 (&Wr)[4][2]) {
+      float d[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) d[u] = dot_chunk(Wr[u][0], x0, dot_chunk(Wr[u][1], x1, 0.f));
+      wave_sum_n(d);
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int r = rb + 8 * u;
-        if (r < r1) lm_score(r, r0, Wr[u][0], Wr[u][1], x0, x1, s_lg, lane, bestv, besti);
+        if (r < r1) {
+          const float v = rbf(d[u]);
+          if (lane == 0) s_lg[r - r0] = v;
+          if (v > bestv) {
+            bestv = v;
+            besti = r;
+          }
+        }
       }
     };
     u32x4 WA[4][2], WB[4][2];
