@@ -339,26 +339,31 @@ __device__ __forceinline__ void attn_scores(const uint8_t* s_kv, const uint16_t*
     const u32x4 t = *reinterpret_cast<const u32x4*>(s_q + (r16 & 1) * HD + 32 * s4 + 8 * kg);
     qb[s4] = r16 < 2 ? t : u32x4{0u, 0u, 0u, 0u};
   }
-  const int nb = (nc + 15) >> 4;
+  // blocks v and v + 8 together (rows < 256 always lie in the LDS copy; rows at or past nc
+  // are masked): both blocks' K operands are read before the two MFMA chains run
   float mx = -INFINITY;
-#pragma unroll 1
-  for (int b = v; b < nb; b += 8) {
-    const int row = 16 * b + r16;
-    u32x4 ka[4];
+  u32x4 ka[2][4];
 #pragma unroll
-    for (int s4 = 0; s4 < 4; s4++) ka[s4] = *reinterpret_cast<const u32x4*>(s_kv + kv_off(row, 4 * s4 + kg));
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int bi = 0; bi < 2; bi++)
 #pragma unroll
-    for (int s4 = 0; s4 < 4; s4++) acc = mfma_16x16x32(ka[s4], qb[s4], acc);
-    // lane (column r16 = head, rows 4kg + e)
+    for (int s4 = 0; s4 < 4; s4++)
+      ka[bi][s4] = *reinterpret_cast<const u32x4*>(s_kv + kv_off(16 * (v + 8 * bi) + r16, 4 * s4 + kg));
+  f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int s4 = 0; s4 < 4; s4++) {
+    acc[0] = mfma_16x16x32(ka[0][s4], qb[s4], acc[0]);
+    acc[1] = mfma_16x16x32(ka[1][s4], qb[s4], acc[1]);
+  }
+  // lane (column r16 = head, rows 4kg + e)
+#pragma unroll
+  for (int bi = 0; bi < 2; bi++)
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      const int r = 16 * b + 4 * kg + e;
-      const float val = r < nc ? acc[e] * scale : -INFINITY;
+      const int r = 16 * (v + 8 * bi) + 4 * kg + e;
+      const float val = r < nc ? acc[bi][e] * scale : -INFINITY;
       if (r16 < 2) s_sc[r16][r] = val;
       mx = fmaxf(mx, val);
     }
-  }
   // per-head maximum over the lanes of column 0 (head 0) and column 1 (head 1)
   const float m0 = fmaxf(fmaxf(readlane(mx, 0), readlane(mx, 16)), fmaxf(readlane(mx, 32), readlane(mx, 48)));
   const float m1 = fmaxf(fmaxf(readlane(mx, 1), readlane(mx, 17)), fmaxf(readlane(mx, 33), readlane(mx, 49)));
@@ -407,20 +412,29 @@ __device__ __forceinline__ void attn_pv(const uint8_t* s_kv, const uint16_t* s_p
   const int dim = 16 * v + r16;
   const int dq = 16 * v + 4 * (r16 & 3);                // this lane's 4 dims in the transpose reads
   const uint32_t vb0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(s_kv + KV_CAP * 256);
+  // 32-row blocks in pairs with two accumulators (a block past nc has p = 0: rows < 256
+  // always lie in the LDS copy and hold finite values)
   const int nb = (nc + 31) >> 5;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int t = 0; t < nb; t++) {
-    const int rr = 32 * t + 8 * kg;
-    const u32x4 pt = *reinterpret_cast<const u32x4*>(s_p + (r16 & 1) * KV_CAP + rr);
-    const u32x4 pa = r16 < 2 ? pt : u32x4{0u, 0u, 0u, 0u};
-    const int ra = rr + (r16 >> 2), rb = ra + 4;
-    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_v4s*)(uintptr_t)(vb0 + kv_off(ra, dq >> 3) + 2 * (dq & 7)));
-    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_v4s*)(uintptr_t)(vb0 + kv_off(rb, dq >> 3) + 2 * (dq & 7)));
-    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-    acc = mfma_16x16x32(pa, u32x4{l2.x, l2.y, h2.x, h2.y}, acc);
+  f32x4 acc2[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  for (int t0 = 0; t0 < nb; t0 += 2) {
+    u32x4 pa[2], vb[2];
+#pragma unroll
+    for (int bi = 0; bi < 2; bi++) {
+      const int rr = 32 * (t0 + bi) + 8 * kg;
+      const u32x4 pt = *reinterpret_cast<const u32x4*>(s_p + (r16 & 1) * KV_CAP + rr);
+      pa[bi] = r16 < 2 ? pt : u32x4{0u, 0u, 0u, 0u};
+      const int ra = rr + (r16 >> 2), rb = ra + 4;
+      const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_v4s*)(uintptr_t)(vb0 + kv_off(ra, dq >> 3) + 2 * (dq & 7)));
+      const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_v4s*)(uintptr_t)(vb0 + kv_off(rb, dq >> 3) + 2 * (dq & 7)));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      vb[bi] = u32x4{l2.x, l2.y, h2.x, h2.y};
+    }
+    acc2[0] = mfma_16x16x32(pa[0], vb[0], acc2[0]);
+    acc2[1] = mfma_16x16x32(pa[1], vb[1], acc2[1]);
   }
+  const f32x4 acc = acc2[0] + acc2[1];
   L0 = 0.f;
   L1 = 0.f;
 #pragma unroll
