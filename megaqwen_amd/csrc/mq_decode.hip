@@ -52,6 +52,7 @@
 #include "mq_common.h"
 
 #include <math.h>
+#include <atomic>
 #include <mutex>
 #include <string.h>
 
@@ -87,7 +88,7 @@ constexpr int LM_PRE = 4;                     // LM-head rows each stream wave l
 constexpr int S_LOADS_AFTER_KV = 4;
 
 // Workspace layout, in 32-bit words.
-constexpr uint32_t WS_EPOCH = 0;
+constexpr uint32_t WS_RESERVED = 0;  // (words 0..31 unused)
 constexpr uint32_t WS_ERR = 32;
 constexpr uint32_t WS_FINAL_TICKET = 64;
 // word WS_PREFILL_ERR (96) belongs to the prefill kernels
@@ -138,6 +139,7 @@ struct DecodeParams {
   int max_seq_len;
   float attn_scale;
   int mode;
+  uint32_t epoch;  // launch counter of the device (the host's): tags of this launch's exchanges
 };
 
 // Workgroup barrier without a memory fence: LDS writes are complete once
@@ -545,7 +547,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   const int w = blockIdx.x, g = w & (NXCD - 1), j = w / NXCD;
   uint32_t* ws = P.ws;
   const Buf wsb(ws);
-  const uint32_t epoch = wsb.ld1(WS_EPOCH * 4u);
+  const uint32_t epoch = P.epoch;
   // The XCD-local exchange (plain stores, L2-coherent loads) assumes that the
   // dispatcher placed workgroup w on XCD w % 8; check it on the hardware.
   if (tid == 0) {
@@ -1326,7 +1328,6 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     *P.out_token = err ? -(int)(1u + err) : tok;
     wsb.st1(0u, WS_ERR * 4u);
     wsb.st1(0u, WS_FINAL_TICKET * 4u);
-    wsb.st1(epoch + 1u, WS_EPOCH * 4u);
   }
 }
 
@@ -1335,6 +1336,10 @@ struct DeviceState {
   bool init = false;
   int status = MQ_OK;
   uint32_t* ws = nullptr;
+  // Launches on the device so far. The epoch comes from the host rather than from the
+  // workspace: an ordinary launch may start its first workgroups on CUs that the previous
+  // launch has already released while that launch's last workgroup is still finishing.
+  std::atomic<uint32_t> launches{0};
 };
 static std::mutex g_mu;
 static DeviceState g_dev[64];
@@ -1367,6 +1372,7 @@ static int launch(DecodeParams& P, hipStream_t stream) {
   const int st = ensure_device(dev);
   if (st != MQ_OK) return st;
   P.ws = g_dev[dev].ws;
+  P.epoch = g_dev[dev].launches.fetch_add(1u, std::memory_order_relaxed) + 1u;
   if (!P.out_token) P.out_token = reinterpret_cast<int*>(g_dev[dev].ws + WS_WORDS);
   // All NWG workgroups must be resident at once. Each one needs a whole CU
   // (its LDS use exceeds half a CU's), ensure_device() checked that the GPU has
