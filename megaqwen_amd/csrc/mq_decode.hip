@@ -518,6 +518,10 @@ __device__ __forceinline__ void norm_chunk(const float* x, float rstd, uint32_t 
 }
 
 // ---------------------------------------------------------------- the kernel
+// SPLIT = false is the instance for contexts of at most KV_CAP positions (one
+// attention workgroup per XCD, one LDS pass): the chunk-merge and two-pass code
+// is compiled out of it. SPLIT = true handles every context length.
+template <bool SPLIT>
 __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ __align__(16) uint8_t s_kv[2 * KV_CAP * HD * 2];  // K rows, then V rows of the chunk
   __shared__ __align__(16) uint32_t s_x0[H / 2];               // normed h or h1 (bf16 pairs)
@@ -529,7 +533,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ float s_cos[HD], s_sin[HD];
   __shared__ __align__(16) uint16_t s_q[2 * HD];      // normed, rotated q of the two heads
   __shared__ __align__(16) uint16_t s_p[2 * KV_CAP];  // bf16 softmax numerators
-  __shared__ float s_sc[2][KV_CAP];                    // attention scores, later the combined output
+  __shared__ float s_sc[2][KV_CAP];                    // attention scores
   __shared__ float s_ao[2][HD];                        // attention output (or unnormalised partial)
   __shared__ float s_ao1[2][HD];                       // second LDS pass's unnormalised partial
   __shared__ float s_mx[8][2], s_l[8][2];              // per-wave score maxima and softmax sums
@@ -562,16 +566,15 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   // attention chunking: nsplit chunks of <= 2 KV_CAP positions, chunk j on workgroup (g, j),
   // attended in npass LDS passes of <= KV_CAP positions (rows KV_CAP.. in the second)
   const int p = P.position, n_ctx = p + 1;
-  const int nsplit = min(WG_PER_XCD, (n_ctx + KV_CAP - 1) / KV_CAP);
+  const int nsplit = SPLIT ? min(WG_PER_XCD, (n_ctx + KV_CAP - 1) / KV_CAP) : 1;
   const int CH = (n_ctx + nsplit - 1) / nsplit;
   const bool att = j < nsplit;
   const int c0 = j * CH;
   const int nc = att ? min(n_ctx, c0 + CH) - c0 : 0;
-  const int npass = (nc + KV_CAP - 1) / KV_CAP;
+  const int npass = SPLIT ? (nc + KV_CAP - 1) / KV_CAP : 1;
   const int nc0 = min(nc, KV_CAP);
   const bool own_p = att && p >= c0 && p < c0 + nc;  // p is always in the last pass
   const int prow = p - c0 - KV_CAP * (npass - 1);     // its LDS row there
-  const bool combine = att && nsplit > 1 && j == 0;
   const uint32_t lds_kv = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)s_kv;
 
   // LM-head rows of this workgroup: 594 for w < 128, 593 after (151936 in total)
@@ -732,7 +735,6 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           MQ_STAMP(layer * 40 + 3);
         }
         load_gu(layer);
-        if (combine) BAR();  // B5
       }
       // ---------------- o_proj partials: rows 32j + 8s + 2i + rg over the group's 256 columns
       BAR();  // C1: attention output of the group in s_x1
@@ -941,57 +943,68 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           BAR();  // B4
         }
         MQ_STAMP(layer * 40 + 17);
-        if (combine) {
-          // outputs (hh, dim) = pt, pt + 128: merge the chunk partials of the XCD's workgroups
-#pragma unroll 1
-          for (int o = pt; o < 2 * HD; o += NPW * 64) {
-            const int hh = o >> 7, dim = o & (HD - 1);
-            float Mc = -INFINITY, Lc = 0.f, Oc = 0.f;
-            for (int s0 = 0; s0 < nsplit; s0 += 8) {
-              u32x2 vm[8], vl[8], vo[8];
-#pragma unroll
-              for (int q = 0; q < 8; q++) {
-                const uint32_t b = lb + LX_PART + 2 * (((s0 + q) * 2 + hh) * APART);
-                if (s0 + q < nsplit) {
-                  vm[q] = ldl64(wsb, b);
-                  vl[q] = ldl64(wsb, b + 2);
-                  vo[q] = ldl64(wsb, b + 2 * (2 + dim));
-                }
-              }
-#pragma unroll
-              for (int q = 0; q < 8; q++) {
-                const uint32_t b = lb + LX_PART + 2 * (((s0 + q) * 2 + hh) * APART);
-                if (s0 + q < nsplit) {
-                  const float m = repoll_l64(wsb, ws, b, tag64, vm[q]);
-                  const float l = repoll_l64(wsb, ws, b + 2, tag64, vl[q]);
-                  const float ov = repoll_l64(wsb, ws, b + 2 * (2 + dim), tag64, vo[q]);
-                  const float nm = fmaxf(Mc, m);
-                  const float ea = Mc == -INFINITY ? 0.f : expf(Mc - nm), eb = expf(m - nm);
-                  Lc = Lc * ea + l * eb;
-                  Oc = Oc * ea + ov * eb;
-                  Mc = nm;
-                }
-              }
-            }
-            s_sc[hh][dim] = Oc * (1.0f / Lc);
-          }
-          BAR();  // B5
-          MQ_STAMP(layer * 40 + 18);
-        }
       }
-      // ---------------- o_proj input: the group's 256 attention outputs (poll wave 0); the
-      // workgroup that finished them (one chunk, or the combining workgroup) has them in LDS
-      if (c == 0) {
-        if (att && (nsplit == 1 || combine)) {
-          const int hh = lane >> 5, dim = 4 * (lane & 31);
-          const float* src = nsplit == 1 ? &s_ao[hh][dim] : &s_sc[hh][dim];
-          reinterpret_cast<u32x2*>(s_x1)[lane] =
-              u32x2{pack_bf2(rbf(src[0]), rbf(src[1])), pack_bf2(rbf(src[2]), rbf(src[3]))};
-        } else {
-          u32x4 v = ldl4(wsb, lb + LX_ATT + 4 * lane);
-          v = repoll_l4(wsb, ws, lb + LX_ATT + 4 * lane, tag, v);
-          reinterpret_cast<u32x2*>(s_x1)[lane] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
+      // ---------------- o_proj input: the group's 256 attention outputs as bf16 pairs in s_x1
+      if (nsplit == 1) {
+        // poll wave 0: the attention workgroup has them in LDS, the others gather them
+        if (c == 0) {
+          if (att) {
+            const int hh = lane >> 5, dim = 4 * (lane & 31);
+            const float* src = &s_ao[hh][dim];
+            reinterpret_cast<u32x2*>(s_x1)[lane] =
+                u32x2{pack_bf2(rbf(src[0]), rbf(src[1])), pack_bf2(rbf(src[2]), rbf(src[3]))};
+          } else {
+            u32x4 v = ldl4(wsb, lb + LX_ATT + 4 * lane);
+            v = repoll_l4(wsb, ws, lb + LX_ATT + 4 * lane, tag, v);
+            reinterpret_cast<u32x2*>(s_x1)[lane] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
+          }
         }
+      } else {
+        // every workgroup merges the XCD's chunk partials itself (no second hand-over through
+        // a combining workgroup): thread pt takes dims d0, d0 + 1 of head hh, four chunks per
+        // round; a round issues all its loads, then re-polls the stale ones together
+        const int hh = pt >> 6, d0 = 2 * (pt & 63);
+        float Mc = -INFINITY, Lc = 0.f, O0 = 0.f, O1 = 0.f;
+        constexpr int CG = 4;
+        for (int s0 = 0; s0 < nsplit; s0 += CG) {
+          const int nq = min(CG, nsplit - s0);
+          const uint32_t b0 = lb + LX_PART + 2 * ((s0 * 2 + hh) * APART);
+          u32x4 ml[CG], ov[CG];  // (m, tag, l, tag) and (acc[d0], tag, acc[d0 + 1], tag)
+#pragma unroll
+          for (int q = 0; q < CG; q++)
+            if (q < nq) {
+              ml[q] = ldl4(wsb, b0 + 4 * q * APART);
+              ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
+            }
+          auto fresh = [&](const u32x4& v) { return (v.y == tag64) & (v.w == tag64); };
+          uint32_t spins = 0;
+          for (;;) {
+            bool ok = true;
+#pragma unroll
+            for (int q = 0; q < CG; q++) ok &= q >= nq || (fresh(ml[q]) & fresh(ov[q]));
+            if (ok || watchdog(wsb, ws, ++spins)) break;
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int q = 0; q < CG; q++)
+              if (q < nq) {
+                if (!fresh(ml[q])) ml[q] = ldl4(wsb, b0 + 4 * q * APART);
+                if (!fresh(ov[q])) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
+              }
+          }
+#pragma unroll
+          for (int q = 0; q < CG; q++)
+            if (q < nq) {
+              const float m = __uint_as_float(ml[q].x), l = __uint_as_float(ml[q].z);
+              const float nm = fmaxf(Mc, m);
+              const float ea = Mc == -INFINITY ? 0.f : expf(Mc - nm), eb = expf(m - nm);
+              Lc = Lc * ea + l * eb;
+              O0 = O0 * ea + __uint_as_float(ov[q].x) * eb;
+              O1 = O1 * ea + __uint_as_float(ov[q].z) * eb;
+              Mc = nm;
+            }
+        }
+        const float rl = 1.0f / Lc;
+        s_x1[pt] = pack_bf2(rbf(O0 * rl), rbf(O1 * rl));
       }
       MQ_STAMP(layer * 40 + 19);
       BAR();  // C1
@@ -1083,7 +1096,6 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
           BAR();  // B4
         }
-        if (combine) BAR();  // B5
       }
       BAR();  // C1
       MQ_STAMP(layer * 40 + 29);
@@ -1167,7 +1179,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
                     u32x4{tagged(tag, rbf(s_ao[hh][dim])), tagged(tag, rbf(s_ao[hh][dim + 1])),
                           tagged(tag, rbf(s_ao[hh][dim + 2])), tagged(tag, rbf(s_ao[hh][dim + 3]))});
         } else {
-          // chunk partial (m, l, unnormalised acc) as (fp32, tag) pairs; workgroup (g, 0) combines
+          // chunk partial (m, l, unnormalised acc) as (fp32, tag) pairs; every workgroup of the
+          // XCD merges them
           uint32_t* pb = ws + lb + LX_PART + 2 * ((j * 2 + hh) * APART);
           st4_plain(pb + 2 * (2 + dim), u32x4{__float_as_uint(s_ao[hh][dim]), tag64,
                                               __float_as_uint(s_ao[hh][dim + 1]), tag64});
@@ -1175,12 +1188,6 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
                                               __float_as_uint(s_ao[hh][dim + 3]), tag64});
           if (dim == 0)
             st4_plain(pb, u32x4{__float_as_uint(hh ? M1 : M0), tag64, __float_as_uint(hh ? L1 : L0), tag64});
-          if (combine) {
-            BAR();  // B5: combined output in s_sc
-            st4_plain(ws + lb + LX_ATT + hh * HD + dim,
-                      u32x4{tagged(tag, rbf(s_sc[hh][dim])), tagged(tag, rbf(s_sc[hh][dim + 1])),
-                            tagged(tag, rbf(s_sc[hh][dim + 2])), tagged(tag, rbf(s_sc[hh][dim + 3]))});
-          }
         }
       }
       MQ_STAMP(layer * 40 + 35);
@@ -1353,11 +1360,12 @@ static int ensure_device(int dev) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return d.status = MQ_ERR_HIP;
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0 || !prop.cooperativeLaunch) return d.status = MQ_ERR_DEVICE;
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(mq_decode_kernel), NT,
-                                                   0) != hipSuccess)
-    return d.status = MQ_ERR_HIP;
-  if (per_cu * prop.multiProcessorCount < NWG) return d.status = MQ_ERR_DEVICE;
+  for (const void* k : {reinterpret_cast<const void*>(mq_decode_kernel<false>),
+                        reinterpret_cast<const void*>(mq_decode_kernel<true>)}) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NT, 0) != hipSuccess) return d.status = MQ_ERR_HIP;
+    if (per_cu * prop.multiProcessorCount < NWG) return d.status = MQ_ERR_DEVICE;
+  }
   void* p = nullptr;
   if (hipMalloc(&p, WS_BYTES) != hipSuccess) return d.status = MQ_ERR_ALLOC;
   if (hipMemset(p, 0, WS_BYTES) != hipSuccess) return d.status = MQ_ERR_HIP;
@@ -1380,8 +1388,9 @@ static int launch(DecodeParams& P, hipStream_t stream) {
   // error after a bounded spin, so an ordinary launch is used: a cooperative
   // launch adds about 18 us of queue synchronisation per token on this stack.
   void* args[] = {&P};
-  const hipError_t e =
-      hipLaunchKernel(reinterpret_cast<const void*>(mq_decode_kernel), dim3(NWG), dim3(NT), args, 0, stream);
+  const void* kern = P.position < KV_CAP ? reinterpret_cast<const void*>(mq_decode_kernel<false>)
+                                         : reinterpret_cast<const void*>(mq_decode_kernel<true>);
+  const hipError_t e = hipLaunchKernel(kern, dim3(NWG), dim3(NT), args, 0, stream);
   return e == hipSuccess ? MQ_OK : MQ_ERR_HIP;
 }
 
