@@ -259,6 +259,33 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
       : "memory");
 }
 
+// L2 warm-up of the K/V rows [0, p) of (layer, group g) for the XCD's attention
+// workgroup: one 4-byte LDS DMA per 64-byte line, so one instruction touches 64
+// lines. Instruction t of the ceil(p / 8) needed (K lines, then V lines) goes to
+// worker t % nworkers; a worker is the store wave of one of the XCD's other
+// workgroups, whose LDS K/V area is otherwise unused and takes the dead data.
+// The issuing wave awaits the copies before that area is reused.
+__device__ __forceinline__ void kv_warm(const DecodeParams& P, int layer, int g, int p, uint32_t lds, int wk,
+                                        int nworkers, int lane) {
+  const size_t base = (size_t)(layer * NKV + g) * P.max_seq_len * HD;
+  const uint8_t* kb = reinterpret_cast<const uint8_t*>(P.k_cache + base);
+  const uint8_t* vb = reinterpret_cast<const uint8_t*>(P.v_cache + base);
+  const int nlk = 4 * p;  // 64-byte lines of K rows 0 .. p-1
+  const int ninst = (2 * nlk + 63) >> 6;
+  for (int t = wk; t < ninst; t += nworkers) {
+    const int li = 64 * t + lane;
+    if (li < 2 * nlk) {
+      const uint8_t* gp = li < nlk ? kb + 64 * (size_t)li : vb + 64 * (size_t)(li - nlk);
+      uint32_t saved;
+      asm volatile(
+          "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "v"(gp), "s"(lds)
+          : "memory");
+    }
+  }
+}
+
 // K/V rows of a chunk live in LDS as [row][16 chunks of 8 dims], chunk c of row r
 // stored in slot c ^ (r & 15) so that 16 rows read at one chunk hit distinct banks.
 __device__ __forceinline__ uint32_t kv_off(int row, int chunk) { return row * 256 + 16 * (chunk ^ (row & 15)); }
@@ -1126,6 +1153,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       wait_count(&s_cnt, target);
       if (lane < 16) st1_plain(ws + lb + LX_QKV + 16 * j + lane, tagged(tag, rbf(s_res[lane])));
       MQ_STAMP(layer * 40 + 34);
+      // the next layer's K/V rows into this XCD's L2 ahead of the attention workgroup's
+      // LDS copy at its gate/up stage: copying them from HBM there held up its down_proj
+      // partials, the last input of the layer's final reduction
+      if (!SPLIT && !att && layer + 1 < L) kv_warm(P, layer + 1, g, p, lds_kv, j - 1, WG_PER_XCD - 1, lane);
       if (att) {
         float M0 = 0.f, M1 = 0.f, L0 = 0.f, L1 = 0.f, Ma0 = 0.f, Ma1 = 0.f, La0 = 0.f, La1 = 0.f;
         for (int ps = 0; ps < npass; ps++) {
@@ -1216,6 +1247,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         st2_dev(ws + X_DPART + 2 * ((j * ROWS + lane) * NXCD + g), u32x2{__float_as_uint(s_res[lane]), tag64});
         MQ_STAMP(layer * 40 + 38);
     }
+    if (!SPLIT) wait_vmem();  // the K/V warm-up copies have landed before the LM head reuses their LDS
     BAR();  // F1
   }
 
