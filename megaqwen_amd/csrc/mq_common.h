@@ -136,6 +136,21 @@ __device__ __forceinline__ void row16_sum_n(float (&v)[N]) {
 #pragma unroll
   for (int k = 0; k < N; k++) v[k] += dpp<0x140>(v[k]);
 }
+// wave_max of N independent values, interleaved like wave_sum_n (results identical to wave_max)
+template <int N>
+__device__ __forceinline__ void wave_max_n(float (&v)[N]) {
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] = fmaxf(v[k], dpp<0xB1>(v[k]));
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] = fmaxf(v[k], dpp<0x4E>(v[k]));
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] = fmaxf(v[k], dpp<0x141>(v[k]));
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] = fmaxf(v[k], dpp<0x140>(v[k]));
+#pragma unroll
+  for (int k = 0; k < N; k++)
+    v[k] = fmaxf(fmaxf(readlane(v[k], 0), readlane(v[k], 16)), fmaxf(readlane(v[k], 32), readlane(v[k], 48)));
+}
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<0xB1>(v));
   v = fmaxf(v, dpp<0x4E>(v));
@@ -196,5 +211,19 @@ struct Buf {
 // stores; gfx9 counts both in vmcnt) to complete. simm16 = vmcnt(0),
 // expcnt(7), lgkmcnt(15).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+// One 16-byte LDS DMA per lane: lane l's 16 bytes at `gptr` land at LDS byte
+// address lds + 16 * l. Issued as inline assembly so that the compiler's vmcnt
+// bookkeeping for register loads ignores it (the waits it
+// derives stay correct, at worst longer); its completion is awaited explicitly.
+// M0 (which carries the LDS address) is saved and restored around it.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gptr), "s"(lds)
+      : "memory");
+}
 
 }  // namespace mq

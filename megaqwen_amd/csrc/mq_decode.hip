@@ -245,20 +245,6 @@ __device__ __forceinline__ float repoll_l64(const Buf& b, uint32_t* ws, uint32_t
   return __uint_as_float(v.x);
 }
 
-// One 16-byte LDS DMA per lane: lane l's 16 bytes at `gptr` land at LDS byte
-// address lds + 16 * l. Issued as inline assembly so that the compiler's vmcnt
-// bookkeeping for the stream waves' register loads ignores it (the waits it
-// derives stay correct, at worst longer); its completion is awaited explicitly.
-// M0 (which carries the LDS address) is saved and restored around it.
-__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(gptr), "s"(lds)
-      : "memory");
-}
-
 // L2 warm-up of the K/V rows [0, p) of (layer, group g) for the XCD's attention
 // workgroup: one 4-byte LDS DMA per 64-byte line, so one instruction touches 64
 // lines. Instruction t of the ceil(p / 8) needed (K lines, then V lines) goes to

@@ -35,12 +35,22 @@ namespace pf {
 
 // ------------------------------------------------------------------ GEMM
 // C[m, n] = sum_k A[m, k] * W[n, k] (both operands k-contiguous, HF nn.Linear
-// layout), one TM x 64 output tile per workgroup, k in steps of 64 staged
-// through LDS (double-buffered). The four waves form a 2 x 2 grid: wave (wm, wn)
-// owns rows 32wm.. (TM = 64) or 16wm.. (TM = 32) of the tile and two 16-column
-// blocks, so every 16-byte fragment read from LDS feeds one or two MFMAs.
-// TM = 32 is used for the N = 1024 products (o_proj, down_proj) so that a
-// 512-row prompt still gives 256 workgroups.
+// layout), one TM x 64 output tile per workgroup, k in steps of 64.
+//
+// Operand tiles move from global memory straight into LDS (global_load_lds_dwordx4,
+// no register staging) through NST LDS stages, so NST - 1 k-steps are in flight
+// while one is multiplied: the k loop runs at the rate the CU can stream operands
+// rather than one memory latency per step. A stage holds the A tile (TM rows) and
+// then the B tile (64 rows), each row as eight 16-byte chunks XOR-swizzled with
+// the row, so that the 8 rows a quarter-wave reads in one fragment load fall in
+// distinct banks. A DMA instruction writes 64 consecutive chunk slots (lane l ->
+// slot base + l), so the swizzle is applied on the source side: the lane that owns
+// slot s fetches the chunk that belongs there.
+//
+// The four waves form a 2 x 2 grid: wave (wm, wn) owns rows 32wm.. (TM = 64) or
+// 16wm.. (TM = 32) of the tile and two 16-column blocks, so every 16-byte
+// fragment read from LDS feeds one or two MFMAs. TM = 32 is used for the N = 1024
+// products (o_proj, down_proj) so that a 512-row prompt still gives 256 workgroups.
 constexpr int TN = 64, TK = 64, GT = 256;
 
 enum : int { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2 };
@@ -58,17 +68,17 @@ struct GemmArgs {
   GemmSeg seg[3];
 };
 
-// LDS slot (in 16-byte chunks) of chunk kc (0..7) of tile row r. The chunks of a
-// row are XOR-swizzled with the row so that the 8 rows a quarter-wave reads in
-// one fragment load fall in distinct banks.
+// LDS slot (in 16-byte chunks) of chunk kc (0..7) of tile row r.
 __device__ __forceinline__ int tslot(int r, int kc) { return r * 8 + (kc ^ (r & 7)); }
 
-template <int EPI, int TM>
+template <int EPI, int TM, int NST, int KS = 1>
 __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
-  constexpr int RB = TM / 32;            // 16-row blocks per wave: 2 (TM 64) or 1 (TM 32)
-  constexpr int AC = TM * 8 / GT;        // A chunks per thread per k tile: 2 or 1
-  __shared__ u32x4 sa[2][TM * 8];
-  __shared__ u32x4 sb[2][TN * 8];
+  constexpr int RB = TM / 32;             // 16-row blocks per wave: 2 (TM 64) or 1 (TM 32)
+  constexpr int ACH = TM * 8, BCH = TN * 8;  // chunk slots of the A and B tiles
+  constexpr int SCH = ACH + BCH;          // slots per stage
+  constexpr int NI = SCH / GT;            // DMA instructions per thread and stage: 4 or 3
+  static_assert(ACH % 64 == 0 && SCH % GT == 0, "a DMA instruction covers 64 slots of one operand");
+  __shared__ u32x4 sbuf[NST][KS][SCH];  // a stage holds KS consecutive 64-wide k-steps
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv >> 1, wn = wv & 1;
   int nt = blockIdx.x, si = 0;
   while (si + 1 < G.nseg && nt >= G.seg[si].ntiles) nt -= G.seg[si++].ntiles;
@@ -77,67 +87,69 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
   // the wave's two column blocks; EPI_SILU pairs gate block wn with up block wn + 2
   const int jb0 = EPI == EPI_SILU ? wn : 2 * wn, jb1 = EPI == EPI_SILU ? wn + 2 : 2 * wn + 1;
 
-  const uint16_t* ga[AC];
-  const uint16_t* gb[2];
-  bool va[AC];
-  int sla[AC], slb[2];
+  // DMA instruction i of this wave fills slots 64 (4 i + wv) .. +63 of a stage
+  const uint16_t* src[NI];
+  uint32_t dst[NI];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sbuf[0][0][0];
 #pragma unroll
-  for (int i = 0; i < AC; i++) {
-    const int c = tid + GT * i, r = c >> 3, kc = c & 7;
-    sla[i] = tslot(r, kc);
-    va[i] = m0 + r < G.m;
-    ga[i] = G.a + (size_t)(va[i] ? m0 + r : 0) * G.lda + 8 * kc;
-  }
-#pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int c = tid + GT * i, r = c >> 3, kc = c & 7;
-    slb[i] = tslot(r, kc);
-    if (EPI == EPI_SILU)
-      gb[i] = (r < 32 ? S.w + (size_t)(32 * nt + r) * G.k : S.w2 + (size_t)(32 * nt + r - 32) * G.k) + 8 * kc;
-    else
-      gb[i] = S.w + (size_t)(TN * nt + r) * G.k + 8 * kc;
-  }
-  u32x4 ra[AC], rb[2];
-  auto gload = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < AC; i++) {
-      const u32x4 t = ldw(ga[i] + kt * TK);
-      ra[i] = va[i] ? t : u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < NI; i++) {
+    const int s0 = 64 * (4 * i + wv), sl = s0 + lane;
+    dst[i] = __builtin_amdgcn_readfirstlane(lds0 + 16u * (uint32_t)s0);  // wave-uniform (M0)
+    if (s0 < ACH) {
+      const int r = sl >> 3, kc = (sl & 7) ^ (r & 7);
+      const int row = min(m0 + r, G.m - 1);  // rows past the prompt repeat its last row (never stored)
+      src[i] = G.a + (size_t)row * G.lda + 8 * kc;
+    } else {
+      const int t = sl - ACH, r = t >> 3, kc = (t & 7) ^ (r & 7);
+      if (EPI == EPI_SILU)
+        src[i] = (r < 32 ? S.w + (size_t)(32 * nt + r) * G.k : S.w2 + (size_t)(32 * nt + r - 32) * G.k) + 8 * kc;
+      else
+        src[i] = S.w + (size_t)(TN * nt + r) * G.k + 8 * kc;
     }
+  }
+  const int KT = G.k / (TK * KS);
+  // stage kt % NST <- k-steps KS kt .. KS kt + KS - 1; steps past the end re-load the last
+  // ones (kept uniform so that every wave issues the same number of DMAs and the vmcnt
+  // waits below are exact)
+  auto issue = [&](int kt) {
+    const int kk = min(kt, KT - 1) * TK * KS;
 #pragma unroll
-    for (int i = 0; i < 2; i++) rb[i] = ldw(gb[i] + kt * TK);
-  };
-  auto lstore = [&](int buf) {
+    for (int q = 0; q < KS; q++) {
+      const uint32_t so = 16u * (uint32_t)(SCH * (KS * (kt % NST) + q));
 #pragma unroll
-    for (int i = 0; i < AC; i++) sa[buf][sla[i]] = ra[i];
-#pragma unroll
-    for (int i = 0; i < 2; i++) sb[buf][slb[i]] = rb[i];
+      for (int i = 0; i < NI; i++) dma16(src[i] + kk + TK * q, dst[i] + so);
+    }
   };
 
   f32x4 acc[RB][2];
 #pragma unroll
   for (int i = 0; i < RB; i++) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int KT = G.k / TK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
+#pragma unroll
+  for (int kt = 0; kt < NST - 1; kt++) issue(kt);
   for (int kt = 0; kt < KT; kt++) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) gload(kt + 1);
+    // this wave's DMAs of step kt have landed (the NST - 2 later steps may still fly);
+    // the barrier publishes every wave's, and tells that step kt - 1's stage is free
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NST - 2) * NI * KS) : "memory");
+    __syncthreads();
+    issue(kt + NST - 1);
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      const int kc = 4 * ks + (lane >> 4), r = lane & 15;
-      const u32x4 b0 = sb[buf][tslot(16 * jb0 + r, kc)], b1 = sb[buf][tslot(16 * jb1 + r, kc)];
+    for (int q = 0; q < KS; q++) {
+      const u32x4* sa = sbuf[kt % NST][q];
+      const u32x4* sb = sa + ACH;
 #pragma unroll
-      for (int i = 0; i < RB; i++) {
-        const u32x4 af = sa[buf][tslot(16 * (RB * wm + i) + r, kc)];
-        acc[i][0] = mfma_16x16x32(af, b0, acc[i][0]);
-        acc[i][1] = mfma_16x16x32(af, b1, acc[i][1]);
+      for (int ks = 0; ks < 2; ks++) {
+        const int kc = 4 * ks + (lane >> 4), r = lane & 15;
+        const u32x4 b0 = sb[tslot(16 * jb0 + r, kc)], b1 = sb[tslot(16 * jb1 + r, kc)];
+#pragma unroll
+        for (int i = 0; i < RB; i++) {
+          const u32x4 af = sa[tslot(16 * (RB * wm + i) + r, kc)];
+          acc[i][0] = mfma_16x16x32(af, b0, acc[i][0]);
+          acc[i][1] = mfma_16x16x32(af, b1, acc[i][1]);
+        }
       }
     }
-    if (kt + 1 < KT) lstore(buf ^ 1);
-    __syncthreads();
   }
+  wait_vmem();  // no DMA may still target this workgroup's LDS when it exits
 
   // lane holds rows 4 * (lane / 16) + e of column lane % 16 of each block
   const int col = lane & 15, rq = 4 * (lane >> 4);
@@ -179,9 +191,9 @@ __global__ void __launch_bounds__(128) embed_rows(const int* ids, const uint16_t
 }
 
 // HF Qwen3RMSNorm (modeling_qwen3.py:59-64) of each row: y = bf16(w * bf16(x * rstd)),
-// rstd = 1 / sqrt(mean(x^2) + eps) in fp32. One wave per row.
-__global__ void __launch_bounds__(256) rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* y, int m) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+// rstd = 1 / sqrt(mean(x^2) + eps) in fp32. One single-wave workgroup per row.
+__global__ void __launch_bounds__(64) rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* y, int m) {
+  const int row = blockIdx.x, lane = threadIdx.x;
   if (row >= m) return;
   const uint16_t* xr = x + (size_t)row * H;
   const u32x4 c[2] = {ldw(xr + 8 * lane), ldw(xr + 512 + 8 * lane)};
@@ -219,29 +231,43 @@ __global__ void __launch_bounds__(256) qk_rope_kv(uint16_t* q, const uint16_t* k
                                                   const uint16_t* qn, const uint16_t* kn, const uint16_t* cos_t,
                                                   const uint16_t* sin_t, uint16_t* kc, uint16_t* vc, int max_seq) {
   const int s = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  constexpr int NH = (NQ + 2 * NKV) / 4;  // heads per wave: hh = wv + 4 i (q, then k, then v heads)
+  // every load of the wave first (q is rewritten in place, but no two heads overlap, so no
+  // store below feeds a load; loading up front keeps the eight heads from running serially)
+  float x1[NH], x2[NH];
+#pragma unroll
+  for (int i = 0; i < NH; i++) {
+    const int hh = wv + 4 * i;
+    const uint16_t* src = hh < NQ         ? q + (size_t)s * QS + HD * hh
+                          : hh < NQ + NKV ? k + (size_t)s * KVS + HD * (hh - NQ)
+                                          : v + (size_t)s * KVS + HD * (hh - NQ - NKV);
+    x1[i] = bf2f(src[lane]);
+    x2[i] = bf2f(src[64 + lane]);
+  }
   const float c1 = bf2f(cos_t[(size_t)s * HD + lane]), c2 = bf2f(cos_t[(size_t)s * HD + 64 + lane]);
   const float s1 = bf2f(sin_t[(size_t)s * HD + lane]), s2 = bf2f(sin_t[(size_t)s * HD + 64 + lane]);
-  for (int hh = wv; hh < NQ + 2 * NKV; hh += 4) {
+  const float qw1 = bf2f(qn[lane]), qw2 = bf2f(qn[64 + lane]), kw1 = bf2f(kn[lane]), kw2 = bf2f(kn[64 + lane]);
+  float ss[NH];
+#pragma unroll
+  for (int i = 0; i < NH; i++) ss[i] = x1[i] * x1[i] + x2[i] * x2[i];
+  wave_sum_n(ss);
+#pragma unroll
+  for (int i = 0; i < NH; i++) {
+    const int hh = wv + 4 * i;
     if (hh < NQ + NKV) {
       const bool isq = hh < NQ;
       const int h = isq ? hh : hh - NQ;
-      const uint16_t* src = isq ? q + (size_t)s * QS + HD * h : k + (size_t)s * KVS + HD * h;
-      const float x1 = bf2f(src[lane]), x2 = bf2f(src[64 + lane]);
-      const float ss = wave_sum(x1 * x1 + x2 * x2);
-      const float rstd = 1.0f / sqrtf(ss * (1.0f / HD) + EPS);
-      const uint16_t* nw = isq ? qn : kn;
-      const float n1 = rbf(bf2f(nw[lane]) * rbf(x1 * rstd)), n2 = rbf(bf2f(nw[64 + lane]) * rbf(x2 * rstd));
+      const float rstd = 1.0f / sqrtf(ss[i] * (1.0f / HD) + EPS);
+      const float n1 = rbf((isq ? qw1 : kw1) * rbf(x1[i] * rstd)), n2 = rbf((isq ? qw2 : kw2) * rbf(x2[i] * rstd));
       const float o1 = rbf(rbf(n1 * c1) - rbf(n2 * s1));
       const float o2 = rbf(rbf(n2 * c2) + rbf(n1 * s2));
       uint16_t* dst = isq ? q + (size_t)s * QS + HD * h : kc + ((size_t)h * max_seq + s) * HD;
       dst[lane] = (uint16_t)f2bf(o1);
       dst[64 + lane] = (uint16_t)f2bf(o2);
     } else {
-      const int h = hh - NQ - NKV;
-      const uint16_t* src = v + (size_t)s * KVS + HD * h;
-      uint16_t* dst = vc + ((size_t)h * max_seq + s) * HD;
-      dst[lane] = src[lane];
-      dst[64 + lane] = src[64 + lane];
+      uint16_t* dst = vc + ((size_t)(hh - NQ - NKV) * max_seq + s) * HD;
+      dst[lane] = (uint16_t)f2bf(x1[i]);  // exact: x is a bf16 value
+      dst[64 + lane] = (uint16_t)f2bf(x2[i]);
     }
   }
 }
@@ -254,17 +280,25 @@ __global__ void __launch_bounds__(256) qk_rope_kv(uint16_t* q, const uint16_t* k
 // accumulator rescaled by exp(m_old - m_new).
 constexpr int AQ = 32;
 constexpr int AKB = 512;
+// LDS row pitches: a P row is padded by 16 bytes so that the 16 rows a quarter-wave
+// reads in one P.V fragment load fall in distinct bank groups (unpadded, 1 KB rows
+// share their banks), and a score row by one word, which spreads the score writes
+constexpr int SC_PITCH = AKB + 1, P_PITCH = AKB + 8;
 constexpr int VT_STRIDE = 72;  // keys per row of the transposed V stage: 64 + 8 (144-byte rows keep
                                // 16-byte alignment and spread 8 consecutive dims over the banks)
 
 __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                                                     uint16_t* out, int S, int max_seq, float scale) {
-  __shared__ float s_sc[AQ][AKB];
-  __shared__ __align__(16) uint16_t s_p[AQ][AKB];
+  __shared__ float s_sc[AQ][SC_PITCH];
+  __shared__ __align__(16) uint16_t s_p[AQ][P_PITCH];
   __shared__ __align__(16) uint16_t s_vt[HD][VT_STRIDE];
   __shared__ float s_m[AQ], s_l[AQ], s_a[AQ];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int r0 = blockIdx.x * AQ, h = blockIdx.y, g = h >> 1;
+  // XCD-aware order: workgroup id runs on XCD id % 8, which is made the KV group g, so the
+  // 32 workgroups reading one group's K/V rows share one L2; the longest query blocks
+  // (the most keys) are dispatched first
+  const int id = blockIdx.x, g = id & 7, r = id >> 3, h = 2 * g + (r & 1);
+  const int r0 = (gridDim.x / NQ - 1 - (r >> 1)) * AQ;
   const uint16_t* K = kc + (size_t)g * max_seq * HD;
   const uint16_t* V = vc + (size_t)g * max_seq * HD;
   const int nkey = min(S, r0 + AQ);
@@ -276,7 +310,7 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
     const int row = r0 + 16 * rb + r16;
 #pragma unroll
     for (int ks = 0; ks < 4; ks++)
-      qf[rb][ks] = row < S ? ldw(q + (size_t)row * QS + HD * h + 32 * ks + 8 * kg) : u32x4{0u, 0u, 0u, 0u};
+      qf[rb][ks] = ldw(q + (size_t)min(row, S - 1) * QS + HD * h + 32 * ks + 8 * kg);  // rows >= S: never stored
   }
   if (tid < AQ) {
     s_m[tid] = -INFINITY;
@@ -290,48 +324,94 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
 
   for (int kb0 = 0; kb0 < nkey; kb0 += AKB) {
     const int kb1 = min(nkey, kb0 + AKB), nk = kb1 - kb0, nk32 = (nk + 31) & ~31;
-    // ---- scores of 16-key blocks b = wv, wv + 4, ...
-    for (int b = wv; b < (nk + 15) >> 4; b += 4) {
-      const int key = kb0 + 16 * b + r16;
-      u32x4 kf[4];
+    // ---- scores of 16-key blocks b = wv + 4i (i < 8): every K load of the wave is issued
+    // before the first product, so the block costs one memory latency, not eight. Keys past
+    // the block read its last row (loads stay unconditional, so none waits for another);
+    // their scores are masked to -inf.
+    const int nb = (nk + 15) >> 4;
+    {
+      u32x4 kf[AKB / 64][4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ks++)
-        kf[ks] = key < kb1 ? ldw(K + (size_t)key * HD + 32 * ks + 8 * kg) : u32x4{0u, 0u, 0u, 0u};
+      for (int i = 0; i < AKB / 64; i++) {
+        const int b = wv + 4 * i, key = kb0 + 16 * b + r16;
+        if (b < nb)
 #pragma unroll
-      for (int rb = 0; rb < 2; rb++) {
-        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int ks = 0; ks < 4; ks++)
+            kf[i][ks] = ldw(K + (size_t)min(key, kb1 - 1) * HD + 32 * ks + 8 * kg);
+      }
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) a = mfma_16x16x32(qf[rb][ks], kf[ks], a);
+      for (int i = 0; i < AKB / 64; i++) {
+        const int b = wv + 4 * i, key = kb0 + 16 * b + r16;
+        if (b < nb)
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int rl = 16 * rb + 4 * kg + e;
-          s_sc[rl][16 * b + r16] = (key <= r0 + rl && key < kb1) ? a[e] * scale : -INFINITY;
-        }
+          for (int rb = 0; rb < 2; rb++) {
+            f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) a = mfma_16x16x32(qf[rb][ks], kf[i][ks], a);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              const int rl = 16 * rb + 4 * kg + e;
+              s_sc[rl][16 * b + r16] = (key <= r0 + rl && key < kb1) ? a[e] * scale : -INFINITY;
+            }
+          }
       }
     }
+    // the block's V rows, all in flight during the softmax: chunk c (64 keys), lane = key,
+    // dims 8 dc .. 8 dc + 7 with dc = 4 it + wv (keys past the block: its last row, weighted 0)
+    u32x4 vr[AKB / 64][4];
+#pragma unroll
+    for (int c = 0; c < AKB / 64; c++)
+      if (64 * c < nk32)
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+          const int dc = 4 * it + wv, key = kb0 + 64 * c + lane;
+          vr[c][it] = ldw(V + (size_t)min(key, kb1 - 1) * HD + 8 * dc);
+        }
     __syncthreads();
-    // ---- softmax rows 8 wv .. 8 wv + 7
-    for (int i = 0; i < 8; i++) {
-      const int rl = 8 * wv + i;
-      float mx = -INFINITY;
-      for (int c = lane; c < nk; c += 64) mx = fmaxf(mx, s_sc[rl][c]);
-      mx = wave_max(mx);
-      const float mo = s_m[rl];
-      const float mn = fmaxf(mo, mx);
-      const float base = mn == -INFINITY ? 0.f : mn;
-      float sum = 0.f;
-      for (int c = lane; c < nk32; c += 64) {
-        const float e = c < nk ? expf(s_sc[rl][c] - base) : 0.f;
-        sum += e;
-        s_p[rl][c] = (uint16_t)f2bf(e);
+    // ---- softmax of rows 8 wv .. 8 wv + 7, all eight at once (the LDS reads of every row
+    // are issued together and the reductions interleaved); lane takes keys lane + 64 u
+    {
+      float x[8][AKB / 64], mx[8], sum[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int u = 0; u < AKB / 64; u++) x[i][u] = s_sc[8 * wv + i][lane + 64 * u];  // past nk: unused
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        mx[i] = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < AKB / 64; u++) mx[i] = fmaxf(mx[i], lane + 64 * u < nk ? x[i][u] : -INFINITY);
       }
-      sum = wave_sum(sum);
-      const float al = mo == -INFINITY ? 0.f : expf(mo - base);
-      if (lane == 0) {
-        s_m[rl] = mn;
-        s_l[rl] = sum + al * s_l[rl];
-        s_a[rl] = al;
+      wave_max_n(mx);
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int rl = 8 * wv + i;
+        const float mn = fmaxf(s_m[rl], mx[i]);
+        const float base = mn == -INFINITY ? 0.f : mn;
+        sum[i] = 0.f;
+        // branch-free: every lane evaluates all eight keys and selects 0 past nk (adding
+        // +0 leaves the sum unchanged; P.V reads s_p only below nk32)
+#pragma unroll
+        for (int u = 0; u < AKB / 64; u++) {
+          const int c = lane + 64 * u;
+          const float ev = expf(x[i][u] - base);
+          const float e = c < nk ? ev : 0.f;
+          sum[i] += e;
+          s_p[rl][c] = (uint16_t)f2bf(e);
+        }
+        mx[i] = mn;
       }
+      wave_sum_n(sum);
+      if (lane == 0)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const int rl = 8 * wv + i;
+          const float mo = s_m[rl], mn = mx[i], base = mn == -INFINITY ? 0.f : mn;
+          const float al = mo == -INFINITY ? 0.f : expf(mo - base);
+          s_m[rl] = mn;
+          s_l[rl] = sum[i] + al * s_l[rl];
+          s_a[rl] = al;
+        }
     }
     __syncthreads();
     // ---- P.V: wave wv owns dims 32 wv .. 32 wv + 31. V rows are staged through LDS
@@ -345,11 +425,14 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
         oacc[rb][0][e] *= al;
         oacc[rb][1][e] *= al;
       }
-    for (int c0 = 0; c0 < nk32; c0 += 64) {
+#pragma unroll
+    for (int c = 0; c < AKB / 64; c++) {
+      const int c0 = 64 * c;
+      if (c0 >= nk32) break;
 #pragma unroll
       for (int it = 0; it < 4; it++) {
-        const int dc = 4 * it + wv, key = kb0 + c0 + lane;  // lane: key, dc: 8-dim chunk
-        const u32x4 v = key < kb1 ? ldw(V + (size_t)key * HD + 8 * dc) : u32x4{0u, 0u, 0u, 0u};
+        const int dc = 4 * it + wv;  // lane: key, dc: 8-dim chunk
+        const u32x4 v = vr[c][it];
         s_vt[8 * dc + 0][lane] = (uint16_t)v.x;
         s_vt[8 * dc + 1][lane] = (uint16_t)(v.x >> 16);
         s_vt[8 * dc + 2][lane] = (uint16_t)v.y;
@@ -501,6 +584,10 @@ __global__ void __launch_bounds__(256) argmax_final(const float* bmv, const int*
 using namespace mq;
 using namespace mq::pf;
 
+// GEMM pipelines (measured on MI355X at S = 512): 64-row tiles keep two 128-wide k stages
+// (64 KB of LDS, two workgroups per CU), 32-row tiles four (96 KB, one per CU)
+constexpr int NST64 = 2, NST32 = 4, KS2 = 2;
+
 extern "C" int launch_prefill_float(const int* input_token_ids, int* output_token_id, int seq_len,
                                     const void* embed_weight, const PrefillLayerWeights* layer_weights,
                                     const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
@@ -557,36 +644,36 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     const PrefillLayerWeights& w = layer_weights[l];
     uint16_t* kcl = bfm(k_cache) + l * kv_layer;
     uint16_t* vcl = bfm(v_cache) + l * kv_layer;
-    rmsnorm_rows<<<(S + 3) / 4, 256, 0, stream>>>(h, bf(w.input_layernorm_weight), nrm, S);
+    rmsnorm_rows<<<S, 64, 0, stream>>>(h, bf(w.input_layernorm_weight), nrm, S);
     chk();
     GemmArgs g{};
     g.a = nrm; g.lda = H; g.m = S; g.k = H; g.nseg = 3;
     g.seg[0] = GemmSeg{bf(w.q_proj_weight), nullptr, qp, QS / TN, QS};
     g.seg[1] = GemmSeg{bf(w.k_proj_weight), nullptr, kp, KVS / TN, KVS};
     g.seg[2] = GemmSeg{bf(w.v_proj_weight), nullptr, vp, KVS / TN, KVS};
-    gemm_nt<EPI_STORE, 64><<<dim3((QS + 2 * KVS) / TN, mt64), GT, 0, stream>>>(g);
+    gemm_nt<EPI_STORE, 64, NST64, KS2><<<dim3((QS + 2 * KVS) / TN, mt64), GT, 0, stream>>>(g);
     chk();
     qk_rope_kv<<<S, 256, 0, stream>>>(qp, kp, vp, bf(w.q_norm_weight), bf(w.k_norm_weight), bf(cos_table),
                                       bf(sin_table), kcl, vcl, max_seq_len);
     chk();
-    attn_prefill<<<dim3((S + AQ - 1) / AQ, NQ), 256, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
+    attn_prefill<<<NQ * ((S + AQ - 1) / AQ), 256, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
     chk();
     GemmArgs go{};
     go.a = att; go.lda = QS; go.m = S; go.k = QS; go.nseg = 1;
     go.seg[0] = GemmSeg{bf(w.o_proj_weight), nullptr, h, H / TN, H};
-    gemm_nt<EPI_RESID, 32><<<dim3(H / TN, mt32), GT, 0, stream>>>(go);
+    gemm_nt<EPI_RESID, 32, NST32, KS2><<<dim3(H / TN, mt32), GT, 0, stream>>>(go);
     chk();
-    rmsnorm_rows<<<(S + 3) / 4, 256, 0, stream>>>(h, bf(w.post_attn_layernorm_weight), mln, S);
+    rmsnorm_rows<<<S, 64, 0, stream>>>(h, bf(w.post_attn_layernorm_weight), mln, S);
     chk();
     GemmArgs gu{};
     gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
     gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, I / 32, I};
-    gemm_nt<EPI_SILU, 64><<<dim3(I / 32, mt64), GT, 0, stream>>>(gu);
+    gemm_nt<EPI_SILU, 64, NST64, KS2><<<dim3(I / 32, mt64), GT, 0, stream>>>(gu);
     chk();
     GemmArgs gd{};
     gd.a = mid; gd.lda = I; gd.m = S; gd.k = I; gd.nseg = 1;
     gd.seg[0] = GemmSeg{bf(w.down_proj_weight), nullptr, h, H / TN, H};
-    gemm_nt<EPI_RESID, 32><<<dim3(H / TN, mt32), GT, 0, stream>>>(gd);
+    gemm_nt<EPI_RESID, 32, NST32, KS2><<<dim3(H / TN, mt32), GT, 0, stream>>>(gd);
     chk();
   }
   lm_partial<<<LMB, 256, 0, stream>>>(h + (size_t)(S - 1) * H, bf(final_norm_weight), bf(lm_head_weight),
