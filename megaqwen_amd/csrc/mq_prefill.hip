@@ -51,7 +51,7 @@ namespace pf {
 // 16wm.. (TM = 32) of the tile and two 16-column blocks, so every 16-byte
 // fragment read from LDS feeds one or two MFMAs. TM = 32 is used for the N = 1024
 // products (o_proj, down_proj) so that a 512-row prompt still gives 256 workgroups.
-constexpr int TN = 64, TK = 64, GT = 256;
+constexpr int TK = 64, GT = 256;
 
 enum : int { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2 };
 
@@ -71,9 +71,11 @@ struct GemmArgs {
 // LDS slot (in 16-byte chunks) of chunk kc (0..7) of tile row r.
 __device__ __forceinline__ int tslot(int r, int kc) { return r * 8 + (kc ^ (r & 7)); }
 
-template <int EPI, int TM, int NST, int KS = 1>
+template <int EPI, int TM, int TN, int NST, int KS>
 __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
-  constexpr int RB = TM / 32;             // 16-row blocks per wave: 2 (TM 64) or 1 (TM 32)
+  constexpr int RB = TM / 32;             // 16-row blocks per wave
+  constexpr int CB = TN / 32;             // 16-column blocks per wave
+  constexpr int HB = TN / 32;             // EPI_SILU: gate (and up) blocks per tile
   constexpr int ACH = TM * 8, BCH = TN * 8;  // chunk slots of the A and B tiles
   constexpr int SCH = ACH + BCH;          // slots per stage
   constexpr int NI = SCH / GT;            // DMA instructions per thread and stage: 4 or 3
@@ -84,8 +86,12 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
   while (si + 1 < G.nseg && nt >= G.seg[si].ntiles) nt -= G.seg[si++].ntiles;
   const GemmSeg S = G.seg[si];
   const int m0 = blockIdx.y * TM;
-  // the wave's two column blocks; EPI_SILU pairs gate block wn with up block wn + 2
-  const int jb0 = EPI == EPI_SILU ? wn : 2 * wn, jb1 = EPI == EPI_SILU ? wn + 2 : 2 * wn + 1;
+  // the wave's column blocks; EPI_SILU: blocks j < CB / 2 are gate blocks, each paired with
+  // the up block j + CB / 2 (gate rows are the tile's first TN / 2 rows, up rows the rest)
+  int jb[CB];
+#pragma unroll
+  for (int j = 0; j < CB; j++)
+    jb[j] = EPI == EPI_SILU ? (j < CB / 2 ? (CB / 2) * wn + j : HB + (CB / 2) * wn + j - CB / 2) : CB * wn + j;
 
   // DMA instruction i of this wave fills slots 64 (4 i + wv) .. +63 of a stage
   const uint16_t* src[NI];
@@ -102,7 +108,8 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
     } else {
       const int t = sl - ACH, r = t >> 3, kc = (t & 7) ^ (r & 7);
       if (EPI == EPI_SILU)
-        src[i] = (r < 32 ? S.w + (size_t)(32 * nt + r) * G.k : S.w2 + (size_t)(32 * nt + r - 32) * G.k) + 8 * kc;
+        src[i] = (r < TN / 2 ? S.w + (size_t)(TN / 2 * nt + r) * G.k : S.w2 + (size_t)(TN / 2 * nt + r - TN / 2) * G.k) +
+                 8 * kc;
       else
         src[i] = S.w + (size_t)(TN * nt + r) * G.k + 8 * kc;
     }
@@ -121,9 +128,11 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
     }
   };
 
-  f32x4 acc[RB][2];
+  f32x4 acc[RB][CB];
 #pragma unroll
-  for (int i = 0; i < RB; i++) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < RB; i++)
+#pragma unroll
+    for (int j = 0; j < CB; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kt = 0; kt < NST - 1; kt++) issue(kt);
   for (int kt = 0; kt < KT; kt++) {
@@ -139,12 +148,14 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
 #pragma unroll
       for (int ks = 0; ks < 2; ks++) {
         const int kc = 4 * ks + (lane >> 4), r = lane & 15;
-        const u32x4 b0 = sb[tslot(16 * jb0 + r, kc)], b1 = sb[tslot(16 * jb1 + r, kc)];
+        u32x4 bf[CB];
+#pragma unroll
+        for (int j = 0; j < CB; j++) bf[j] = sb[tslot(16 * jb[j] + r, kc)];
 #pragma unroll
         for (int i = 0; i < RB; i++) {
           const u32x4 af = sa[tslot(16 * (RB * wm + i) + r, kc)];
-          acc[i][0] = mfma_16x16x32(af, b0, acc[i][0]);
-          acc[i][1] = mfma_16x16x32(af, b1, acc[i][1]);
+#pragma unroll
+          for (int j = 0; j < CB; j++) acc[i][j] = mfma_16x16x32(af, bf[j], acc[i][j]);
         }
       }
     }
@@ -162,13 +173,16 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
       uint16_t* orow = S.out + (size_t)row * S.ldo;
       if (EPI == EPI_SILU) {
         // HF Qwen3MLP (modeling_qwen3.py:81-83): down(bf16(silu(bf16 gate)) * bf16 up)
-        const float g = rbf(acc[i][0][e]), u = rbf(acc[i][1][e]);
-        const float sg = rbf(g / (1.0f + expf(-g)));
-        orow[32 * nt + 16 * wn + col] = (uint16_t)f2bf(sg * u);
+#pragma unroll
+        for (int j = 0; j < CB / 2; j++) {
+          const float g = rbf(acc[i][j][e]), u = rbf(acc[i][j + CB / 2][e]);
+          const float sg = rbf(g / (1.0f + expf(-g)));
+          orow[TN / 2 * nt + 16 * jb[j] + col] = (uint16_t)f2bf(sg * u);
+        }
       } else {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-          const int c = TN * nt + 16 * (j ? jb1 : jb0) + col;
+        for (int j = 0; j < CB; j++) {
+          const int c = TN * nt + 16 * jb[j] + col;
           float v = rbf(acc[i][j][e]);
           if (EPI == EPI_RESID) v = bf2f(orow[c]) + v;  // residual add, rounded once more
           orow[c] = (uint16_t)f2bf(v);
@@ -194,31 +208,32 @@ __global__ void __launch_bounds__(128) embed_rows(const int* ids, const uint16_t
 // rstd = 1 / sqrt(mean(x^2) + eps) in fp32. One single-wave workgroup per row.
 __global__ void __launch_bounds__(64) rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* y, int m) {
   const int row = blockIdx.x, lane = threadIdx.x;
-  if (row >= m) return;
-  const uint16_t* xr = x + (size_t)row * H;
-  const u32x4 c[2] = {ldw(xr + 8 * lane), ldw(xr + 512 + 8 * lane)};
-  const u32x4 wc[2] = {ldw(w + 8 * lane), ldw(w + 512 + 8 * lane)};
-  float f[2][8];
-  float ss = 0.f;
+  if (row < m) {
+    const uint16_t* xr = x + (size_t)row * H;
+    const u32x4 c[2] = {ldw(xr + 8 * lane), ldw(xr + 512 + 8 * lane)};
+    const u32x4 wc[2] = {ldw(w + 8 * lane), ldw(w + 512 + 8 * lane)};
+    float f[2][8];
+    float ss = 0.f;
 #pragma unroll
-  for (int h = 0; h < 2; h++) {
-    unpack8(c[h], f[h]);
+    for (int h = 0; h < 2; h++) {
+      unpack8(c[h], f[h]);
 #pragma unroll
-    for (int i = 0; i < 8; i++) ss = fmaf(f[h][i], f[h][i], ss);
-  }
-  ss = wave_sum(ss);
-  const float rstd = 1.0f / sqrtf(ss * (1.0f / H) + EPS);
-  uint16_t* yr = y + (size_t)row * H;
+      for (int i = 0; i < 8; i++) ss = fmaf(f[h][i], f[h][i], ss);
+    }
+    ss = wave_sum(ss);
+    const float rstd = 1.0f / sqrtf(ss * (1.0f / H) + EPS);
+    uint16_t* yr = y + (size_t)row * H;
 #pragma unroll
-  for (int h = 0; h < 2; h++) {
-    float wf[8];
-    unpack8(wc[h], wf);
-    u32x4 o;
-    o.x = pack_bf2(rbf(wf[0] * rbf(f[h][0] * rstd)), rbf(wf[1] * rbf(f[h][1] * rstd)));
-    o.y = pack_bf2(rbf(wf[2] * rbf(f[h][2] * rstd)), rbf(wf[3] * rbf(f[h][3] * rstd)));
-    o.z = pack_bf2(rbf(wf[4] * rbf(f[h][4] * rstd)), rbf(wf[5] * rbf(f[h][5] * rstd)));
-    o.w = pack_bf2(rbf(wf[6] * rbf(f[h][6] * rstd)), rbf(wf[7] * rbf(f[h][7] * rstd)));
-    reinterpret_cast<u32x4*>(yr + 512 * h)[lane] = o;
+    for (int h = 0; h < 2; h++) {
+      float wf[8];
+      unpack8(wc[h], wf);
+      u32x4 o;
+      o.x = pack_bf2(rbf(wf[0] * rbf(f[h][0] * rstd)), rbf(wf[1] * rbf(f[h][1] * rstd)));
+      o.y = pack_bf2(rbf(wf[2] * rbf(f[h][2] * rstd)), rbf(wf[3] * rbf(f[h][3] * rstd)));
+      o.z = pack_bf2(rbf(wf[4] * rbf(f[h][4] * rstd)), rbf(wf[5] * rbf(f[h][5] * rstd)));
+      o.w = pack_bf2(rbf(wf[6] * rbf(f[h][6] * rstd)), rbf(wf[7] * rbf(f[h][7] * rstd)));
+      reinterpret_cast<u32x4*>(yr + 512 * h)[lane] = o;
+    }
   }
 }
 
@@ -587,6 +602,14 @@ using namespace mq::pf;
 // GEMM pipelines (measured on MI355X at S = 512): 64-row tiles keep two 128-wide k stages
 // (64 KB of LDS, two workgroups per CU), 32-row tiles four (96 KB, one per CU)
 constexpr int NST64 = 2, NST32 = 4, KS2 = 2;
+// tile widths of the four products
+constexpr int TN_QKV = 64, TN_GU = 64, TN_RES = 64;
+
+// one launch of gemm_nt over a [m, sum of the segments' widths] output
+template <int EPI, int TM, int TN, int NST, int KS>
+void gemm(const GemmArgs& g, int ntiles, hipStream_t stream) {
+  gemm_nt<EPI, TM, TN, NST, KS><<<dim3(ntiles, (g.m + TM - 1) / TM), GT, 0, stream>>>(g);
+}
 
 extern "C" int launch_prefill_float(const int* input_token_ids, int* output_token_id, int seq_len,
                                     const void* embed_weight, const PrefillLayerWeights* layer_weights,
@@ -630,7 +653,6 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
   uint16_t* mln = bfm(mlp_norm);
   uint16_t* mid = bfm(mlp_intermediate);
   const size_t kv_layer = (size_t)NKV * max_seq_len * HD;
-  const int mt64 = (S + 63) / 64, mt32 = (S + 31) / 32;
 
   hipError_t launch_err = hipSuccess;
   auto chk = [&]() {
@@ -648,10 +670,10 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     chk();
     GemmArgs g{};
     g.a = nrm; g.lda = H; g.m = S; g.k = H; g.nseg = 3;
-    g.seg[0] = GemmSeg{bf(w.q_proj_weight), nullptr, qp, QS / TN, QS};
-    g.seg[1] = GemmSeg{bf(w.k_proj_weight), nullptr, kp, KVS / TN, KVS};
-    g.seg[2] = GemmSeg{bf(w.v_proj_weight), nullptr, vp, KVS / TN, KVS};
-    gemm_nt<EPI_STORE, 64, NST64, KS2><<<dim3((QS + 2 * KVS) / TN, mt64), GT, 0, stream>>>(g);
+    g.seg[0] = GemmSeg{bf(w.q_proj_weight), nullptr, qp, QS / TN_QKV, QS};
+    g.seg[1] = GemmSeg{bf(w.k_proj_weight), nullptr, kp, KVS / TN_QKV, KVS};
+    g.seg[2] = GemmSeg{bf(w.v_proj_weight), nullptr, vp, KVS / TN_QKV, KVS};
+    gemm<EPI_STORE, 64, TN_QKV, NST64, KS2>(g, (QS + 2 * KVS) / TN_QKV, stream);
     chk();
     qk_rope_kv<<<S, 256, 0, stream>>>(qp, kp, vp, bf(w.q_norm_weight), bf(w.k_norm_weight), bf(cos_table),
                                       bf(sin_table), kcl, vcl, max_seq_len);
@@ -660,20 +682,20 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     chk();
     GemmArgs go{};
     go.a = att; go.lda = QS; go.m = S; go.k = QS; go.nseg = 1;
-    go.seg[0] = GemmSeg{bf(w.o_proj_weight), nullptr, h, H / TN, H};
-    gemm_nt<EPI_RESID, 32, NST32, KS2><<<dim3(H / TN, mt32), GT, 0, stream>>>(go);
+    go.seg[0] = GemmSeg{bf(w.o_proj_weight), nullptr, h, H / TN_RES, H};
+    gemm<EPI_RESID, 32, TN_RES, NST32, KS2>(go, H / TN_RES, stream);
     chk();
     rmsnorm_rows<<<S, 64, 0, stream>>>(h, bf(w.post_attn_layernorm_weight), mln, S);
     chk();
     GemmArgs gu{};
     gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
-    gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, I / 32, I};
-    gemm_nt<EPI_SILU, 64, NST64, KS2><<<dim3(I / 32, mt64), GT, 0, stream>>>(gu);
+    gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, I / (TN_GU / 2), I};
+    gemm<EPI_SILU, 64, TN_GU, NST64, KS2>(gu, I / (TN_GU / 2), stream);
     chk();
     GemmArgs gd{};
     gd.a = mid; gd.lda = I; gd.m = S; gd.k = I; gd.nseg = 1;
-    gd.seg[0] = GemmSeg{bf(w.down_proj_weight), nullptr, h, H / TN, H};
-    gemm_nt<EPI_RESID, 32, NST32, KS2><<<dim3(H / TN, mt32), GT, 0, stream>>>(gd);
+    gd.seg[0] = GemmSeg{bf(w.down_proj_weight), nullptr, h, H / TN_RES, H};
+    gemm<EPI_RESID, 32, TN_RES, NST32, KS2>(gd, H / TN_RES, stream);
     chk();
   }
   lm_partial<<<LMB, 256, 0, stream>>>(h + (size_t)(S - 1) * H, bf(final_norm_weight), bf(lm_head_weight),
