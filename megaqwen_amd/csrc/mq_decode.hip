@@ -272,6 +272,39 @@ __device__ __forceinline__ void kv_warm(const DecodeParams& P, int layer, int g,
   }
 }
 
+// L2 warm-up of the weight rows that XCD g's attention workgroup (j = 0) loads during
+// this layer after its attention (gate and up rows 384g .. 384g+11; down_proj rows 0..31,
+// columns 384g .. 384g+383) and at the end of it for the next layer (q rows 256g ..
+// 256g+15; o_proj rows 0..31, columns 256g .. 256g+255): 960 128-byte lines, one 4-byte
+// LDS DMA each, line t on worker t % nworkers (the same workers as kv_warm).
+// `wl` is the layer's and `wn` the next layer's weight-pointer row.
+__device__ __forceinline__ void att_weight_warm(const uint16_t* const* wl, const uint16_t* const* wn, int g,
+                                                uint32_t lds, int wk, int nworkers, int lane) {
+  constexpr int NQL = 16 * 16, NOL = 32 * 4, NGL = 12 * 16, NDL = 32 * 6;  // lines per part
+  constexpr int NL = NQL + NOL + 2 * NGL + NDL;
+  for (int t = 64 * wk + lane; t < NL; t += 64 * nworkers) {
+    const uint8_t* a;
+    if (t < NQL) {
+      a = reinterpret_cast<const uint8_t*>(uniform_ptr(wn[W_Q]) + (size_t)256 * g * H) + 128 * t;
+    } else if (t < NQL + NOL) {
+      const int u = t - NQL;
+      a = reinterpret_cast<const uint8_t*>(uniform_ptr(wn[W_O]) + (size_t)(u >> 2) * QS + 256 * g) + 128 * (u & 3);
+    } else if (t < NQL + NOL + 2 * NGL) {
+      const int u = t - NQL - NOL;
+      const uint16_t* w = uniform_ptr(wl[u < NGL ? W_G : W_U]);
+      a = reinterpret_cast<const uint8_t*>(w + (size_t)XUNITS * g * H) + 128 * (u < NGL ? u : u - NGL);
+    } else {
+      const int u = t - NQL - NOL - 2 * NGL, row = u / 6;
+      a = reinterpret_cast<const uint8_t*>(uniform_ptr(wl[W_D]) + (size_t)row * I + XUNITS * g) + 128 * (u - 6 * row);
+    }
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(a), "s"(lds)
+                 : "memory");
+  }
+}
+
 // K/V rows of a chunk live in LDS as [row][16 chunks of 8 dims], chunk c of row r
 // stored in slot c ^ (r & 15) so that 16 rows read at one chunk hit distinct banks.
 __device__ __forceinline__ uint32_t kv_off(int row, int chunk) { return row * 256 + 16 * (chunk ^ (row & 15)); }
@@ -1142,7 +1175,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       // the next layer's K/V rows into this XCD's L2 ahead of the attention workgroup's
       // LDS copy at its gate/up stage: copying them from HBM there held up its down_proj
       // partials, the last input of the layer's final reduction
-      if (!SPLIT && !att && layer + 1 < L) kv_warm(P, layer + 1, g, p, lds_kv, j - 1, WG_PER_XCD - 1, lane);
+      if (!SPLIT && !att && layer + 1 < L) {
+        kv_warm(P, layer + 1, g, p, lds_kv, j - 1, WG_PER_XCD - 1, lane);
+        // and the attention workgroup's weight rows of its stages after attention
+        att_weight_warm(s_lw[layer], s_lw[layer + 1], g, lds_kv, j - 1, WG_PER_XCD - 1, lane);
+      }
       if (att) {
         float M0 = 0.f, M1 = 0.f, L0 = 0.f, L1 = 0.f, Ma0 = 0.f, Ma1 = 0.f, La0 = 0.f, La1 = 0.f;
         for (int ps = 0; ps < npass; ps++) {
