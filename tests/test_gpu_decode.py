@@ -73,10 +73,12 @@ def test_block_config2_matches_hf(gpu_weights, layer0, state_dict):
     assert np.array_equal(vg[:, :200], vc[:, :200]) and np.array_equal(vg[:, 201:], vc[:, 201:])
 
 
-@pytest.mark.parametrize("pos", [0, 1, 31, 32, 33, 200, 1023, 1024, 2047, 4097, 8191, 8192, 8447, 12000, 16383])
+@pytest.mark.parametrize("pos", [0, 1, 31, 32, 33, 200, 255, 256, 257, 511, 512, 1023, 1024, 2047, 4097, 8191, 8192, 8447,
+                                 12000, 16383])
 def test_block_attention_splits_vs_oracle(gpu_weights, layer0, state_dict, pos):
     """Split-K attention over every split count, and past 8192 positions the two LDS
-    passes per workgroup: random N(0,1) cache, query at `pos`."""
+    passes per workgroup: random N(0,1) cache, query at `pos`. Positions up to 255 run the
+    kernel instance without split code (255: one full 256-row LDS pass), 256 on the other."""
     print(f"block pos {pos}", flush=True)
     g = torch.Generator().manual_seed(100 + pos)
     max_seq = 16384
