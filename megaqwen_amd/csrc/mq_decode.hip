@@ -24,7 +24,10 @@
 //   * reduce wave 6 sums the eight XCDs' o_proj and down_proj partials of the
 //     workgroup's 32 residual rows and applies the residual adds.
 //   * store wave 7 publishes the stream waves' dot products (handed over
-//     through LDS) and the K/V append.
+//     through LDS) and the K/V append. In the instance for contexts of at most
+//     256 positions the store waves of the 31 workgroups without attention also
+//     warm the XCD's L2 with the attention workgroup's next K/V rows and weight
+//     rows, which it would otherwise copy from HBM on its critical path.
 // Per layer and workgroup (g, j):
 //   q/k/v : rows 16j .. 16j+15 of the group's [q0; q1; k; v]
 //   attn  : workgroups j < nsplit attend over chunk j (<= 256 positions) for the
@@ -32,7 +35,10 @@
 //   o_proj: partial sums of rows 32j .. 32j+31 over the group's 256 columns
 //   MLP   : gate and up rows of units 384g + 12j .. +11, then down_proj
 //           partial sums of rows 32j .. 32j+31 over the XCD's 384 units
-// so a layer has five XCD-local all-gathers and two cross-XCD reductions.
+// so a layer has five XCD-local all-gathers and two cross-XCD reductions. The
+// kernel has two instances: SPLIT = false for contexts of at most 256
+// positions (one attention workgroup per XCD, no chunk merge compiled in) and
+// SPLIT = true for the rest.
 //
 // Exchanges use "tagged words": a bf16 value in the low half of a 32-bit word
 // and a 16-bit tag (launch epoch x 32 + layer) in the high half, or an fp32
@@ -1006,9 +1012,9 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           }
         }
       } else {
-        // every workgroup merges the XCD's chunk partials itself (no second hand-over through
-        // a combining workgroup): thread pt takes dims d0, d0 + 1 of head hh, four chunks per
-        // round; a round issues all its loads, then re-polls the stale ones together
+        // every workgroup merges the XCD's chunk partials itself, straight into its o_proj
+        // input: thread pt takes dims d0, d0 + 1 of head hh, four chunks per round; a round
+        // issues all its loads, then re-polls the stale ones together
         const int hh = pt >> 6, d0 = 2 * (pt & 63);
         float Mc = -INFINITY, Lc = 0.f, O0 = 0.f, O1 = 0.f;
         constexpr int CG = 4;
