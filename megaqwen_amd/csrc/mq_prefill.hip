@@ -290,23 +290,47 @@ __global__ void __launch_bounds__(256) qk_rope_kv(uint16_t* q, const uint16_t* k
 // ------------------------------------------------------------------ causal attention
 // Workgroup (q block, head h): query rows r0 .. r0+31 of head h against keys
 // 0 .. min(S, r0 + 32) - 1 of KV head h / 2, in blocks of 512 keys. Per block:
-// scores (MFMA, K fragments straight from the cache) -> LDS; per-row max, exp and
-// sum with the running maximum -> bf16 probabilities in LDS; P.V on MFMA with the
-// accumulator rescaled by exp(m_old - m_new).
+// scores (MFMA) -> LDS; per-row max, exp and sum with the running maximum -> bf16
+// probabilities in LDS; P.V on MFMA with the accumulator rescaled by exp(m_old - m_new).
+//
+// K and V rows reach LDS by 1 KB DMA instructions (four whole rows each), 64 keys at a
+// time through two buffers, one chunk in flight while the previous one is used: loading
+// MFMA operands straight from global memory would touch 16 rows per instruction, which
+// streams at a third of the rate. A row's eight-dim chunk c sits in slot c ^ (row & 15),
+// so the 16 rows of a score fragment read hit distinct banks; P.V reads V with transpose
+// reads (ds_read_b64_tr_b16), so V needs no transposed copy.
 constexpr int AQ = 32;
 constexpr int AKB = 512;
+constexpr int ACK = 64;  // keys per LDS chunk
 // LDS row pitches: a P row is padded by 16 bytes so that the 16 rows a quarter-wave
 // reads in one P.V fragment load fall in distinct bank groups (unpadded, 1 KB rows
 // share their banks), and a score row by one word, which spreads the score writes
 constexpr int SC_PITCH = AKB + 1, P_PITCH = AKB + 8;
-constexpr int VT_STRIDE = 72;  // keys per row of the transposed V stage: 64 + 8 (144-byte rows keep
-                               // 16-byte alignment and spread 8 consecutive dims over the banks)
+
+__device__ __forceinline__ uint32_t akv_off(int row, int chunk) { return row * 256 + 16 * (chunk ^ (row & 15)); }
+
+// Rows k0 .. k0 + ACK - 1 of a K or V cache head (rows past klast repeat row klast) into
+// the chunk buffer at LDS address `lds`: instruction q moves rows 4q .. 4q + 3, lane ->
+// row 4q + lane / 16, slot lane % 16.
+__device__ __forceinline__ void kv_chunk(const uint16_t* src, int k0, int klast, uint32_t lds, int wv, int lane) {
+#pragma unroll
+  for (int i = 0; i < ACK / 16; i++) {
+    const int q = wv + 4 * i, row = 4 * q + (lane >> 4), chunk = (lane & 15) ^ (row & 15);
+    dma16(src + (size_t)min(k0 + row, klast) * HD + 8 * chunk, __builtin_amdgcn_readfirstlane(lds + 1024u * q));
+  }
+}
+// Waits for this wave's chunk DMAs with at most n instructions still in flight, then a
+// workgroup barrier (no vector-memory fence, so a prefetched chunk stays in flight).
+#define AWAIT(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
+#define ABAR() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
 __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                                                     uint16_t* out, int S, int max_seq, float scale) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
   __shared__ float s_sc[AQ][SC_PITCH];
   __shared__ __align__(16) uint16_t s_p[AQ][P_PITCH];
-  __shared__ __align__(16) uint16_t s_vt[HD][VT_STRIDE];
+  __shared__ __align__(16) uint8_t s_kv[2][ACK * 256];
   __shared__ float s_m[AQ], s_l[AQ], s_a[AQ];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   // XCD-aware order: workgroup id runs on XCD id % 8, which is made the KV group g, so the
@@ -318,6 +342,7 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
   const uint16_t* V = vc + (size_t)g * max_seq * HD;
   const int nkey = min(S, r0 + AQ);
   const int r16 = lane & 15, kg = lane >> 4;
+  const uint32_t kv0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_kv[0][0];
 
   u32x4 qf[2][4];
 #pragma unroll
@@ -339,50 +364,35 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
 
   for (int kb0 = 0; kb0 < nkey; kb0 += AKB) {
     const int kb1 = min(nkey, kb0 + AKB), nk = kb1 - kb0, nk32 = (nk + 31) & ~31;
-    // ---- scores of 16-key blocks b = wv + 4i (i < 8): every K load of the wave is issued
-    // before the first product, so the block costs one memory latency, not eight. Keys past
-    // the block read its last row (loads stay unconditional, so none waits for another);
-    // their scores are masked to -inf.
-    const int nb = (nk + 15) >> 4;
-    {
-      u32x4 kf[AKB / 64][4];
+    const int nch = (nk + ACK - 1) / ACK;
+    // ---- scores: chunk c (keys kb0 + 64c ..), wave wv takes its 16 keys 16 wv .. of it
+    kv_chunk(K, kb0, kb1 - 1, kv0, wv, lane);
+    for (int c = 0; c < nch; c++) {
+      AWAIT(0);  // chunk c (the only one in flight)
+      ABAR();    // ... for every wave, which are also done with chunk c - 1's buffer
+      if (c + 1 < nch) kv_chunk(K, kb0 + ACK * (c + 1), kb1 - 1, kv0 + ((c + 1) & 1) * ACK * 256, wv, lane);
+      const uint8_t* kb = s_kv[c & 1];
+      const int row = 16 * wv + r16, key = kb0 + ACK * c + row;
+      u32x4 kf[4];
 #pragma unroll
-      for (int i = 0; i < AKB / 64; i++) {
-        const int b = wv + 4 * i, key = kb0 + 16 * b + r16;
-        if (b < nb)
+      for (int ks = 0; ks < 4; ks++) kf[ks] = *reinterpret_cast<const u32x4*>(kb + akv_off(row, 4 * ks + kg));
 #pragma unroll
-          for (int ks = 0; ks < 4; ks++)
-            kf[i][ks] = ldw(K + (size_t)min(key, kb1 - 1) * HD + 32 * ks + 8 * kg);
-      }
+      for (int rb = 0; rb < 2; rb++) {
+        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < AKB / 64; i++) {
-        const int b = wv + 4 * i, key = kb0 + 16 * b + r16;
-        if (b < nb)
+        for (int ks = 0; ks < 4; ks++) a = mfma_16x16x32(qf[rb][ks], kf[ks], a);
 #pragma unroll
-          for (int rb = 0; rb < 2; rb++) {
-            f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) a = mfma_16x16x32(qf[rb][ks], kf[i][ks], a);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-              const int rl = 16 * rb + 4 * kg + e;
-              s_sc[rl][16 * b + r16] = (key <= r0 + rl && key < kb1) ? a[e] * scale : -INFINITY;
-            }
-          }
+        for (int e = 0; e < 4; e++) {
+          const int rl = 16 * rb + 4 * kg + e;
+          s_sc[rl][ACK * c + row] = (key <= r0 + rl && key < kb1) ? a[e] * scale : -INFINITY;
+        }
       }
     }
-    // the block's V rows, all in flight during the softmax: chunk c (64 keys), lane = key,
-    // dims 8 dc .. 8 dc + 7 with dc = 4 it + wv (keys past the block: its last row, weighted 0)
-    u32x4 vr[AKB / 64][4];
-#pragma unroll
-    for (int c = 0; c < AKB / 64; c++)
-      if (64 * c < nk32)
-#pragma unroll
-        for (int it = 0; it < 4; it++) {
-          const int dc = 4 * it + wv, key = kb0 + 64 * c + lane;
-          vr[c][it] = ldw(V + (size_t)min(key, kb1 - 1) * HD + 8 * dc);
-        }
-    __syncthreads();
+    ABAR();  // scores complete, K buffers free
+    // the block's first two V chunks, in flight during the softmax
+    const int ncv = nk32 / ACK + ((nk32 & (ACK - 1)) != 0);
+    kv_chunk(V, kb0, kb1 - 1, kv0, wv, lane);
+    if (ncv > 1) kv_chunk(V, kb0 + ACK, kb1 - 1, kv0 + ACK * 256, wv, lane);
     // ---- softmax of rows 8 wv .. 8 wv + 7, all eight at once (the LDS reads of every row
     // are issued together and the reductions interleaved); lane takes keys lane + 64 u
     {
@@ -408,11 +418,11 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
         // +0 leaves the sum unchanged; P.V reads s_p only below nk32)
 #pragma unroll
         for (int u = 0; u < AKB / 64; u++) {
-          const int c = lane + 64 * u;
+          const int cc = lane + 64 * u;
           const float ev = expf(x[i][u] - base);
-          const float e = c < nk ? ev : 0.f;
+          const float e = cc < nk ? ev : 0.f;
           sum[i] += e;
-          s_p[rl][c] = (uint16_t)f2bf(e);
+          s_p[rl][cc] = (uint16_t)f2bf(e);
         }
         mx[i] = mn;
       }
@@ -428,10 +438,8 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
           s_a[rl] = al;
         }
     }
-    __syncthreads();
-    // ---- P.V: wave wv owns dims 32 wv .. 32 wv + 31. V rows are staged through LDS
-    // transposed ([dim][key], 64 keys at a time) so that an MFMA operand (8 keys of
-    // one dim) is one 16-byte read.
+    ABAR();  // s_p, s_a
+    // ---- P.V: wave wv owns dims 32 wv .. 32 wv + 31 (two 16-dim blocks)
 #pragma unroll
     for (int rb = 0; rb < 2; rb++)
 #pragma unroll
@@ -440,37 +448,40 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
         oacc[rb][0][e] *= al;
         oacc[rb][1][e] *= al;
       }
+    for (int c = 0; c < ncv; c++) {
+      // chunk c landed (for c = 0, chunk 1 may still be in flight)
+      if (c == 0 && ncv > 1)
+        AWAIT(ACK / 16);
+      else
+        AWAIT(0);
+      ABAR();  // ... for every wave, which are also done with chunk c - 1's buffer
+      if (c >= 1 && c + 1 < ncv) kv_chunk(V, kb0 + ACK * (c + 1), kb1 - 1, kv0 + ((c + 1) & 1) * ACK * 256, wv, lane);
+      const uint32_t vb = kv0 + (c & 1) * ACK * 256;
+      for (int kk = 0; kk < 2 && ACK * c + 32 * kk < nk32; kk++) {
+        // B operand (8 keys of one dim per lane) from two transpose reads: within each
+        // 16-lane group, lane j addresses key base + j / 4, dims 4 (j % 4) .. +3 of the
+        // 16-dim block, and lane i receives that dim's 4 keys
+        const int ra = 32 * kk + 8 * kg + (r16 >> 2);
+        u32x4 vf[2];
 #pragma unroll
-    for (int c = 0; c < AKB / 64; c++) {
-      const int c0 = 64 * c;
-      if (c0 >= nk32) break;
-#pragma unroll
-      for (int it = 0; it < 4; it++) {
-        const int dc = 4 * it + wv;  // lane: key, dc: 8-dim chunk
-        const u32x4 v = vr[c][it];
-        s_vt[8 * dc + 0][lane] = (uint16_t)v.x;
-        s_vt[8 * dc + 1][lane] = (uint16_t)(v.x >> 16);
-        s_vt[8 * dc + 2][lane] = (uint16_t)v.y;
-        s_vt[8 * dc + 3][lane] = (uint16_t)(v.y >> 16);
-        s_vt[8 * dc + 4][lane] = (uint16_t)v.z;
-        s_vt[8 * dc + 5][lane] = (uint16_t)(v.z >> 16);
-        s_vt[8 * dc + 6][lane] = (uint16_t)v.w;
-        s_vt[8 * dc + 7][lane] = (uint16_t)(v.w >> 16);
-      }
-      __syncthreads();
-      for (int kk = 0; kk < 2 && c0 + 32 * kk < nk32; kk++) {
-        const u32x4 vf0 = *reinterpret_cast<const u32x4*>(&s_vt[32 * wv + r16][32 * kk + 8 * kg]);
-        const u32x4 vf1 = *reinterpret_cast<const u32x4*>(&s_vt[32 * wv + 16 + r16][32 * kk + 8 * kg]);
+        for (int db = 0; db < 2; db++) {
+          const int dq = 32 * wv + 16 * db + 4 * (r16 & 3);
+          const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_v4s*)(uintptr_t)(vb + akv_off(ra, dq >> 3) + 2 * (dq & 7)));
+          const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_v4s*)(uintptr_t)(vb + akv_off(ra + 4, dq >> 3) + 2 * (dq & 7)));
+          const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+          vf[db] = u32x4{l2.x, l2.y, h2.x, h2.y};
+        }
 #pragma unroll
         for (int rb = 0; rb < 2; rb++) {
-          const u32x4 pfr = *reinterpret_cast<const u32x4*>(&s_p[16 * rb + r16][c0 + 32 * kk + 8 * kg]);
-          oacc[rb][0] = mfma_16x16x32(pfr, vf0, oacc[rb][0]);
-          oacc[rb][1] = mfma_16x16x32(pfr, vf1, oacc[rb][1]);
+          const u32x4 pfr = *reinterpret_cast<const u32x4*>(&s_p[16 * rb + r16][ACK * c + 32 * kk + 8 * kg]);
+          oacc[rb][0] = mfma_16x16x32(pfr, vf[0], oacc[rb][0]);
+          oacc[rb][1] = mfma_16x16x32(pfr, vf[1], oacc[rb][1]);
         }
       }
-      __syncthreads();
     }
-    __syncthreads();
+    ABAR();  // V buffers and s_p free for the next key block
   }
 #pragma unroll
   for (int rb = 0; rb < 2; rb++)
@@ -484,6 +495,8 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
       o[16] = (uint16_t)f2bf(oacc[rb][1][e] * inv);
     }
 }
+#undef AWAIT
+#undef ABAR
 
 // ------------------------------------------------------------------ LM head
 constexpr int LMB = 1184;  // partial-argmax blocks (the length of the reference's block_max_* buffers)
