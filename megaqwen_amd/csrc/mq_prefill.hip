@@ -309,6 +309,11 @@ constexpr int SC_PITCH = AKB + 1, P_PITCH = AKB + 8;
 
 __device__ __forceinline__ uint32_t akv_off(int row, int chunk) { return row * 256 + 16 * (chunk ^ (row & 15)); }
 
+// exp(x) as 2^(x log2 e) on the hardware exp2 (v_exp_f32): about 2^-20 relative error for
+// the arguments of the softmax (x <= 0), the accuracy class of the vectorised exp that
+// torch's CPU flash-attention kernel uses (exp_u20); exp(-inf) = 0.
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
 // Rows k0 .. k0 + ACK - 1 of a K or V cache head (rows past klast repeat row klast) into
 // the chunk buffer at LDS address `lds`: instruction q moves rows 4q .. 4q + 3, lane ->
 // row 4q + lane / 16, slot lane % 16.
@@ -419,7 +424,7 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
 #pragma unroll
         for (int u = 0; u < AKB / 64; u++) {
           const int cc = lane + 64 * u;
-          const float ev = expf(x[i][u] - base);
+          const float ev = exp_fast(x[i][u] - base);
           const float e = cc < nk ? ev : 0.f;
           sum[i] += e;
           s_p[rl][cc] = (uint16_t)f2bf(e);
