@@ -97,10 +97,13 @@ int mq_decode_layer(const void* hidden_in, void* hidden_out, const LDGLayerWeigh
  *   Scratch (bf16, device, caller-owned, as the reference sizes them):
  *     hidden_bf16 [seq_len, 1024], normalized [seq_len, 1024], q_proj [seq_len, 2048],
  *     k_proj / v_proj [seq_len, 1024], attn_out [seq_len, 2048], mlp_norm [seq_len, 1024],
- *     mlp_intermediate [seq_len, 3072], final_hidden [1024] (final-norm output of the
- *     last row), block_max_vals f32 [1184], block_max_idxs i32 [1184].
- *     residual, o_proj_out, gate_out, up_out and down_out are accepted and unused
- *     (the epilogues fuse those steps); they may be NULL.
+ *     mlp_intermediate [seq_len, 3072], gate_out / up_out [seq_len, 3072] (here they,
+ *     q_proj and k_proj | v_proj hold fp32 partial sums of the k-split o_proj and
+ *     down_proj products once the attention has consumed q, k and v),
+ *     final_hidden [1024] (final-norm output of the last row), block_max_vals f32
+ *     [1184], block_max_idxs i32 [1184]. Every buffer needs 16-byte alignment.
+ *     residual, o_proj_out and down_out are accepted and unused (the epilogues fuse
+ *     those steps); they may be NULL.
  *   hidden_bf16_out [1024]: the last row's final hidden state (before the final norm).
  *   On return (stream-ordered): *output_token_id = argmax of the last row's bf16
  *   logits (lowest index on ties), or -2 if an input id was outside [0, 151936). */

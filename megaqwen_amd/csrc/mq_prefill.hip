@@ -3,16 +3,17 @@
 // Replaces launch_prefill_float (csrc/megakernel/fused_prefill.cu:601-867): the
 // prompt's hidden states go through every layer as [S, *] bf16 matrices, K/V
 // slots 0..S-1 of every layer are written, and the greedy next token is taken
-// from the last row. Per layer:
-//   rmsnorm_rows -> gemm_nt (q, k, v in one launch) -> qk_rope_kv (QK-norm,
-//   RoPE, K/V append) -> attn_prefill (causal, MFMA) -> gemm_nt (o_proj + residual)
-//   -> rmsnorm_rows -> gemm_nt (gate and up, SiLU(gate) * up epilogue)
-//   -> gemm_nt (down_proj + residual)
+// from the last row. After embed_rows and the first layer's rmsnorm_rows, per layer:
+//   gemm_nt (q, k, v in one launch) -> qk_rope_kv (QK-norm, RoPE, K/V append)
+//   -> attn_prefill (causal, MFMA) -> gemm_nt (o_proj, k split four ways)
+//   -> resid_norm_rows (partials + residual, post-attention RMSNorm)
+//   -> gemm_nt (gate and up, SiLU(gate) * up epilogue) -> gemm_nt (down_proj, k split)
+//   -> resid_norm_rows (partials + residual, the next layer's input RMSNorm)
 // then lm_partial (final norm of the last row, tied LM head, per-block argmax) and
 // argmax_final. The GEMMs run on v_mfma_f32_16x16x32_bf16 with fp32 accumulation.
 //
-// The intermediates live in the caller's scratch buffers (the reference's own
-// argument list), so a launch allocates nothing.
+// The intermediates, the fp32 partial sums included, live in the caller's scratch
+// buffers (the reference's own argument list), so a launch allocates nothing.
 //
 // Numerics are HF Qwen3's bf16 rounding points, as in the decode kernel. The
 // attention reproduces torch's CPU flash kernel (the sdpa path HF runs on the
@@ -35,57 +36,78 @@ namespace pf {
 
 // ------------------------------------------------------------------ GEMM
 // C[m, n] = sum_k A[m, k] * W[n, k] (both operands k-contiguous, HF nn.Linear
-// layout), one TM x 64 output tile per workgroup, k in steps of 64.
+// layout), one TM x TN output tile per workgroup, k in steps of 64.
 //
 // Operand tiles move from global memory straight into LDS (global_load_lds_dwordx4,
-// no register staging) through NST LDS stages, so NST - 1 k-steps are in flight
-// while one is multiplied: the k loop runs at the rate the CU can stream operands
-// rather than one memory latency per step. A stage holds the A tile (TM rows) and
-// then the B tile (64 rows), each row as eight 16-byte chunks XOR-swizzled with
-// the row, so that the 8 rows a quarter-wave reads in one fragment load fall in
-// distinct banks. A DMA instruction writes 64 consecutive chunk slots (lane l ->
-// slot base + l), so the swizzle is applied on the source side: the lane that owns
-// slot s fetches the chunk that belongs there.
+// no register staging) through NST LDS stages, so NST - 1 stages are in flight
+// while one is multiplied. A stage holds KS consecutive 64-wide k-steps, each as the
+// A tile (TM rows) and then the B tile (TN rows), each row as eight 16-byte chunks
+// XOR-swizzled with the row, so that the 8 rows a quarter-wave reads in one fragment
+// load fall in distinct banks. A DMA instruction writes 64 consecutive chunk slots
+// (lane l -> slot base + l), so the swizzle is applied on the source side: the lane
+// that owns slot s fetches the chunk that belongs there.
 //
-// The four waves form a 2 x 2 grid: wave (wm, wn) owns rows 32wm.. (TM = 64) or
-// 16wm.. (TM = 32) of the tile and two 16-column blocks, so every 16-byte
-// fragment read from LDS feeds one or two MFMAs. TM = 32 is used for the N = 1024
-// products (o_proj, down_proj) so that a 512-row prompt still gives 256 workgroups.
-constexpr int TK = 64, GT = 256;
+// The WM x WN waves tile the output: wave (wm, wn) owns TM / WM rows and TN / WN
+// columns, as 16 x 16 MFMA blocks. A launch streams M N K 2 (1 / TM + 1 / TN) operand
+// bytes from L2 into the CUs, so tiles are large (128 rows), and the N = 1024 products
+// split k over blockIdx.z (EPI_PART: fp32 partial sums, added up by the row kernel
+// that follows) so that their grid still fills the 256 CUs.
+constexpr int TK = 64;
 
-enum : int { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2 };
+enum : int { EPI_STORE = 0, EPI_SILU = 1, EPI_PART = 2 };
 
 struct GemmSeg {
   const uint16_t* w;   // weight rows [n, k]; EPI_SILU: gate_proj rows
   const uint16_t* w2;  // EPI_SILU: up_proj rows
   uint16_t* out;       // [m, ldo] bf16
-  int ntiles;          // column tiles of this segment (EPI_SILU: 32 units each)
+  int ntiles;          // column tiles of this segment (EPI_SILU: TN / 2 units each)
   int ldo;
+};
+// EPI_PART output: the fp32 partial sums of one k split over a [m, 1024] output, as two
+// 512-column halves, each with its own base and row pitch (in floats), so that a set
+// can live in one [m, 1024] fp32 buffer (hi = lo + 512, ld = 1024) or in two buffers of
+// 2 KB rows (ld = 512)
+constexpr int MAX_SPLIT = 4, PART_HALF = 512;
+struct PartSet {
+  float* lo[MAX_SPLIT];
+  float* hi[MAX_SPLIT];
+  int ld[MAX_SPLIT];
+  int n;
 };
 struct GemmArgs {
   const uint16_t* a;  // [m, lda] bf16
   int lda, m, k, nseg;
   GemmSeg seg[3];
+  PartSet part;  // EPI_PART: set z takes the partial sums of k split z (blockIdx.z)
 };
 
 // LDS slot (in 16-byte chunks) of chunk kc (0..7) of tile row r.
 __device__ __forceinline__ int tslot(int r, int kc) { return r * 8 + (kc ^ (r & 7)); }
 
-template <int EPI, int TM, int TN, int NST, int KS>
-__global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
-  constexpr int RB = TM / 32;             // 16-row blocks per wave
-  constexpr int CB = TN / 32;             // 16-column blocks per wave
+template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
+  constexpr int NW = WM * WN, NT = 64 * NW;
+  constexpr int RB = TM / (16 * WM);      // 16-row blocks per wave
+  constexpr int CB = TN / (16 * WN);      // 16-column blocks per wave
   constexpr int HB = TN / 32;             // EPI_SILU: gate (and up) blocks per tile
   constexpr int ACH = TM * 8, BCH = TN * 8;  // chunk slots of the A and B tiles
-  constexpr int SCH = ACH + BCH;          // slots per stage
-  constexpr int NI = SCH / GT;            // DMA instructions per thread and stage: 4 or 3
-  static_assert(ACH % 64 == 0 && SCH % GT == 0, "a DMA instruction covers 64 slots of one operand");
-  __shared__ u32x4 sbuf[NST][KS][SCH];  // a stage holds KS consecutive 64-wide k-steps
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv >> 1, wn = wv & 1;
-  int nt = blockIdx.x, si = 0;
+  constexpr int SCH = ACH + BCH;          // slots per k-step
+  constexpr int NI = KS * SCH / NT;       // DMA instructions per thread and stage
+  static_assert(RB * 16 * WM == TM && CB * 16 * WN == TN, "waves tile the output");
+  static_assert(EPI != EPI_SILU || CB % 2 == 0, "a wave pairs each gate block with its up block");
+  static_assert(ACH % 64 == 0 && BCH % 64 == 0 && (KS * SCH) % NT == 0,
+                "a DMA instruction covers 64 slots of one operand of one k-step");
+  __shared__ u32x4 sbuf[NST][KS][SCH];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv / WN, wn = wv % WN;
+  int nt = blockIdx.x;
+  const int mt = blockIdx.y, z = blockIdx.z;  // column tile, row tile, k split
+  int si = 0;
   while (si + 1 < G.nseg && nt >= G.seg[si].ntiles) nt -= G.seg[si++].ntiles;
   const GemmSeg S = G.seg[si];
-  const int m0 = blockIdx.y * TM;
+  const int m0 = mt * TM;
+  const int kp = G.k / (int)gridDim.z, kz = kp * z;  // this split's k range
+  const int KT = kp / (TK * KS);
+
   // the wave's column blocks; EPI_SILU: blocks j < CB / 2 are gate blocks, each paired with
   // the up block j + CB / 2 (gate rows are the tile's first TN / 2 rows, up rows the rest)
   int jb[CB];
@@ -93,39 +115,38 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
   for (int j = 0; j < CB; j++)
     jb[j] = EPI == EPI_SILU ? (j < CB / 2 ? (CB / 2) * wn + j : HB + (CB / 2) * wn + j - CB / 2) : CB * wn + j;
 
-  // DMA instruction i of this wave fills slots 64 (4 i + wv) .. +63 of a stage
+  // DMA instruction i of this wave fills the 64 slots 64 b .. 64 b + 63 of a stage,
+  // b = NW i + wv, counted over the stage's KS k-steps
   const uint16_t* src[NI];
   uint32_t dst[NI];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sbuf[0][0][0];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
-    const int s0 = 64 * (4 * i + wv), sl = s0 + lane;
-    dst[i] = __builtin_amdgcn_readfirstlane(lds0 + 16u * (uint32_t)s0);  // wave-uniform (M0)
+    const int b0 = 64 * (NW * i + wv), q = b0 / SCH, s0 = b0 % SCH, sl = s0 + lane;
+    dst[i] = __builtin_amdgcn_readfirstlane(lds0 + 16u * (uint32_t)b0);  // wave-uniform (M0)
+    const uint16_t* p;
     if (s0 < ACH) {
       const int r = sl >> 3, kc = (sl & 7) ^ (r & 7);
       const int row = min(m0 + r, G.m - 1);  // rows past the prompt repeat its last row (never stored)
-      src[i] = G.a + (size_t)row * G.lda + 8 * kc;
+      p = G.a + (size_t)row * G.lda + 8 * kc;
     } else {
       const int t = sl - ACH, r = t >> 3, kc = (t & 7) ^ (r & 7);
       if (EPI == EPI_SILU)
-        src[i] = (r < TN / 2 ? S.w + (size_t)(TN / 2 * nt + r) * G.k : S.w2 + (size_t)(TN / 2 * nt + r - TN / 2) * G.k) +
-                 8 * kc;
+        p = (r < TN / 2 ? S.w + (size_t)(TN / 2 * nt + r) * G.k : S.w2 + (size_t)(TN / 2 * nt + r - TN / 2) * G.k) +
+            8 * kc;
       else
-        src[i] = S.w + (size_t)(TN * nt + r) * G.k + 8 * kc;
+        p = S.w + (size_t)(TN * nt + r) * G.k + 8 * kc;
     }
+    src[i] = p + kz + TK * q;
   }
-  const int KT = G.k / (TK * KS);
-  // stage kt % NST <- k-steps KS kt .. KS kt + KS - 1; steps past the end re-load the last
-  // ones (kept uniform so that every wave issues the same number of DMAs and the vmcnt
-  // waits below are exact)
+  // stage kt % NST <- k-steps KS kt .. KS kt + KS - 1 of the split; steps past the end
+  // re-load the last ones (kept uniform so that every wave issues the same number of DMAs
+  // and the vmcnt waits below are exact)
   auto issue = [&](int kt) {
     const int kk = min(kt, KT - 1) * TK * KS;
+    const uint32_t so = 16u * (uint32_t)(KS * SCH * (kt % NST));
 #pragma unroll
-    for (int q = 0; q < KS; q++) {
-      const uint32_t so = 16u * (uint32_t)(SCH * (KS * (kt % NST) + q));
-#pragma unroll
-      for (int i = 0; i < NI; i++) dma16(src[i] + kk + TK * q, dst[i] + so);
-    }
+    for (int i = 0; i < NI; i++) dma16(src[i] + kk, dst[i] + so);
   };
 
   f32x4 acc[RB][CB];
@@ -136,9 +157,9 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
 #pragma unroll
   for (int kt = 0; kt < NST - 1; kt++) issue(kt);
   for (int kt = 0; kt < KT; kt++) {
-    // this wave's DMAs of step kt have landed (the NST - 2 later steps may still fly);
-    // the barrier publishes every wave's, and tells that step kt - 1's stage is free
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NST - 2) * NI * KS) : "memory");
+    // this wave's DMAs of stage kt have landed (the NST - 2 later stages may still fly);
+    // the barrier publishes every wave's, and tells that stage kt - 1 is free
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NST - 2) * NI) : "memory");
     __syncthreads();
     issue(kt + NST - 1);
 #pragma unroll
@@ -170,6 +191,14 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
     for (int e = 0; e < 4; e++) {
       const int row = m0 + 16 * (RB * wm + i) + rq + e;
       if (row >= G.m) continue;
+      if (EPI == EPI_PART) {
+        static_assert(PART_HALF % TN == 0, "a tile lies in one column half");
+        const int c0 = TN * nt;
+        float* prow = (c0 < PART_HALF ? G.part.lo[z] : G.part.hi[z]) + (size_t)row * G.part.ld[z] + c0 % PART_HALF;
+#pragma unroll
+        for (int j = 0; j < CB; j++) prow[16 * jb[j] + col] = acc[i][j][e];
+        continue;
+      }
       uint16_t* orow = S.out + (size_t)row * S.ldo;
       if (EPI == EPI_SILU) {
         // HF Qwen3MLP (modeling_qwen3.py:81-83): down(bf16(silu(bf16 gate)) * bf16 up)
@@ -181,12 +210,7 @@ __global__ void __launch_bounds__(GT) gemm_nt(GemmArgs G) {
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < CB; j++) {
-          const int c = TN * nt + 16 * jb[j] + col;
-          float v = rbf(acc[i][j][e]);
-          if (EPI == EPI_RESID) v = bf2f(orow[c]) + v;  // residual add, rounded once more
-          orow[c] = (uint16_t)f2bf(v);
-        }
+        for (int j = 0; j < CB; j++) orow[TN * nt + 16 * jb[j] + col] = (uint16_t)f2bf(acc[i][j][e]);
       }
     }
 }
@@ -234,6 +258,69 @@ __global__ void __launch_bounds__(64) rmsnorm_rows(const uint16_t* x, const uint
       o.w = pack_bf2(rbf(wf[6] * rbf(f[h][6] * rstd)), rbf(wf[7] * rbf(f[h][7] * rstd)));
       reinterpret_cast<u32x4*>(yr + 512 * h)[lane] = o;
     }
+  }
+}
+
+// The row step after a k-split residual product (o_proj or down_proj): the split's fp32
+// partial sums of row r added in split order and rounded to bf16 (the Linear output),
+// the residual add h = bf16(h + y) (modeling_qwen3.py:316,322), and, when w is given,
+// the next RMSNorm of the new row into y_norm, as rmsnorm_rows computes it. One
+// single-wave workgroup per row; lane l owns columns 8l .. 8l + 7 and 512 + 8l .. +7.
+__global__ void __launch_bounds__(64) resid_norm_rows(PartSet ps, uint16_t* h, const uint16_t* w, uint16_t* y, int m) {
+  static_assert(2 * PART_HALF == H, "a partial set is two column halves");
+  const int row = blockIdx.x, lane = threadIdx.x;
+  if (row >= m) return;
+  typedef const __attribute__((address_space(1))) f32x4 gf32x4;
+  auto load = [&](int s, f32x4 (&v)[2][2]) {
+    const float* half[2] = {ps.lo[s] + (size_t)row * ps.ld[s], ps.hi[s] + (size_t)row * ps.ld[s]};
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+      for (int u = 0; u < 2; u++) v[hh][u] = *(gf32x4*)(half[hh] + 8 * lane + 4 * u);
+  };
+  f32x4 a[2][2];
+  load(0, a);
+  for (int s = 1; s < ps.n; s++) {
+    f32x4 b[2][2];
+    load(s, b);
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+      for (int u = 0; u < 2; u++) a[hh][u] += b[hh][u];
+  }
+  uint16_t* hr = h + (size_t)row * H;
+  float f[2][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++) {
+    float r[8];
+    unpack8(ldw(hr + 512 * hh + 8 * lane), r);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      f[hh][i] = rbf(r[i] + rbf(a[hh][i >> 2][i & 3]));
+      ss = fmaf(f[hh][i], f[hh][i], ss);
+    }
+    u32x4 o;
+    o.x = pack_bf2(f[hh][0], f[hh][1]);
+    o.y = pack_bf2(f[hh][2], f[hh][3]);
+    o.z = pack_bf2(f[hh][4], f[hh][5]);
+    o.w = pack_bf2(f[hh][6], f[hh][7]);
+    reinterpret_cast<u32x4*>(hr + 512 * hh)[lane] = o;
+  }
+  if (!w) return;
+  ss = wave_sum(ss);
+  const float rstd = 1.0f / sqrtf(ss * (1.0f / H) + EPS);
+  uint16_t* yr = y + (size_t)row * H;
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++) {
+    float wf[8];
+    unpack8(ldw(w + 512 * hh + 8 * lane), wf);
+    u32x4 o;
+    o.x = pack_bf2(rbf(wf[0] * rbf(f[hh][0] * rstd)), rbf(wf[1] * rbf(f[hh][1] * rstd)));
+    o.y = pack_bf2(rbf(wf[2] * rbf(f[hh][2] * rstd)), rbf(wf[3] * rbf(f[hh][3] * rstd)));
+    o.z = pack_bf2(rbf(wf[4] * rbf(f[hh][4] * rstd)), rbf(wf[5] * rbf(f[hh][5] * rstd)));
+    o.w = pack_bf2(rbf(wf[6] * rbf(f[hh][6] * rstd)), rbf(wf[7] * rbf(f[hh][7] * rstd)));
+    reinterpret_cast<u32x4*>(yr + 512 * hh)[lane] = o;
   }
 }
 
@@ -617,16 +704,17 @@ __global__ void __launch_bounds__(256) argmax_final(const float* bmv, const int*
 using namespace mq;
 using namespace mq::pf;
 
-// GEMM pipelines (measured on MI355X at S = 512): 64-row tiles keep two 128-wide k stages
-// (64 KB of LDS, two workgroups per CU), 32-row tiles four (96 KB, one per CU)
-constexpr int NST64 = 2, NST32 = 4, KS2 = 2;
-// tile widths of the four products
-constexpr int TN_QKV = 64, TN_GU = 64, TN_RES = 64;
+// GEMM shapes (measured on MI355X at S = 512 with the weights cold, as each layer's are):
+// eight-wave workgroups with 128-row tiles and a four-stage ring of 64-wide k-steps;
+// o_proj and down_proj split k four ways into fp32 partials, so that each of their 256
+// workgroups streams (128 + 64) rows instead of (32 + 64) rows over a quarter of k
+constexpr int GST = 4, GKS = 1, GWM = 4, GWN = 2;
+constexpr int TM_G = 128, TN_QKV = 64, TN_GU = 128, TN_RES = 64, RES_SPLIT = 4;
 
-// one launch of gemm_nt over a [m, sum of the segments' widths] output
-template <int EPI, int TM, int TN, int NST, int KS>
-void gemm(const GemmArgs& g, int ntiles, hipStream_t stream) {
-  gemm_nt<EPI, TM, TN, NST, KS><<<dim3(ntiles, (g.m + TM - 1) / TM), GT, 0, stream>>>(g);
+// one launch of gemm_nt over a [m, sum of the segments' widths] output, k split `split` ways
+template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
+void gemm(const GemmArgs& g, int ntiles, hipStream_t stream, int split = 1) {
+  gemm_nt<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, (g.m + TM - 1) / TM, split), 64 * WM * WN, 0, stream>>>(g);
 }
 
 extern "C" int launch_prefill_float(const int* input_token_ids, int* output_token_id, int seq_len,
@@ -638,11 +726,11 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
                                     void* mlp_intermediate, void* down_out, void* final_hidden, void* block_max_vals,
                                     void* block_max_idxs, void* hidden_bf16_out, int num_layers, int max_seq_len,
                                     float attn_scale, hipStream_t stream) {
-  (void)residual; (void)o_proj_out; (void)gate_out; (void)up_out; (void)down_out;
+  (void)residual; (void)o_proj_out; (void)down_out;
   if (!input_token_ids || !output_token_id || !embed_weight || !layer_weights || !final_norm_weight ||
       !lm_head_weight || !cos_table || !sin_table || !k_cache || !v_cache || !hidden_bf16 || !normalized ||
-      !q_proj || !k_proj || !v_proj || !attn_out || !mlp_norm || !mlp_intermediate || !final_hidden ||
-      !block_max_vals || !block_max_idxs || !hidden_bf16_out)
+      !q_proj || !k_proj || !v_proj || !attn_out || !mlp_norm || !gate_out || !up_out || !mlp_intermediate ||
+      !final_hidden || !block_max_vals || !block_max_idxs || !hidden_bf16_out)
     return MQ_ERR_ARG;
   if (seq_len < 1 || max_seq_len < 1 || seq_len > max_seq_len || num_layers < 1 || num_layers > MAX_LAYERS ||
       !(attn_scale > 0.f) || !isfinite(attn_scale))
@@ -678,20 +766,36 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     if (e != hipSuccess && launch_err == hipSuccess) launch_err = e;
   };
   (void)hipGetLastError();  // clear an error left by an unrelated earlier call
+  // fp32 partial sums of the k-split o_proj and down_proj, [S, 1024] a split, in scratch
+  // that is dead while they live: gate_out and up_out (unused otherwise), q_proj (read by
+  // the attention before o_proj) and k_proj | v_proj as the two column halves of the
+  // fourth set (both read by qk_rope_kv before the attention)
+  auto f32 = [](void* p) { return static_cast<float*>(p); };
+  PartSet parts{};
+  parts.n = RES_SPLIT;
+  float* const whole[3] = {f32(gate_out), f32(up_out), f32(q_proj)};
+  for (int z = 0; z < 3; z++) {
+    parts.lo[z] = whole[z];
+    parts.hi[z] = whole[z] + PART_HALF;
+    parts.ld[z] = H;
+  }
+  parts.lo[3] = f32(k_proj);
+  parts.hi[3] = f32(v_proj);
+  parts.ld[3] = PART_HALF;
   embed_rows<<<S, 128, 0, stream>>>(input_token_ids, bf(embed_weight), h, err);
+  chk();
+  rmsnorm_rows<<<S, 64, 0, stream>>>(h, bf(layer_weights[0].input_layernorm_weight), nrm, S);
   chk();
   for (int l = 0; l < num_layers; l++) {
     const PrefillLayerWeights& w = layer_weights[l];
     uint16_t* kcl = bfm(k_cache) + l * kv_layer;
     uint16_t* vcl = bfm(v_cache) + l * kv_layer;
-    rmsnorm_rows<<<S, 64, 0, stream>>>(h, bf(w.input_layernorm_weight), nrm, S);
-    chk();
     GemmArgs g{};
     g.a = nrm; g.lda = H; g.m = S; g.k = H; g.nseg = 3;
     g.seg[0] = GemmSeg{bf(w.q_proj_weight), nullptr, qp, QS / TN_QKV, QS};
     g.seg[1] = GemmSeg{bf(w.k_proj_weight), nullptr, kp, KVS / TN_QKV, KVS};
     g.seg[2] = GemmSeg{bf(w.v_proj_weight), nullptr, vp, KVS / TN_QKV, KVS};
-    gemm<EPI_STORE, 64, TN_QKV, NST64, KS2>(g, (QS + 2 * KVS) / TN_QKV, stream);
+    gemm<EPI_STORE, TM_G, TN_QKV, GST, GKS, GWM, GWN>(g, (QS + 2 * KVS) / TN_QKV, stream);
     chk();
     qk_rope_kv<<<S, 256, 0, stream>>>(qp, kp, vp, bf(w.q_norm_weight), bf(w.k_norm_weight), bf(cos_table),
                                       bf(sin_table), kcl, vcl, max_seq_len);
@@ -700,20 +804,26 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     chk();
     GemmArgs go{};
     go.a = att; go.lda = QS; go.m = S; go.k = QS; go.nseg = 1;
-    go.seg[0] = GemmSeg{bf(w.o_proj_weight), nullptr, h, H / TN_RES, H};
-    gemm<EPI_RESID, 32, TN_RES, NST32, KS2>(go, H / TN_RES, stream);
+    go.seg[0] = GemmSeg{bf(w.o_proj_weight), nullptr, nullptr, H / TN_RES, H};
+    go.part = parts;
+    gemm<EPI_PART, TM_G, TN_RES, GST, GKS, GWM, GWN>(go, H / TN_RES, stream, RES_SPLIT);
     chk();
-    rmsnorm_rows<<<S, 64, 0, stream>>>(h, bf(w.post_attn_layernorm_weight), mln, S);
+    resid_norm_rows<<<S, 64, 0, stream>>>(parts, h, bf(w.post_attn_layernorm_weight), mln, S);
     chk();
     GemmArgs gu{};
     gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
     gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, I / (TN_GU / 2), I};
-    gemm<EPI_SILU, 64, TN_GU, NST64, KS2>(gu, I / (TN_GU / 2), stream);
+    gemm<EPI_SILU, TM_G, TN_GU, GST, GKS, GWM, GWN>(gu, I / (TN_GU / 2), stream);
     chk();
     GemmArgs gd{};
     gd.a = mid; gd.lda = I; gd.m = S; gd.k = I; gd.nseg = 1;
-    gd.seg[0] = GemmSeg{bf(w.down_proj_weight), nullptr, h, H / TN_RES, H};
-    gemm<EPI_RESID, 32, TN_RES, NST32, KS2>(gd, H / TN_RES, stream);
+    gd.seg[0] = GemmSeg{bf(w.down_proj_weight), nullptr, nullptr, H / TN_RES, H};
+    gd.part = parts;
+    gemm<EPI_PART, TM_G, TN_RES, GST, GKS, GWM, GWN>(gd, H / TN_RES, stream, RES_SPLIT);
+    chk();
+    // the next layer's input RMSNorm (none after the last: the final norm is the LM head's)
+    resid_norm_rows<<<S, 64, 0, stream>>>(parts, h, l + 1 < num_layers ? bf(layer_weights[l + 1].input_layernorm_weight) : nullptr,
+                                          nrm, S);
     chk();
   }
   lm_partial<<<LMB, 256, 0, stream>>>(h + (size_t)(S - 1) * H, bf(final_norm_weight), bf(lm_head_weight),

@@ -219,6 +219,9 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
         self.v_proj_ = torch.empty(P, KV_SIZE, **bf)
         self.attn_out_ = torch.empty(P, Q_SIZE, **bf)
         self.mlp_norm_ = torch.empty(P, HIDDEN_SIZE, **bf)
+        # gate_out / up_out hold the kernel's fp32 k-split partial sums (4 KB a row)
+        self.gate_out_ = torch.empty(P, INTERMEDIATE_SIZE, **bf)
+        self.up_out_ = torch.empty(P, INTERMEDIATE_SIZE, **bf)
         self.mlp_intermediate_ = torch.empty(P, INTERMEDIATE_SIZE, **bf)
         self.final_hidden_ = torch.empty(HIDDEN_SIZE, **bf)
         self.input_tokens_ = torch.empty(P, dtype=torch.int32, device=dev)
@@ -237,7 +240,7 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
             ctypes.addressof(self.h_layer_weights_), _ptr(self.final_norm_weight_), _ptr(self.lm_head_weight_),
             _ptr(self.cos_table_), _ptr(self.sin_table_), _ptr(self.k_cache_), _ptr(self.v_cache_),
             _ptr(self.hidden_float_), None, _ptr(self.normalized_), _ptr(self.q_proj_), _ptr(self.k_proj_),
-            _ptr(self.v_proj_), _ptr(self.attn_out_), None, _ptr(self.mlp_norm_), None, None,
+            _ptr(self.v_proj_), _ptr(self.attn_out_), None, _ptr(self.mlp_norm_), _ptr(self.gate_out_), _ptr(self.up_out_),
             _ptr(self.mlp_intermediate_), None, _ptr(self.final_hidden_), _ptr(self.block_max_vals_),
             _ptr(self.block_max_idxs_), _ptr(self.hidden_buffer_), self.num_layers_, self.max_seq_len_,
             self.attn_scale_, _stream())

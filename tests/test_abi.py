@@ -85,15 +85,17 @@ def _prefill_args(**over):
              v=1, num_layers=2, max_seq_len=16, scale=0.088)
     a.update(over)
     scratch = [1] * 17
-    scratch[1] = scratch[7] = scratch[9] = scratch[10] = scratch[12] = None  # unused by this build
+    scratch[1] = scratch[7] = scratch[12] = None  # unused by this build
     if a.pop("null_scratch", False):
         scratch[3] = None  # q_proj
+    if a.pop("null_partials", False):
+        scratch[10] = None  # up_out: holds partial sums in this build
     return layers, [a["ids"], a["out"], a["seq_len"], a["embed"], a["layers"], a["norm"], a["lm"], a["cos"],
                     a["sin"], a["k"], a["v"]] + scratch + [a["num_layers"], a["max_seq_len"], a["scale"], None]
 
 
 @pytest.mark.parametrize("bad", [
-    dict(ids=None), dict(out=None), dict(layers=None), dict(k=None), dict(null_scratch=True),
+    dict(ids=None), dict(out=None), dict(layers=None), dict(k=None), dict(null_scratch=True), dict(null_partials=True),
     dict(null_layer_field=True), dict(seq_len=0), dict(seq_len=17), dict(num_layers=0), dict(num_layers=33),
     dict(max_seq_len=0), dict(scale=0.0), dict(scale=float("inf")),
 ])
