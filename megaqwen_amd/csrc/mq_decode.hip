@@ -24,10 +24,11 @@
 //   * reduce wave 6 sums the eight XCDs' o_proj and down_proj partials of the
 //     workgroup's 32 residual rows and applies the residual adds.
 //   * store wave 7 publishes the stream waves' dot products (handed over
-//     through LDS) and the K/V append. In the instance for contexts of at most
-//     256 positions the store waves of the 31 workgroups without attention also
-//     warm the XCD's L2 with the attention workgroup's next K/V rows and weight
-//     rows, which it would otherwise copy from HBM on its critical path.
+//     through LDS) and the K/V append. For contexts of at most 256 positions, and
+//     for contexts split over at most three workgroups, the store waves of the
+//     workgroups without attention also warm the XCD's L2 with the attention
+//     workgroups' next K/V rows and weight rows, which they would otherwise copy
+//     from HBM on their critical path.
 // Per layer and workgroup (g, j):
 //   q/k/v : rows 16j .. 16j+15 of the group's [q0; q1; k; v]
 //   attn  : workgroups j < nsplit attend over chunk j (<= 256 positions) for the
@@ -88,6 +89,7 @@ constexpr int UNITS = I / NWG;                // MLP units per workgroup: 12
 constexpr int XUNITS = I / NXCD;              // MLP units per XCD: 384
 constexpr int KV_CAP = 256;                       // positions per LDS pass of an attention workgroup
 constexpr int MAX_CTX = 2 * WG_PER_XCD * KV_CAP;  // 16384: at most two passes per workgroup
+constexpr int SPLIT_WARM_MAX = 3;  // split contexts whose next-layer rows are warmed in L2
 constexpr int LM_PRE = 4;                     // LM-head rows each stream wave loads during the last layer
 // Attention workgroups issue a layer's K/V copy in the previous layer's gate/up stage;
 // only the layer's o_proj loads (4) follow it before attention.
@@ -302,6 +304,47 @@ __device__ __forceinline__ void att_weight_warm(const uint16_t* const* wl, const
     } else {
       const int u = t - NQL - NOL - 2 * NGL, row = u / 6;
       a = reinterpret_cast<const uint8_t*>(uniform_ptr(wl[W_D]) + (size_t)row * I + XUNITS * g) + 128 * (u - 6 * row);
+    }
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(a), "s"(lds)
+                 : "memory");
+  }
+}
+
+// The same for the attention workgroups j < na of a split context: the weight rows that
+// they load during this layer after their attention (gate and up rows 384g + 12j .. +11; down_proj rows
+// 32j .. 32j+31, columns 384g .. 384g+383) and at the end of it for the next layer (the
+// q/k/v rows 16j .. 16j+15 of the group's [q0; q1; k; v]; o_proj rows 32j .. 32j+31,
+// columns 256g .. 256g+255): 960 128-byte lines per workgroup, one 4-byte LDS DMA each,
+// line t on worker t % nworkers (the same workers as kv_warm).
+// `wl` is the layer's and `wn` the next layer's weight-pointer row.
+__device__ __forceinline__ void att_weight_warm_n(const uint16_t* const* wl, const uint16_t* const* wn, int g, int na,
+                                                uint32_t lds, int wk, int nworkers, int lane) {
+  constexpr int NQL = 16 * 16, NOL = 32 * 4, NGL = 12 * 16, NDL = 32 * 6;  // lines per part
+  constexpr int NL = NQL + NOL + 2 * NGL + NDL;
+  for (int t = 64 * wk + lane; t < na * NL; t += 64 * nworkers) {
+    const int ja = t / NL, v = t - NL * ja;
+    const uint8_t* a;
+    if (v < NQL) {
+      const int r = 16 * ja;
+      const uint16_t* w = r < 256   ? uniform_ptr(wn[W_Q]) + (size_t)(256 * g + r) * H
+                          : r < 384 ? uniform_ptr(wn[W_K]) + (size_t)(128 * g + r - 256) * H
+                                    : uniform_ptr(wn[W_V]) + (size_t)(128 * g + r - 384) * H;
+      a = reinterpret_cast<const uint8_t*>(w) + 128 * v;
+    } else if (v < NQL + NOL) {
+      const int u = v - NQL;
+      a = reinterpret_cast<const uint8_t*>(uniform_ptr(wn[W_O]) + (size_t)(ROWS * ja + (u >> 2)) * QS + 256 * g) +
+          128 * (u & 3);
+    } else if (v < NQL + NOL + 2 * NGL) {
+      const int u = v - NQL - NOL;
+      const uint16_t* w = uniform_ptr(wl[u < NGL ? W_G : W_U]);
+      a = reinterpret_cast<const uint8_t*>(w + (size_t)(XUNITS * g + UNITS * ja) * H) + 128 * (u < NGL ? u : u - NGL);
+    } else {
+      const int u = v - NQL - NOL - 2 * NGL, row = u / 6;
+      a = reinterpret_cast<const uint8_t*>(uniform_ptr(wl[W_D]) + (size_t)(ROWS * ja + row) * I + XUNITS * g) +
+          128 * (u - 6 * row);
     }
     uint32_t saved;
     asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
@@ -1186,6 +1229,13 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         // and the attention workgroup's weight rows of its stages after attention
         att_weight_warm(s_lw[layer], s_lw[layer + 1], g, lds_kv, j - 1, WG_PER_XCD - 1, lane);
       }
+      // the same for a context split over at most SPLIT_WARM_MAX workgroups (measured: it
+      // gains at two and three, and costs from five up, where the copies grow and the
+      // workers fall to 27 or fewer)
+      if (SPLIT && !att && nsplit <= SPLIT_WARM_MAX && layer + 1 < L) {
+        kv_warm(P, layer + 1, g, p, lds_kv, j - nsplit, WG_PER_XCD - nsplit, lane);
+        att_weight_warm_n(s_lw[layer], s_lw[layer + 1], g, nsplit, lds_kv, j - nsplit, WG_PER_XCD - nsplit, lane);
+      }
       if (att) {
         float M0 = 0.f, M1 = 0.f, L0 = 0.f, L1 = 0.f, Ma0 = 0.f, Ma1 = 0.f, La0 = 0.f, La1 = 0.f;
         for (int ps = 0; ps < npass; ps++) {
@@ -1276,7 +1326,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         st2_dev(ws + X_DPART + 2 * ((j * ROWS + lane) * NXCD + g), u32x2{__float_as_uint(s_res[lane]), tag64});
         MQ_STAMP(layer * 40 + 38);
     }
-    if (!SPLIT) wait_vmem();  // the K/V warm-up copies have landed before the LM head reuses their LDS
+    wait_vmem();  // the warm-up copies have landed before the LM head reuses their LDS
     BAR();  // F1
   }
 
