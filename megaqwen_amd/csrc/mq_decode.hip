@@ -1056,40 +1056,42 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         }
       } else {
         // every workgroup merges the XCD's chunk partials itself, straight into its o_proj
-        // input: thread pt takes dims d0, d0 + 1 of head hh, four chunks per round; a round
-        // issues all its loads, then re-polls the stale ones together
+        // input: thread pt takes dims d0, d0 + 1 of head hh (a poll wave per head), CG chunks
+        // per round; lane q loads chunk q's (m, l), which the wave then reads by readlane;
+        // a round issues all its loads, then re-polls the stale ones together
         const int hh = pt >> 6, d0 = 2 * (pt & 63);
         float Mc = -INFINITY, Lc = 0.f, O0 = 0.f, O1 = 0.f;
-        constexpr int CG = 4;
+        // nine chunks a round: contexts up to 2303 positions merge in one round (2048 and
+        // past take nine chunks); measured against 4 and 12 a round, and 6, 8 and 16 spill
+        constexpr int CG = 9;
         for (int s0 = 0; s0 < nsplit; s0 += CG) {
           const int nq = min(CG, nsplit - s0);
           const uint32_t b0 = lb + LX_PART + 2 * ((s0 * 2 + hh) * APART);
-          u32x4 ml[CG], ov[CG];  // (m, tag, l, tag) and (acc[d0], tag, acc[d0 + 1], tag)
+          const bool mlane = lane < nq;
+          const uint32_t bml = b0 + 4 * min(lane, nq - 1) * APART;
+          u32x4 ml, ov[CG];  // this lane's chunk (m, tag, l, tag); (acc[d0], tag, acc[d0 + 1], tag) per chunk
+          ml = ldl4(wsb, bml);
 #pragma unroll
           for (int q = 0; q < CG; q++)
-            if (q < nq) {
-              ml[q] = ldl4(wsb, b0 + 4 * q * APART);
-              ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
-            }
+            if (q < nq) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
           auto fresh = [&](const u32x4& v) { return (v.y == tag64) & (v.w == tag64); };
           uint32_t spins = 0;
           for (;;) {
-            bool ok = true;
+            bool ok = !mlane || fresh(ml);
 #pragma unroll
-            for (int q = 0; q < CG; q++) ok &= q >= nq || (fresh(ml[q]) & fresh(ov[q]));
+            for (int q = 0; q < CG; q++) ok &= q >= nq || fresh(ov[q]);
             if (ok || watchdog(wsb, ws, ++spins)) break;
             __builtin_amdgcn_s_sleep(1);
+            if (mlane && !fresh(ml)) ml = ldl4(wsb, bml);
 #pragma unroll
             for (int q = 0; q < CG; q++)
-              if (q < nq) {
-                if (!fresh(ml[q])) ml[q] = ldl4(wsb, b0 + 4 * q * APART);
-                if (!fresh(ov[q])) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
-              }
+              if (q < nq && !fresh(ov[q])) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
           }
 #pragma unroll
           for (int q = 0; q < CG; q++)
             if (q < nq) {
-              const float m = __uint_as_float(ml[q].x), l = __uint_as_float(ml[q].z);
+              const float m = __uint_as_float(__builtin_amdgcn_readlane(ml.x, q));
+              const float l = __uint_as_float(__builtin_amdgcn_readlane(ml.z, q));
               const float nm = fmaxf(Mc, m);
               const float ea = Mc == -INFINITY ? 0.f : expf(Mc - nm), eb = expf(m - nm);
               Lc = Lc * ea + l * eb;
