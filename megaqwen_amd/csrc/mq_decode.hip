@@ -108,6 +108,8 @@ constexpr uint32_t LX_H1 = 1024;    // [1024] residual stream after attention
 constexpr uint32_t LX_QKV = 2048;   // [512]  raw q0, q1, k, v rows of the XCD's KV group
 constexpr uint32_t LX_ATT = 2560;   // [256]  attention output of the group's two query heads
 constexpr uint32_t LX_M = 2816;     // [384]  SiLU(gate) * up of the XCD's MLP units
+constexpr uint32_t LX_HSS = 3200;   // [32] (fp32, tag) pairs: sum of squares of workgroup j's rows of h
+constexpr uint32_t LX_H1SS = 3264;  // [32] the same for h1
 constexpr uint32_t APART = 130;     // attention partial of one head: m, l, acc[128]
 constexpr uint32_t LX_PART = 4096;  // [32 chunks][2 heads][APART] (fp32, tag) pairs
 // cross-XCD partial sums: [j][row][xcd] (fp32, tag) pairs
@@ -575,34 +577,28 @@ __device__ __forceinline__ void unpack_tagged(const u32x4& v, float* f) {
   f[2] = bflo(v.z);
   f[3] = bflo(v.w);
 }
-// chunk k (uniform) of four
-__device__ __forceinline__ u32x4 pick4(const u32x4 (&v)[4], int k) {
-  return k == 0 ? v[0] : k == 1 ? v[1] : k == 2 ? v[2] : v[3];
-}
 
-// Poll waves: gather a whole 1024-word XCD-local residual-stream vector (chunks
-// lane + 64k), polled until tagged `tag`; returns the sum of squares of its values.
-__device__ __forceinline__ float gather_local(const Buf& b, uint32_t* ws, uint32_t base, uint32_t tag, int lane,
-                                              u32x4 (&v)[4]) {
-#pragma unroll
-  for (int k = 0; k < 4; k++) v[k] = ldl4(b, base + 4 * (lane + 64 * k));
-  // re-poll every stale chunk at once (one memory round trip per iteration)
+// This poll wave's half of a gathered residual stream (chunks lane + 128c into v0 and
+// lane + 128c + 64 into v1) and the stream's sum of squares, added up from the 32 per-workgroup
+// sums of squares published with it (the same order in both poll waves, so their norms
+// agree bit for bit). All three loads are issued, then the stale ones re-polled together.
+__device__ __forceinline__ float gather_half(const Buf& b, uint32_t* ws, uint32_t base, uint32_t ssbase, uint32_t tag,
+                                             uint32_t tag64, int c, int lane, u32x4& v0, u32x4& v1) {
+  const uint32_t w0 = base + 4 * (lane + 128 * c), w1 = w0 + 4 * 64;
+  const uint32_t wq = ssbase + 4 * (lane & 15);  // the sums of workgroups 2 (lane % 16) and +1
+  u32x4 a = ldl4(b, w0), e = ldl4(b, w1), q = ldl4(b, wq);
+  auto fresh = [&](const u32x4& x) { return (x.y == tag64) & (x.w == tag64); };
   uint32_t spins = 0;
-  while (!(tags_ok(v[0], tag) & tags_ok(v[1], tag) & tags_ok(v[2], tag) & tags_ok(v[3], tag))) {
+  while (!(tags_ok(a, tag) & tags_ok(e, tag) & fresh(q))) {
     if (watchdog(b, ws, ++spins)) break;
     __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-      if (!tags_ok(v[k], tag)) v[k] = ldl4(b, base + 4 * (lane + 64 * k));
+    if (!tags_ok(a, tag)) a = ldl4(b, w0);
+    if (!tags_ok(e, tag)) e = ldl4(b, w1);
+    if (!fresh(q)) q = ldl4(b, wq);
   }
-  float ss = 0.f;
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    float f[4];
-    unpack_tagged(v[k], f);
-    ss += (f[0] * f[0] + f[1] * f[1]) + (f[2] * f[2] + f[3] * f[3]);
-  }
-  return wave_sum(ss);
+  v0 = a;
+  v1 = e;
+  return wave_sum(lane < 16 ? __uint_as_float(q.x) + __uint_as_float(q.z) : 0.f);
 }
 
 // HF Qwen3RMSNorm (modeling_qwen3.py:59-64) of one chunk: y = bf16(w * bf16(x * rstd)),
@@ -914,34 +910,34 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
 
     // RMSNorm of a gathered residual-stream vector (chunks lane + 64k, k < 4): poll wave c
     // writes the normalised chunks k = 2c, 2c + 1 to s_x0
-    auto norm_out = [&](const u32x4 (&hv)[4], float ss, const uint32_t* wn) {
+    auto norm_out = [&](const u32x4& hv0, const u32x4& hv1, float ss, const uint32_t* wn) {
       const float rstd = 1.0f / sqrtf(ss * (1.0f / H) + EPS);
 #pragma unroll
       for (int q = 0; q < 2; q++) {
         const int k = 2 * c + q;
         float f[4];
-        unpack_tagged(pick4(hv, k), f);
+        unpack_tagged(q ? hv1 : hv0, f);
         const int ch = lane + 64 * k;
         norm_chunk(f, rstd, wn[2 * ch], wn[2 * ch + 1], s_x0 + 2 * ch);
       }
     };
     // rows 32j .. 32j+31 (chunks 8j .. 8j+7, all in block k = j / 8) for the reduce wave
-    auto keep_rows = [&](const u32x4 (&hv)[4], float* dst) {
+    auto keep_rows = [&](const u32x4& hv0, const u32x4& hv1, float* dst) {
       const int q = lane - ((8 * j) & 63);
-      if (c == 0 && q >= 0 && q < 8) {
+      if (c == (j >> 4) && q >= 0 && q < 8) {  // block j / 8 is in this wave's half
         float f[4];
-        unpack_tagged(pick4(hv, j >> 3), f);
+        unpack_tagged((j >> 3) & 1 ? hv1 : hv0, f);
 #pragma unroll
         for (int e = 0; e < 4; e++) dst[4 * q + e] = f[e];
       }
     };
 
-    u32x4 hv[4];  // the gathered residual stream, chunks lane + 64k
+    u32x4 hv0, hv1;  // this wave's half of the residual stream: chunks lane + 128c and lane + 128c + 64
     for (int layer = 0; layer < L; layer++) {
       const uint32_t tag = tag_of(epoch, layer);
       const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
       MQ_STAMP(layer * 40 + 12);
-      // ---------------- gather h (every poll wave reads all 1024 words), RMSNorm
+      // ---------------- gather h (each poll wave its half, with the sum of squares), RMSNorm
       float ss;
       if (layer == 0) {
         const uint16_t* src = (P.mode & MODE_INPUT_HIDDEN) ? P.hidden_in : P.embed + (size_t)P.token * H;
@@ -950,19 +946,22 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         for (int k = 0; k < 4; k++) {
           const u32x2 v = ldw2(src + 4 * (lane + 64 * k));
           // widen the raw bf16 values to the tagged layout so every layer reads hv alike
-          hv[k] = u32x4{v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16};
+          const u32x4 t = u32x4{v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16};
+          if (k == 2 * c) hv0 = t;
+          if (k == 2 * c + 1) hv1 = t;
           float f[4];
-          unpack_tagged(hv[k], f);
+          unpack_tagged(t, f);
           ss += (f[0] * f[0] + f[1] * f[1]) + (f[2] * f[2] + f[3] * f[3]);
         }
         ss = wave_sum(ss);
       } else {
-        ss = gather_local(wsb, ws, lb + LX_H, tag_of(epoch, layer - 1), lane, hv);
+        ss = gather_half(wsb, ws, lb + LX_H, lb + LX_HSS, tag_of(epoch, layer - 1), epoch * 32u + (uint32_t)layer, c, lane,
+                         hv0, hv1);
       }
       MQ_STAMP(layer * 40 + 13);
-      norm_out(hv, ss, s_wln);
+      norm_out(hv0, hv1, ss, s_wln);
       MQ_STAMP(layer * 40 + 26);
-      keep_rows(hv, s_hrow);
+      keep_rows(hv0, hv1, s_hrow);
       BAR();  // A1
       MQ_STAMP(layer * 40 + 14);
       if (att) {
@@ -1108,9 +1107,9 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       MQ_STAMP(layer * 40 + 20);
       // ---------------- gather h1; post-attention RMSNorm
       {
-        const float ss1 = gather_local(wsb, ws, lb + LX_H1, tag, lane, hv);
+        const float ss1 = gather_half(wsb, ws, lb + LX_H1, lb + LX_H1SS, tag, tag64, c, lane, hv0, hv1);
         MQ_STAMP(layer * 40 + 21);
-        norm_out(hv, ss1, s_wpost);
+        norm_out(hv0, hv1, ss1, s_wpost);
         MQ_STAMP(layer * 40 + 27);
       }
       BAR();  // D1
@@ -1131,16 +1130,17 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
 
     // ---------------- final norm
     {
-      const float ss = gather_local(wsb, ws, lb + LX_H, tag_of(epoch, L - 1), lane, hv);
+      const float ss = gather_half(wsb, ws, lb + LX_H, lb + LX_HSS, tag_of(epoch, L - 1), epoch * 32u + (uint32_t)L, c, lane,
+                                   hv0, hv1);
       MQ_STAMP(32 * 40);
-      if (lm) norm_out(hv, ss, s_wfn);
+      if (lm) norm_out(hv0, hv1, ss, s_wfn);
       if (w == 0) {
         // hidden_out / normed_out chunks k = 2c, 2c + 1
 #pragma unroll
         for (int q = 0; q < 2; q++) {
           const int k = 2 * c + q;
           float f[4];
-          unpack_tagged(pick4(hv, k), f);
+          unpack_tagged(q ? hv1 : hv0, f);
           const int ch = lane + 64 * k;
 #pragma unroll
           for (int e = 0; e < 4; e++) {
@@ -1199,6 +1199,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       // h1 = bf16(h + bf16(o)) (modeling_qwen3.py:297-298)
       h1v = rbf(hrow + rbf(reduce_row(X_OPART, tag64)));
       if (hx == 0) st1_plain(ws + lb + LX_H1 + ROWS * j + rr, tagged(tag, h1v));
+      {
+        const float ssr = wave_sum(hx == 0 ? h1v * h1v : 0.f);
+        if (lane == 0) st2_plain(ws + lb + LX_H1SS + 2 * j, u32x2{__float_as_uint(ssr), tag64});
+      }
       MQ_STAMP(layer * 40 + 30);
       BAR();  // D1
       BAR();  // E1
@@ -1206,6 +1210,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       // h' = bf16(h1 + bf16(down)) (modeling_qwen3.py:303-304)
       const float hn = rbf(h1v + rbf(reduce_row(X_DPART, tag64)));
       if (hx == 0) st1_plain(ws + lb + LX_H + ROWS * j + rr, tagged(tag, hn));
+      {
+        const float ssr = wave_sum(hx == 0 ? hn * hn : 0.f);
+        if (lane == 0) st2_plain(ws + lb + LX_HSS + 2 * j, u32x2{__float_as_uint(ssr), tag64});
+      }
       MQ_STAMP(layer * 40 + 32);
     }
     BAR();  // F1
