@@ -631,6 +631,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ float s_hrow[ROWS];                       // residual rows 32j .. 32j+31 of h
   __shared__ float s_res[ROWS];                        // stream-wave dot products for the store wave
   __shared__ uint32_t s_cnt;                           // stream-wave results published so far
+  __shared__ uint32_t s_attst;                         // attention-output stores issued by the store wave
   __shared__ const uint16_t* s_lw[MAX_LAYERS][11];    // weight pointers, copied once per launch
   __shared__ float s_bestv[8];
   __shared__ int s_besti[8];
@@ -825,6 +826,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           BAR();  // B4: K/V rows consumed
           MQ_STAMP(layer * 40 + 3);
         }
+        // the store wave's attention-output store goes first: a CU's vector-memory
+        // instructions leave in order, so behind these loads it reached L2 late for
+        // the 31 workgroups that wait on it
+        wait_count(&s_attst, (uint32_t)layer + 1u);
         load_gu(layer);
       }
       // ---------------- o_proj partials: rows 32j + 8s + 2i + rg over the group's 256 columns
@@ -1219,7 +1224,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     BAR();  // F1
   } else {
     // ==================================================================== store wave
-    if (lane == 0) s_cnt = 0u;
+    if (lane == 0) {
+      s_cnt = 0u;
+      s_attst = 0u;
+    }
     BAR();  // P00
     BAR();  // P0
     uint32_t target = 0;
@@ -1309,6 +1317,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           if (dim == 0)
             st4_plain(pb, u32x4{__float_as_uint(hh ? M1 : M0), tag64, __float_as_uint(hh ? L1 : L0), tag64});
         }
+        // tells the stream waves that this store is ahead of their next weight loads
+        if (lane == 0) signal_store(&s_attst);
       }
       MQ_STAMP(layer * 40 + 35);
       // o_proj partials of rows 32j .. 32j+31 over this XCD's two heads
