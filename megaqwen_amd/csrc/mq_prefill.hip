@@ -705,10 +705,13 @@ using namespace mq;
 using namespace mq::pf;
 
 // GEMM shapes (measured on MI355X at S = 512 with the weights cold, as each layer's are):
-// eight-wave workgroups with 128-row tiles and a four-stage ring of 64-wide k-steps;
+// eight-wave workgroups (sixteen for gate/up) with 128-row tiles and a ring of 64-wide
+// k-steps (more waves hide more latency: four-wave tiles were 15-25% slower);
 // o_proj and down_proj split k four ways into fp32 partials, so that each of their 256
 // workgroups streams (128 + 64) rows instead of (32 + 64) rows over a quarter of k
 constexpr int GST = 4, GKS = 1, GWM = 4, GWN = 2;
+// gate/up (128 x 128 tiles, 192 workgroups): sixteen waves and a three-step ring
+constexpr int GU_ST = 3, GU_WM = 4, GU_WN = 4;
 constexpr int TM_G = 128, TN_QKV = 64, TN_GU = 128, TN_RES = 64, RES_SPLIT = 4;
 
 // one launch of gemm_nt over a [m, sum of the segments' widths] output, k split `split` ways
@@ -813,7 +816,7 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     GemmArgs gu{};
     gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
     gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, I / (TN_GU / 2), I};
-    gemm<EPI_SILU, TM_G, TN_GU, GST, GKS, GWM, GWN>(gu, I / (TN_GU / 2), stream);
+    gemm<EPI_SILU, TM_G, TN_GU, GU_ST, GKS, GU_WM, GU_WN>(gu, I / (TN_GU / 2), stream);
     chk();
     GemmArgs gd{};
     gd.a = mid; gd.lda = I; gd.m = S; gd.k = I; gd.nseg = 1;
