@@ -4,7 +4,7 @@
 // prompt's hidden states go through every layer as [S, *] bf16 matrices, K/V
 // slots 0..S-1 of every layer are written, and the greedy next token is taken
 // from the last row. After embed_rows and the first layer's rmsnorm_rows, per layer:
-//   gemm_nt (q, k, v in one launch) -> qk_rope_kv (QK-norm, RoPE, K/V append)
+//   gemm_nt (q, k, v in one launch; its epilogue applies QK-norm and RoPE and appends K/V)
 //   -> attn_prefill (causal, MFMA) -> gemm_nt (o_proj, k split four ways)
 //   -> resid_norm_rows (partials + residual, post-attention RMSNorm)
 //   -> gemm_nt (gate and up, SiLU(gate) * up epilogue) -> gemm_nt (down_proj, k split)
@@ -54,7 +54,7 @@ namespace pf {
 // that follows) so that their grid still fills the 256 CUs.
 constexpr int TK = 64;
 
-enum : int { EPI_STORE = 0, EPI_SILU = 1, EPI_PART = 2 };
+enum : int { EPI_STORE = 0, EPI_SILU = 1, EPI_PART = 2, EPI_QKN = 3 };
 
 struct GemmSeg {
   const uint16_t* w;   // weight rows [n, k]; EPI_SILU: gate_proj rows
@@ -74,11 +74,19 @@ struct PartSet {
   int ld[MAX_SPLIT];
   int n;
 };
+// EPI_QKN: the q, k, v segments' tiles are whole heads; the epilogue applies QK-norm and
+// RoPE to q and k and writes q to `q_out` and k, v to the caches at slot = row
+struct QknArgs {
+  const uint16_t *qn, *kn, *cos_t, *sin_t;
+  uint16_t *q_out, *kc, *vc;
+  int max_seq;
+};
 struct GemmArgs {
   const uint16_t* a;  // [m, lda] bf16
   int lda, m, k, nseg;
   GemmSeg seg[3];
   PartSet part;  // EPI_PART: set z takes the partial sums of k split z (blockIdx.z)
+  QknArgs qkn;   // EPI_QKN
 };
 
 // LDS slot (in 16-byte chunks) of chunk kc (0..7) of tile row r.
@@ -185,6 +193,48 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
 
   // lane holds rows 4 * (lane / 16) + e of column lane % 16 of each block
   const int col = lane & 15, rq = 4 * (lane >> 4);
+  if constexpr (EPI == EPI_QKN) {
+    // QK-norm (per head over 128, weights q_norm/k_norm) and RoPE (modeling_qwen3.py:247-257,
+    // rotate_half form, three bf16 ops) of the tile's rows, which are tokens m0.. of head
+    // nt of segment si (q, k or v); per token the reference's ldg_qk_norm_rope_cache
+    // (fused_decode_ldg.cu:166-276) for a whole prompt
+    static_assert(TN == HD && TM * (HD + 1) * 4 <= NST * KS * SCH * 16, "a tile is one head and fits the ring");
+    float* tile = reinterpret_cast<float*>(&sbuf[0][0][0]);  // [TM][HD + 1] bf16-rounded outputs
+    __syncthreads();  // every wave is past its last read of the ring
+#pragma unroll
+    for (int i = 0; i < RB; i++)
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int j = 0; j < CB; j++) tile[(16 * (RB * wm + i) + rq + e) * (HD + 1) + 16 * jb[j] + col] = rbf(acc[i][j][e]);
+    __syncthreads();
+    const QknArgs& Q = G.qkn;
+    const int h = nt;
+    for (int r = wv; r < TM; r += NW) {
+      const int t = m0 + r;  // token (cache slot); wave-uniform
+      if (t >= G.m) break;
+      const float x1 = tile[r * (HD + 1) + lane], x2 = tile[r * (HD + 1) + 64 + lane];
+      if (si == 2) {
+        uint16_t* dst = Q.vc + ((size_t)h * Q.max_seq + t) * HD;
+        dst[lane] = (uint16_t)f2bf(x1);  // exact: x is a bf16 value
+        dst[64 + lane] = (uint16_t)f2bf(x2);
+        continue;
+      }
+      const uint16_t* nw = si == 0 ? Q.qn : Q.kn;
+      float ss[1] = {x1 * x1 + x2 * x2};
+      wave_sum_n(ss);
+      const float rstd = 1.0f / sqrtf(ss[0] * (1.0f / HD) + EPS);
+      const float n1 = rbf(bf2f(nw[lane]) * rbf(x1 * rstd)), n2 = rbf(bf2f(nw[64 + lane]) * rbf(x2 * rstd));
+      const float c1 = bf2f(Q.cos_t[(size_t)t * HD + lane]), c2 = bf2f(Q.cos_t[(size_t)t * HD + 64 + lane]);
+      const float s1 = bf2f(Q.sin_t[(size_t)t * HD + lane]), s2 = bf2f(Q.sin_t[(size_t)t * HD + 64 + lane]);
+      const float o1 = rbf(rbf(n1 * c1) - rbf(n2 * s1));
+      const float o2 = rbf(rbf(n2 * c2) + rbf(n1 * s2));
+      uint16_t* dst = si == 0 ? Q.q_out + (size_t)t * QS + HD * h : Q.kc + ((size_t)h * Q.max_seq + t) * HD;
+      dst[lane] = (uint16_t)f2bf(o1);
+      dst[64 + lane] = (uint16_t)f2bf(o2);
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < RB; i++)
 #pragma unroll
@@ -321,56 +371,6 @@ __global__ void __launch_bounds__(64) resid_norm_rows(PartSet ps, uint16_t* h, c
     o.z = pack_bf2(rbf(wf[4] * rbf(f[hh][4] * rstd)), rbf(wf[5] * rbf(f[hh][5] * rstd)));
     o.w = pack_bf2(rbf(wf[6] * rbf(f[hh][6] * rstd)), rbf(wf[7] * rbf(f[hh][7] * rstd)));
     reinterpret_cast<u32x4*>(yr + 512 * hh)[lane] = o;
-  }
-}
-
-// Per token (one workgroup): QK-norm (per head over 128, weights q_norm/k_norm) and
-// RoPE (modeling_qwen3.py:247-257, rotate_half form, three bf16 ops) of the 16 q and
-// 8 k heads; q is rewritten in place, k goes to the K cache and v is copied to the V
-// cache at slot s (the reference's ldg_qk_norm_rope_cache, fused_decode_ldg.cu:166-276,
-// for a whole prompt). Lane l handles dims l and l + 64, the two halves RoPE pairs.
-__global__ void __launch_bounds__(256) qk_rope_kv(uint16_t* q, const uint16_t* k, const uint16_t* v,
-                                                  const uint16_t* qn, const uint16_t* kn, const uint16_t* cos_t,
-                                                  const uint16_t* sin_t, uint16_t* kc, uint16_t* vc, int max_seq) {
-  const int s = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  constexpr int NH = (NQ + 2 * NKV) / 4;  // heads per wave: hh = wv + 4 i (q, then k, then v heads)
-  // every load of the wave first (q is rewritten in place, but no two heads overlap, so no
-  // store below feeds a load; loading up front keeps the eight heads from running serially)
-  float x1[NH], x2[NH];
-#pragma unroll
-  for (int i = 0; i < NH; i++) {
-    const int hh = wv + 4 * i;
-    const uint16_t* src = hh < NQ         ? q + (size_t)s * QS + HD * hh
-                          : hh < NQ + NKV ? k + (size_t)s * KVS + HD * (hh - NQ)
-                                          : v + (size_t)s * KVS + HD * (hh - NQ - NKV);
-    x1[i] = bf2f(src[lane]);
-    x2[i] = bf2f(src[64 + lane]);
-  }
-  const float c1 = bf2f(cos_t[(size_t)s * HD + lane]), c2 = bf2f(cos_t[(size_t)s * HD + 64 + lane]);
-  const float s1 = bf2f(sin_t[(size_t)s * HD + lane]), s2 = bf2f(sin_t[(size_t)s * HD + 64 + lane]);
-  const float qw1 = bf2f(qn[lane]), qw2 = bf2f(qn[64 + lane]), kw1 = bf2f(kn[lane]), kw2 = bf2f(kn[64 + lane]);
-  float ss[NH];
-#pragma unroll
-  for (int i = 0; i < NH; i++) ss[i] = x1[i] * x1[i] + x2[i] * x2[i];
-  wave_sum_n(ss);
-#pragma unroll
-  for (int i = 0; i < NH; i++) {
-    const int hh = wv + 4 * i;
-    if (hh < NQ + NKV) {
-      const bool isq = hh < NQ;
-      const int h = isq ? hh : hh - NQ;
-      const float rstd = 1.0f / sqrtf(ss[i] * (1.0f / HD) + EPS);
-      const float n1 = rbf((isq ? qw1 : kw1) * rbf(x1[i] * rstd)), n2 = rbf((isq ? qw2 : kw2) * rbf(x2[i] * rstd));
-      const float o1 = rbf(rbf(n1 * c1) - rbf(n2 * s1));
-      const float o2 = rbf(rbf(n2 * c2) + rbf(n1 * s2));
-      uint16_t* dst = isq ? q + (size_t)s * QS + HD * h : kc + ((size_t)h * max_seq + s) * HD;
-      dst[lane] = (uint16_t)f2bf(o1);
-      dst[64 + lane] = (uint16_t)f2bf(o2);
-    } else {
-      uint16_t* dst = vc + ((size_t)(hh - NQ - NKV) * max_seq + s) * HD;
-      dst[lane] = (uint16_t)f2bf(x1[i]);  // exact: x is a bf16 value
-      dst[64 + lane] = (uint16_t)f2bf(x2[i]);
-    }
   }
 }
 
@@ -712,7 +712,9 @@ using namespace mq::pf;
 constexpr int GST = 4, GKS = 1, GWM = 4, GWN = 2;
 // gate/up (128 x 128 tiles, 192 workgroups): sixteen waves and a three-step ring
 constexpr int GU_ST = 3, GU_WM = 4, GU_WN = 4;
-constexpr int TM_G = 128, TN_QKV = 64, TN_GU = 128, TN_RES = 64, RES_SPLIT = 4;
+constexpr int TM_G = 128, TN_GU = 128, TN_RES = 64, RES_SPLIT = 4;
+// q/k/v with the QK-norm/RoPE/K-V-append epilogue: 64 x 128 tiles (one head each), 2 x 4 waves
+constexpr int TM_QKV = 64, TN_QKV = HD, QKV_WM = 2, QKV_WN = 4;
 
 // one launch of gemm_nt over a [m, sum of the segments' widths] output, k split `split` ways
 template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
@@ -756,8 +758,6 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
   uint16_t* h = bfm(hidden_bf16);
   uint16_t* nrm = bfm(normalized);
   uint16_t* qp = bfm(q_proj);
-  uint16_t* kp = bfm(k_proj);
-  uint16_t* vp = bfm(v_proj);
   uint16_t* att = bfm(attn_out);
   uint16_t* mln = bfm(mlp_norm);
   uint16_t* mid = bfm(mlp_intermediate);
@@ -772,7 +772,7 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
   // fp32 partial sums of the k-split o_proj and down_proj, [S, 1024] a split, in scratch
   // that is dead while they live: gate_out and up_out (unused otherwise), q_proj (read by
   // the attention before o_proj) and k_proj | v_proj as the two column halves of the
-  // fourth set (both read by qk_rope_kv before the attention)
+  // fourth set (unused: the q/k/v epilogue writes k and v straight to the caches)
   auto f32 = [](void* p) { return static_cast<float*>(p); };
   PartSet parts{};
   parts.n = RES_SPLIT;
@@ -795,13 +795,11 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     uint16_t* vcl = bfm(v_cache) + l * kv_layer;
     GemmArgs g{};
     g.a = nrm; g.lda = H; g.m = S; g.k = H; g.nseg = 3;
-    g.seg[0] = GemmSeg{bf(w.q_proj_weight), nullptr, qp, QS / TN_QKV, QS};
-    g.seg[1] = GemmSeg{bf(w.k_proj_weight), nullptr, kp, KVS / TN_QKV, KVS};
-    g.seg[2] = GemmSeg{bf(w.v_proj_weight), nullptr, vp, KVS / TN_QKV, KVS};
-    gemm<EPI_STORE, TM_G, TN_QKV, GST, GKS, GWM, GWN>(g, (QS + 2 * KVS) / TN_QKV, stream);
-    chk();
-    qk_rope_kv<<<S, 256, 0, stream>>>(qp, kp, vp, bf(w.q_norm_weight), bf(w.k_norm_weight), bf(cos_table),
-                                      bf(sin_table), kcl, vcl, max_seq_len);
+    g.seg[0] = GemmSeg{bf(w.q_proj_weight), nullptr, nullptr, QS / TN_QKV, QS};
+    g.seg[1] = GemmSeg{bf(w.k_proj_weight), nullptr, nullptr, KVS / TN_QKV, KVS};
+    g.seg[2] = GemmSeg{bf(w.v_proj_weight), nullptr, nullptr, KVS / TN_QKV, KVS};
+    g.qkn = QknArgs{bf(w.q_norm_weight), bf(w.k_norm_weight), bf(cos_table), bf(sin_table), qp, kcl, vcl, max_seq_len};
+    gemm<EPI_QKN, TM_QKV, TN_QKV, GST, GKS, QKV_WM, QKV_WN>(g, (QS + 2 * KVS) / TN_QKV, stream);
     chk();
     attn_prefill<<<NQ * ((S + AQ - 1) / AQ), 256, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
     chk();
