@@ -316,35 +316,45 @@ __global__ void __launch_bounds__(64) rmsnorm_rows(const uint16_t* x, const uint
 // the residual add h = bf16(h + y) (modeling_qwen3.py:316,322), and, when w is given,
 // the next RMSNorm of the new row into y_norm, as rmsnorm_rows computes it. One
 // single-wave workgroup per row; lane l owns columns 8l .. 8l + 7 and 512 + 8l .. +7.
+template <int NS>
 __global__ void __launch_bounds__(64) resid_norm_rows(PartSet ps, uint16_t* h, const uint16_t* w, uint16_t* y, int m) {
   static_assert(2 * PART_HALF == H, "a partial set is two column halves");
   const int row = blockIdx.x, lane = threadIdx.x;
   if (row >= m) return;
   typedef const __attribute__((address_space(1))) f32x4 gf32x4;
-  auto load = [&](int s, f32x4 (&v)[2][2]) {
+  // every load first (the partials, the residual row, the norm weights): one memory
+  // round trip for the row instead of one per partial set
+  f32x4 pa[NS][2][2];
+#pragma unroll
+  for (int s = 0; s < NS; s++) {
     const float* half[2] = {ps.lo[s] + (size_t)row * ps.ld[s], ps.hi[s] + (size_t)row * ps.ld[s]};
 #pragma unroll
     for (int hh = 0; hh < 2; hh++)
 #pragma unroll
-      for (int u = 0; u < 2; u++) v[hh][u] = *(gf32x4*)(half[hh] + 8 * lane + 4 * u);
-  };
-  f32x4 a[2][2];
-  load(0, a);
-  for (int s = 1; s < ps.n; s++) {
-    f32x4 b[2][2];
-    load(s, b);
-#pragma unroll
-    for (int hh = 0; hh < 2; hh++)
-#pragma unroll
-      for (int u = 0; u < 2; u++) a[hh][u] += b[hh][u];
+      for (int u = 0; u < 2; u++) pa[s][hh][u] = *(gf32x4*)(half[hh] + 8 * lane + 4 * u);
   }
   uint16_t* hr = h + (size_t)row * H;
+  const u32x4 hc[2] = {ldw(hr + 8 * lane), ldw(hr + 512 + 8 * lane)};
+  u32x4 wc[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+  if (w) {
+    wc[0] = ldw(w + 8 * lane);
+    wc[1] = ldw(w + 512 + 8 * lane);
+  }
+  f32x4 a[2][2];
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      a[hh][u] = pa[0][hh][u];
+#pragma unroll
+      for (int s = 1; s < NS; s++) a[hh][u] += pa[s][hh][u];  // split order
+    }
   float f[2][8];
   float ss = 0.f;
 #pragma unroll
   for (int hh = 0; hh < 2; hh++) {
     float r[8];
-    unpack8(ldw(hr + 512 * hh + 8 * lane), r);
+    unpack8(hc[hh], r);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       f[hh][i] = rbf(r[i] + rbf(a[hh][i >> 2][i & 3]));
@@ -364,7 +374,7 @@ __global__ void __launch_bounds__(64) resid_norm_rows(PartSet ps, uint16_t* h, c
 #pragma unroll
   for (int hh = 0; hh < 2; hh++) {
     float wf[8];
-    unpack8(ldw(w + 512 * hh + 8 * lane), wf);
+    unpack8(wc[hh], wf);
     u32x4 o;
     o.x = pack_bf2(rbf(wf[0] * rbf(f[hh][0] * rstd)), rbf(wf[1] * rbf(f[hh][1] * rstd)));
     o.y = pack_bf2(rbf(wf[2] * rbf(f[hh][2] * rstd)), rbf(wf[3] * rbf(f[hh][3] * rstd)));
@@ -809,7 +819,7 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     go.part = parts;
     gemm<EPI_PART, TM_G, TN_RES, GST, GKS, GWM, GWN>(go, H / TN_RES, stream, RES_SPLIT);
     chk();
-    resid_norm_rows<<<S, 64, 0, stream>>>(parts, h, bf(w.post_attn_layernorm_weight), mln, S);
+    resid_norm_rows<RES_SPLIT><<<S, 64, 0, stream>>>(parts, h, bf(w.post_attn_layernorm_weight), mln, S);
     chk();
     GemmArgs gu{};
     gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
@@ -823,7 +833,7 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     gemm<EPI_PART, TM_G, TN_RES, GST, GKS, GWM, GWN>(gd, H / TN_RES, stream, RES_SPLIT);
     chk();
     // the next layer's input RMSNorm (none after the last: the final norm is the LM head's)
-    resid_norm_rows<<<S, 64, 0, stream>>>(parts, h, l + 1 < num_layers ? bf(layer_weights[l + 1].input_layernorm_weight) : nullptr,
+    resid_norm_rows<RES_SPLIT><<<S, 64, 0, stream>>>(parts, h, l + 1 < num_layers ? bf(layer_weights[l + 1].input_layernorm_weight) : nullptr,
                                           nrm, S);
     chk();
   }
