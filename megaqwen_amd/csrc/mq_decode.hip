@@ -581,14 +581,23 @@ __device__ __forceinline__ void unpack_tagged(const u32x4& v, float* f) {
 // This poll wave's half of a gathered residual stream (chunks lane + 128c into v0 and
 // lane + 128c + 64 into v1) and the stream's sum of squares, added up from the 32 per-workgroup
 // sums of squares published with it (the same order in both poll waves, so their norms
-// agree bit for bit). All three loads are issued, then the stale ones re-polled together.
+// agree bit for bit).
 __device__ __forceinline__ float gather_half(const Buf& b, uint32_t* ws, uint32_t base, uint32_t ssbase, uint32_t tag,
                                              uint32_t tag64, int c, int lane, u32x4& v0, u32x4& v1) {
   const uint32_t w0 = base + 4 * (lane + 128 * c), w1 = w0 + 4 * 64;
   const uint32_t wq = ssbase + 4 * (lane & 15);  // the sums of workgroups 2 (lane % 16) and +1
-  u32x4 a = ldl4(b, w0), e = ldl4(b, w1), q = ldl4(b, wq);
+  // poll only the 32 sums of squares (each producer stores its sum after its rows): a
+  // third of the polling traffic of polling rows and sums together, which measured 6 us
+  // faster per token; then load the rows once and re-poll any that are still stale
+  u32x4 q = ldl4(b, wq);
   auto fresh = [&](const u32x4& x) { return (x.y == tag64) & (x.w == tag64); };
   uint32_t spins = 0;
+  while (!fresh(q)) {
+    if (watchdog(b, ws, ++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+    q = ldl4(b, wq);
+  }
+  u32x4 a = ldl4(b, w0), e = ldl4(b, w1);
   while (!(tags_ok(a, tag) & tags_ok(e, tag) & fresh(q))) {
     if (watchdog(b, ws, ++spins)) break;
     __builtin_amdgcn_s_sleep(1);
@@ -1061,8 +1070,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       } else {
         // every workgroup merges the XCD's chunk partials itself, straight into its o_proj
         // input: thread pt takes dims d0, d0 + 1 of head hh (a poll wave per head), CG chunks
-        // per round; lane q loads chunk q's (m, l), which the wave then reads by readlane;
-        // a round issues all its loads, then re-polls the stale ones together
+        // per round; lane q loads chunk q's (m, l), which the wave then reads by readlane
         const int hh = pt >> 6, d0 = 2 * (pt & 63);
         float Mc = -INFINITY, Lc = 0.f, O0 = 0.f, O1 = 0.f;
         // nine chunks a round: contexts up to 2303 positions merge in one round (2048 and
@@ -1075,11 +1083,19 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           const uint32_t bml = b0 + 4 * min(lane, nq - 1) * APART;
           u32x4 ml, ov[CG];  // this lane's chunk (m, tag, l, tag); (acc[d0], tag, acc[d0 + 1], tag) per chunk
           ml = ldl4(wsb, bml);
+          auto fresh = [&](const u32x4& v) { return (v.y == tag64) & (v.w == tag64); };
+          uint32_t spins = 0;
+          // the chunks' (m, l) first (each stored after its chunk's accumulators, and polled
+          // by one lane per chunk): far less polling traffic than polling every
+          // accumulator pair, 5-14 us per token at split contexts
+          while (mlane && !fresh(ml)) {
+            if (watchdog(wsb, ws, ++spins)) break;
+            __builtin_amdgcn_s_sleep(1);
+            ml = ldl4(wsb, bml);
+          }
 #pragma unroll
           for (int q = 0; q < CG; q++)
             if (q < nq) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
-          auto fresh = [&](const u32x4& v) { return (v.y == tag64) & (v.w == tag64); };
-          uint32_t spins = 0;
           for (;;) {
             bool ok = !mlane || fresh(ml);
 #pragma unroll
@@ -1167,10 +1183,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     // sum of the 8 partials of row rr of `part` in XCD order, identical in both lanes of the pair
     auto reduce_row = [&](uint32_t part, uint32_t tag64) -> float {
       const uint32_t wd = part + 2 * ((j * ROWS + rr) * NXCD + 4 * hx);
+      auto ok = [&](const u32x4& v) { return (v.y == tag64) & (v.w == tag64); };
+      uint32_t spins = 0;
       u32x4 a = xld4(wsb, wd), b = xld4(wsb, wd + 4);
       // re-poll both stale halves at once (one round trip per iteration)
-      uint32_t spins = 0;
-      auto ok = [&](const u32x4& v) { return (v.y == tag64) & (v.w == tag64); };
       while (!(ok(a) & ok(b))) {
         if (watchdog(wsb, ws, ++spins)) break;
         __builtin_amdgcn_s_sleep(1);
