@@ -210,25 +210,40 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
     __syncthreads();
     const QknArgs& Q = G.qkn;
     const int h = nt;
-    for (int r = wv; r < TM; r += NW) {
-      const int t = m0 + r;  // token (cache slot); wave-uniform
+    constexpr int RPW = TM / NW;  // rows per wave: wave wv takes rows wv + NW i
+    if (si == 2) {
+      for (int i = 0; i < RPW; i++) {
+        const int r = wv + NW * i, t = m0 + r;  // token (cache slot); wave-uniform
+        if (t >= G.m) break;
+        uint16_t* dst = Q.vc + ((size_t)h * Q.max_seq + t) * HD;
+        dst[lane] = (uint16_t)f2bf(tile[r * (HD + 1) + lane]);  // exact: x is a bf16 value
+        dst[64 + lane] = (uint16_t)f2bf(tile[r * (HD + 1) + 64 + lane]);
+      }
+      return;
+    }
+    // every row's cos/sin and the norm weights first: one memory round trip, not one a row
+    const uint16_t* nwp = si == 0 ? Q.qn : Q.kn;
+    const float w1 = bf2f(nwp[lane]), w2 = bf2f(nwp[64 + lane]);
+    float cs[RPW][4];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const size_t t = (size_t)min(m0 + wv + NW * i, G.m - 1) * HD;  // rows past the prompt: never stored
+      cs[i][0] = bf2f(Q.cos_t[t + lane]);
+      cs[i][1] = bf2f(Q.cos_t[t + 64 + lane]);
+      cs[i][2] = bf2f(Q.sin_t[t + lane]);
+      cs[i][3] = bf2f(Q.sin_t[t + 64 + lane]);
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const int r = wv + NW * i, t = m0 + r;
       if (t >= G.m) break;
       const float x1 = tile[r * (HD + 1) + lane], x2 = tile[r * (HD + 1) + 64 + lane];
-      if (si == 2) {
-        uint16_t* dst = Q.vc + ((size_t)h * Q.max_seq + t) * HD;
-        dst[lane] = (uint16_t)f2bf(x1);  // exact: x is a bf16 value
-        dst[64 + lane] = (uint16_t)f2bf(x2);
-        continue;
-      }
-      const uint16_t* nw = si == 0 ? Q.qn : Q.kn;
       float ss[1] = {x1 * x1 + x2 * x2};
       wave_sum_n(ss);
       const float rstd = 1.0f / sqrtf(ss[0] * (1.0f / HD) + EPS);
-      const float n1 = rbf(bf2f(nw[lane]) * rbf(x1 * rstd)), n2 = rbf(bf2f(nw[64 + lane]) * rbf(x2 * rstd));
-      const float c1 = bf2f(Q.cos_t[(size_t)t * HD + lane]), c2 = bf2f(Q.cos_t[(size_t)t * HD + 64 + lane]);
-      const float s1 = bf2f(Q.sin_t[(size_t)t * HD + lane]), s2 = bf2f(Q.sin_t[(size_t)t * HD + 64 + lane]);
-      const float o1 = rbf(rbf(n1 * c1) - rbf(n2 * s1));
-      const float o2 = rbf(rbf(n2 * c2) + rbf(n1 * s2));
+      const float n1 = rbf(w1 * rbf(x1 * rstd)), n2 = rbf(w2 * rbf(x2 * rstd));
+      const float o1 = rbf(rbf(n1 * cs[i][0]) - rbf(n2 * cs[i][2]));
+      const float o2 = rbf(rbf(n2 * cs[i][1]) + rbf(n1 * cs[i][3]));
       uint16_t* dst = si == 0 ? Q.q_out + (size_t)t * QS + HD * h : Q.kc + ((size_t)h * Q.max_seq + t) * HD;
       dst[lane] = (uint16_t)f2bf(o1);
       dst[64 + lane] = (uint16_t)f2bf(o2);
