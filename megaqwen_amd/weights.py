@@ -10,7 +10,11 @@ benchmark uses synthetic weights generated here:
   input/post norms, then the final norm; `lm_head` is tied to the embedding);
 * each matrix is `randn(shape, generator=g) * 0.02` in fp32, cast to bf16
   (round-to-nearest-even);
-* every norm weight is 1.
+* every norm weight is 1, or, with `norms="random"`,
+  `bf16(1 + 0.1 * randn)` drawn per norm tensor from a second generator
+  (`manual_seed(seed + 1000)`), so the matrices are unchanged and every gamma
+  (input, post-attention, q/k and final norms of every layer) is distinct: that
+  variant exists to show that each gamma is applied, and to the right place.
 
 `layer_weights_flat` follows the reference's 11-per-layer order
 (`megakernel_decode.py:1106-1120`).
@@ -60,14 +64,28 @@ def _is_norm(key: str) -> bool:
     return key.endswith("norm.weight")
 
 
-def make_state_dict(seed: int = 0, num_layers: int = C.NUM_LAYERS, std: float = 0.02) -> dict[str, torch.Tensor]:
-    """Return the seeded bf16 state dict (CPU tensors), HF key names, lm_head tied."""
+NORM_STD = 0.1
+
+
+def make_state_dict(seed: int = 0, num_layers: int = C.NUM_LAYERS, std: float = 0.02,
+                    norms: str = "ones") -> dict[str, torch.Tensor]:
+    """Return the seeded bf16 state dict (CPU tensors), HF key names, lm_head tied.
+
+    norms: "ones" (every norm weight 1) or "random" (bf16(1 + NORM_STD * randn) from
+    `manual_seed(seed + 1000)`, walked in the same key order).
+    """
+    if norms not in ("ones", "random"):
+        raise ValueError(f"norms must be 'ones' or 'random', got {norms!r}")
     g = torch.Generator("cpu").manual_seed(seed)
+    gn = torch.Generator("cpu").manual_seed(seed + 1000)
     sd: dict[str, torch.Tensor] = {}
     for key in hf_state_dict_keys(num_layers):
         shape = _shape_of(key)
         if _is_norm(key):
-            sd[key] = torch.ones(shape, dtype=torch.bfloat16)
+            if norms == "ones":
+                sd[key] = torch.ones(shape, dtype=torch.bfloat16)
+            else:
+                sd[key] = (1.0 + NORM_STD * torch.randn(shape, generator=gn, dtype=torch.float32)).to(torch.bfloat16)
         else:
             sd[key] = (torch.randn(shape, generator=g, dtype=torch.float32) * std).to(torch.bfloat16)
     return sd

@@ -20,10 +20,13 @@ rounding boundary; the parity tests quantify that against HF fixtures.
 
 Pinning (see tests/test_oracle.py): RoPE tables bitwise vs HF's rotary module;
 `rmsnorm`, `apply_rope`, `silu_mul`, `linear` against closed forms and fp64 brute
-force; `attention_*` against invariants (cache_len 1 -> V[0]; equal keys ->
-mean of V; GQA h -> h//2) and fp64 softmax; the single decoder block against
-the HF fixture for config 2; end-to-end greedy ids and logits against the HF
-fixture for config 1.
+force; `attention_rows` against invariants (cache_len 1 -> V[0]; equal keys ->
+mean of V; GQA h -> h//2), fp64 softmax, and past 512 keys (the blocked online
+softmax, `flash_block_update`) against fp64 and a one-block run at 513..8448 keys,
+with planted rescale mistakes shown to fail; the single decoder block against the
+HF fixture for config 2, with unit and with random norm gammas (misplaced gammas
+shown to fail); end-to-end greedy ids and logits against HF's prefill path
+(config 1) and HF's decode path (config 1, unit and random gammas).
 """
 
 from __future__ import annotations
@@ -130,14 +133,21 @@ def attention_rows(q, K, V, q_pos, scale=SCALE, kv_split: int | None = None) -> 
         s = (q @ K[s0:s1].T).astype(np.float32) * np.float32(scale)
         mask = col[None, s0:s1] > q_pos[:, None]
         s = np.where(mask, np.float32(-np.inf), s)
-        bm = np.maximum(m, s.max(axis=1, keepdims=True))
-        bm_safe = np.where(np.isinf(bm), np.float32(0), bm)
-        p = np.exp(s - bm_safe, dtype=np.float32)
-        alpha = np.where(np.isinf(m), np.float32(0), np.exp(m - bm_safe, dtype=np.float32))
-        lsum = p.sum(axis=1, keepdims=True, dtype=np.float32) + alpha * lsum
-        acc = acc * alpha + bf16r(p) @ V[s0:s1]
-        m = bm
+        m, lsum, acc = flash_block_update(m, lsum, acc, s, V[s0:s1])
     return bf16r(acc * (np.float32(1.0) / lsum))
+
+
+def flash_block_update(m, lsum, acc, s, Vb):
+    """One kv block of the online softmax (torch's CPU flash kernel, see attention_rows):
+    the running max m, sum lsum and accumulator acc are rescaled by exp(m_old - m_new)
+    before the block's exp(s - m_new) (summed in fp32, cast to bf16 for P.V) is added."""
+    bm = np.maximum(m, s.max(axis=1, keepdims=True))
+    bm_safe = np.where(np.isinf(bm), np.float32(0), bm)
+    p = np.exp(s - bm_safe, dtype=np.float32)
+    alpha = np.where(np.isinf(m), np.float32(0), np.exp(m - bm_safe, dtype=np.float32))
+    lsum = p.sum(axis=1, keepdims=True, dtype=np.float32) + alpha * lsum
+    acc = acc * alpha + bf16r(p) @ Vb
+    return bm, lsum, acc
 
 
 def attention_decode_fp64(q, K, V, scale=float(SCALE)) -> np.ndarray:

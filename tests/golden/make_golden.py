@@ -7,7 +7,13 @@ on the seeded synthetic weights of `megaqwen_amd.weights`. Nothing from the
 reference repository is imported or executed. The fixtures are small `.npz` /
 `.json` files committed next to this script; GPU boxes never run it.
 
-Usage: python tests/golden/make_golden.py [rope] [block] [c1] [c4] [c3] [c5]
+Usage: python tests/golden/make_golden.py [rope] [block] [c1] [c4] [c3] [c5] [c1d] [blockg] [c1g] [c4g]
+
+* c1d: config 1 on HF's decode path (the prompt fed one token at a time through the
+  KV cache, as the megakernel decoder does), full logits at steps 0, 15 and 31;
+* blockg / c1g / c4g: the block, config-1 (decode path) and a 64-token prefill case
+  on the `norms="random"` weights, whose norm gammas all differ from 1 and from
+  each other.
 """
 
 from __future__ import annotations
@@ -94,7 +100,7 @@ def block_inputs():
     return hidden, k, v
 
 
-def write_block(sd):
+def write_block(sd, name="block_pos200"):
     """Config 2: one decoder block (layer 0 weights) decoding at position 200."""
     from transformers import DynamicCache
     from transformers.models.qwen3.modeling_qwen3 import Qwen3DecoderLayer, Qwen3RotaryEmbedding
@@ -132,7 +138,7 @@ def write_block(sd):
     kc, vc = cache.layers[0].keys, cache.layers[0].values
     assert kc.shape == (1, 8, 201, 128)
     np.savez_compressed(
-        os.path.join(HERE, "block_pos200.npz"),
+        os.path.join(HERE, f"{name}.npz"),
         out=u16(out.reshape(-1)), k_slot=u16(kc[0, :, 200]), v_slot=u16(vc[0, :, 200]),
         attn=u16(traces["attn"].reshape(-1)), o=u16(traces["attn_o"].reshape(-1)), m=u16(traces["m"].reshape(-1)),
         hidden_sha=np.frombuffer(weights.tensor_sha256(hidden).encode(), dtype=np.uint8),
@@ -140,8 +146,11 @@ def write_block(sd):
     print("block written", out.reshape(-1)[:4])
 
 
-def hf_greedy(model, prompt, n_new, topk=TOPK, full_logit_steps=()):
-    """Greedy decode with HF forward + DynamicCache (== generate(do_sample=False))."""
+def hf_greedy(model, prompt, n_new, topk=TOPK, full_logit_steps=(), decode_path=False):
+    """Greedy decode with HF forward + DynamicCache (== generate(do_sample=False)).
+
+    decode_path: feed the prompt one token at a time (HF's decode path for every
+    position) instead of one prefill forward."""
     from transformers import DynamicCache
 
     ids = torch.tensor([prompt])
@@ -149,7 +158,11 @@ def hf_greedy(model, prompt, n_new, topk=TOPK, full_logit_steps=()):
     out_ids, tk_ids, tk_vals, full = [], [], [], {}
     t0 = time.perf_counter()
     with torch.no_grad():
-        res = model(input_ids=ids, past_key_values=cache, use_cache=True)
+        if decode_path:
+            for t in prompt:
+                res = model(input_ids=torch.tensor([[t]]), past_key_values=cache, use_cache=True)
+        else:
+            res = model(input_ids=ids, past_key_values=cache, use_cache=True)
         t_prefill = time.perf_counter() - t0
         t1 = time.perf_counter()
         for step in range(n_new):
@@ -167,9 +180,9 @@ def hf_greedy(model, prompt, n_new, topk=TOPK, full_logit_steps=()):
     return out_ids, np.stack(tk_ids), np.stack(tk_vals), full, t_prefill, t_decode
 
 
-def write_greedy(model, name, prompt_len, n_new, full_steps=()):
+def write_greedy(model, name, prompt_len, n_new, full_steps=(), decode_path=False, norms="ones"):
     prompt = weights.random_prompt(prompt_len, seed=1)
-    ids, tki, tkv, full, tp, td = hf_greedy(model, prompt, n_new, full_logit_steps=full_steps)
+    ids, tki, tkv, full, tp, td = hf_greedy(model, prompt, n_new, full_logit_steps=full_steps, decode_path=decode_path)
     margins = tkv[:, 0] - tkv[:, 1]
     arrays = dict(prompt=np.array(prompt, dtype=np.int32), ids=np.array(ids, dtype=np.int32),
                   topk_ids=tki, topk_vals=tkv.astype(np.float32), margins=margins.astype(np.float32))
@@ -177,6 +190,7 @@ def write_greedy(model, name, prompt_len, n_new, full_steps=()):
         arrays[f"logits_step{s}"] = v
     np.savez_compressed(os.path.join(HERE, f"greedy_{name}.npz"), **arrays)
     meta = {"prompt_len": prompt_len, "n_new": n_new, "hf_prefill_s": tp, "hf_decode_s": td,
+            "prompt_path": "decode (one token at a time)" if decode_path else "prefill", "norms": norms,
             "min_margin": float(margins.min()), "n_zero_margin": int((margins == 0).sum()),
             "transformers": __import__("transformers").__version__, "torch": torch.__version__,
             "threads": torch.get_num_threads()}
@@ -189,7 +203,22 @@ def main(argv):
     torch.set_num_threads(os.cpu_count())
     if "rope" in what:
         write_rope()
-    need_sd = what & {"block", "c1", "c3", "c4", "c5"}
+    if what & {"blockg", "c1g", "c4g"}:
+        sdg = weights.make_state_dict(seed=0, norms="random")
+        gh = {k: weights.tensor_sha256(sdg[k]) for k in
+              ["model.layers.0.input_layernorm.weight", "model.layers.13.self_attn.k_norm.weight",
+               "model.layers.27.post_attention_layernorm.weight", "model.norm.weight"]}
+        json.dump(gh, open(os.path.join(HERE, "weights_gamma_sha256.json"), "w"), indent=1)
+        if "blockg" in what:
+            write_block(sdg, "block_pos200_gamma")
+        if what & {"c1g", "c4g"}:
+            model = hf_model(sdg)
+            if "c1g" in what:
+                write_greedy(model, "c1g", 8, 32, full_steps=(0, 31), decode_path=True, norms="random")
+            if "c4g" in what:
+                write_greedy(model, "c4g", 64, 16, full_steps=(0,), norms="random")
+            del model
+    need_sd = what & {"block", "c1", "c3", "c4", "c5", "c1d"}
     if not need_sd:
         return
     t0 = time.perf_counter()
@@ -201,10 +230,12 @@ def main(argv):
     json.dump(hashes, open(os.path.join(HERE, "weights_sha256.json"), "w"), indent=1)
     if "block" in what:
         write_block(sd)
-    if what & {"c1", "c3", "c4", "c5"}:
+    if what & {"c1", "c3", "c4", "c5", "c1d"}:
         model = hf_model(sd)
         if "c1" in what:
             write_greedy(model, "c1", 8, 32, full_steps=(0, 31))
+        if "c1d" in what:
+            write_greedy(model, "c1d", 8, 32, full_steps=(0, 15, 31), decode_path=True)
         if "c4" in what:
             write_greedy(model, "c4", 512, 128, full_steps=(0,))
         if "c3" in what:
