@@ -46,6 +46,18 @@ typedef struct LDGLayerWeights {
 
 typedef LDGLayerWeights PrefillLayerWeights;
 
+/* Device-resident decode step (16 bytes, device memory): the input of the next launch of
+ * mq_decode_step_device. Each launch reads it at its start and its last workgroup writes
+ * {argmax token, position + 1, epoch + 1, count + 1} back (a failed step writes its
+ * negative status as the token and keeps the position; launches that find a negative
+ * token, an invalid position or count == capacity do nothing). */
+typedef struct MqDecodeStep {
+  int token;      /* input token of the next step */
+  int position;   /* KV slot the next step writes (cache_len = position + 1) */
+  unsigned epoch; /* exchange tag base of the next step (set by mq_decode_step_init) */
+  int count;      /* steps done: out_ids[count] receives the next step's token */
+} MqDecodeStep;
+
 /* One greedy decode step of the full model.
  * Replaces `launch_ldg_decode` (csrc/megakernel/fused_decode_ldg.cu:893-921).
  *   layer_weights : DEVICE array of num_layers structs (as in the reference).
@@ -115,6 +127,42 @@ int launch_prefill_float(const int* input_token_ids, int* output_token_id, int s
                          void* gate_out, void* up_out, void* mlp_intermediate, void* down_out, void* final_hidden,
                          void* block_max_vals, void* block_max_idxs, void* hidden_bf16_out, int num_layers,
                          int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* Device-resident generation (reference idea: experimental/qwen_persistent_kernel.cu:1028-1033,
+ * which reads token and position from device memory so a captured graph can replay).
+ * mq_decode_step_init writes {token, position, epoch, 0} to `step` (stream-ordered copy of
+ * pageable host memory) and reserves `capacity` launch epochs for it. Then up to
+ * `capacity` launches of mq_decode_step_device (directly, or as nodes of a captured HIP
+ * graph: the launch itself does no memset, copy or allocation) each decode one token of
+ * the full model like launch_ldg_decode, taking token/position/epoch from `step`,
+ * appending the greedy token to out_ids[count] and advancing `step`. No host read is
+ * needed between steps. split_instance: 0 runs the kernel instance for contexts of at
+ * most 256 positions (a step past that fails with a negative token), 1 the instance for
+ * every length (see mq_decode_plan). Re-initialise `step` before replaying a graph. */
+int mq_decode_step_init(MqDecodeStep* step, int token, int position, int capacity, hipStream_t stream);
+int mq_decode_step_device(MqDecodeStep* step, int* out_ids, int out_capacity, int split_instance,
+                          const void* embed_weight, const LDGLayerWeights* layer_weights,
+                          const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
+                          const void* sin_table, void* k_cache, void* v_cache, void* hidden_buffer,
+                          void* g_normalized, int num_layers, int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* The decode kernel's work split for the query at `position` (host-side, no GPU needed):
+ * *instance = 0 (one attention workgroup per XCD, contexts of at most 256 positions) or 1;
+ * the attention is split into *nsplit chunks of at most *chunk positions, each attended
+ * in at most *npass LDS passes. The MI355X counterpart of the reference's decode-kernel
+ * variant choice (chat.py:17-29). MQ_ERR_ARG past the 16384-position limit. */
+int mq_decode_plan(int position, int* instance, int* nsplit, int* chunk, int* npass);
+
+/* Launch mode of the decode entry points (process-wide): 0 = ordinary launch (default;
+ * all 256 workgroups are resident by construction and every inter-workgroup wait is
+ * bounded), 1 = hipLaunchCooperativeKernel (the reference's launch,
+ * csrc/megakernel/fused_decode_ldg.cu:947). Returns the previous mode. */
+int mq_set_launch_mode(int cooperative);
+
+/* Test hook: sets this device's decode error word, as a failed wait would. The next
+ * decode launch then gives up every wait that does not succeed at once, completes, and
+ * reports the flags as a negative token; mq_reset_workspace clears them. Synchronous. */
+int mq_debug_set_error(int device, unsigned flags);
 
 /* Zero this device's workspace (exchange buffers and counters). Needed only
  * after a launch reported a watchdog error. Synchronous. */

@@ -39,6 +39,13 @@ class LDGLayerWeights(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in LAYER_FIELDS]
 
 
+class MqDecodeStep(ctypes.Structure):
+    """Mirror of the device-resident step descriptor (include/megaqwen_amd.h)."""
+
+    _fields_ = [("token", ctypes.c_int), ("position", ctypes.c_int), ("epoch", ctypes.c_uint),
+                ("count", ctypes.c_int)]
+
+
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _f = ctypes.c_float
@@ -53,6 +60,13 @@ SIGNATURES = {
     # ids, out, seq_len, embed, layers (host array), final norm, lm head, cos, sin, k, v, 17 scratch,
     # num_layers, max_seq_len, scale, stream
     "launch_prefill_float": [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_vp] * 17 + [_i, _i, _f, _vp],
+    "mq_decode_step_init": [_vp, _i, _i, _i, _vp],
+    # step, out_ids, capacity, split_instance, embed, layers, final norm, lm head, cos, sin, k, v,
+    # hidden_buffer, g_normalized, num_layers, max_seq_len, scale, stream
+    "mq_decode_step_device": [_vp, _vp, _i, _i] + [_vp] * 10 + [_i, _i, _f, _vp],
+    "mq_decode_plan": [_i, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)],
+    "mq_set_launch_mode": [_i],
+    "mq_debug_set_error": [_i, ctypes.c_uint],
     "mq_reset_workspace": [_i],
     "mq_strerror": [_i],
 }
@@ -89,3 +103,13 @@ def check(status: int, what: str) -> None:
 
 def exported_symbols() -> list[str]:
     return list(SIGNATURES)
+
+
+def decode_plan(position: int) -> dict:
+    """The decode kernel's work split for the query at `position` (C ABI `mq_decode_plan`,
+    host only): kernel instance (0: contexts <= 256 positions, 1: any), number of attention
+    chunks, positions per chunk, LDS passes per chunk."""
+    inst, ns, ch, npass = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    check(lib().mq_decode_plan(int(position), ctypes.byref(inst), ctypes.byref(ns), ctypes.byref(ch),
+                               ctypes.byref(npass)), "mq_decode_plan")
+    return {"instance": inst.value, "nsplit": ns.value, "chunk": ch.value, "npass": npass.value}

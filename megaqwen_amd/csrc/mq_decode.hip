@@ -5,9 +5,8 @@
 // reference's ldg_decode_kernel + ldg_lm_head_phase1/2
 // (csrc/megakernel/fused_decode_ldg.cu:617-887).
 //
-// Chip layout: 256 workgroups of 512 threads, one per CU; workgroup w runs on
-// XCD g = w % 8 (checked against the hardware XCC id) as that XCD's member
-// j = w / 8. XCD g owns KV group g: the 512 q/k/v rows of query heads 2g, 2g+1
+// Chip layout: 256 workgroups of 512 threads, one per CU; workgroup w serves the
+// XCD g it runs on (read from the hardware XCC id) as that XCD's member j = w / 8. XCD g owns KV group g: the 512 q/k/v rows of query heads 2g, 2g+1
 // and KV head g, the attention of those heads, the o_proj columns of those
 // heads (a K-split of o_proj across XCDs) and MLP units 384g .. 384g+383 (a
 // K-split of down_proj). Every workgroup runs four roles, one per wave kind:
@@ -91,9 +90,24 @@ constexpr int KV_CAP = 256;                       // positions per LDS pass of a
 constexpr int MAX_CTX = 2 * WG_PER_XCD * KV_CAP;  // 16384: at most two passes per workgroup
 constexpr int SPLIT_WARM_MAX = 3;  // split contexts whose next-layer rows are warmed in L2
 constexpr int LM_PRE = 4;                     // LM-head rows each stream wave loads during the last layer
-// Attention workgroups issue a layer's K/V copy in the previous layer's gate/up stage;
-// only the layer's o_proj loads (4) follow it before attention.
-constexpr int S_LOADS_AFTER_KV = 4;
+
+// Attention split of a context of n positions (the query at n - 1): nsplit chunks of at
+// most `chunk` positions, chunk j on workgroup (g, j) of every XCD g, each attended in
+// passes of at most KV_CAP positions (the LDS copy holds KV_CAP rows).
+__host__ __device__ constexpr int plan_nsplit(int n) {
+  return (n + KV_CAP - 1) / KV_CAP < WG_PER_XCD ? (n + KV_CAP - 1) / KV_CAP : WG_PER_XCD;
+}
+__host__ __device__ constexpr int plan_chunk(int n) { return (n + plan_nsplit(n) - 1) / plan_nsplit(n); }
+// Every context length the kernel accepts (1 .. MAX_CTX) gives chunks of at most two LDS
+// passes, none of them empty, covering all n positions.
+constexpr bool plan_is_sound() {
+  for (int n = 1; n <= MAX_CTX; n++) {
+    const int ns = plan_nsplit(n), ch = plan_chunk(n);
+    if (ns < 1 || ns > WG_PER_XCD || ch > 2 * KV_CAP || ch * ns < n || (ns - 1) * ch >= n) return false;
+  }
+  return true;
+}
+static_assert(plan_is_sound(), "attention chunks must fit two LDS passes and cover the context");
 
 // Workspace layout, in 32-bit words.
 constexpr uint32_t WS_RESERVED = 0;  // (words 0..31 unused)
@@ -121,11 +135,12 @@ constexpr size_t WS_BYTES = ((WS_WORDS * 4 + 4 + 65535) / 65536) * 65536;
 
 constexpr uint32_t POLL_LIMIT = 1u << 21;  // ~1 s of polling before the watchdog fires
 constexpr uint32_t ERR_POLL = 1u;
-constexpr uint32_t ERR_XCD = 2u;  // a workgroup did not run on XCD blockIdx % 8
+constexpr uint32_t ERR_XCD = 2u;  // a workgroup ran on an XCD numbered 8 or above
+constexpr uint32_t ERR_STEP = 4u;  // a device-resident step found an invalid token, position or count
 
 constexpr int NT_LD = 2;  // non-temporal cache policy: bypasses the CU's L1, served by the XCD's L2
 
-enum : int { MODE_INPUT_HIDDEN = 1, MODE_NO_LMHEAD = 2, MODE_LOGITS = 4 };
+enum : int { MODE_INPUT_HIDDEN = 1, MODE_NO_LMHEAD = 2, MODE_LOGITS = 4, MODE_DEVICE_STEP = 8 };
 enum { W_IN = 0, W_Q, W_K, W_V, W_QN, W_KN, W_O, W_POST, W_G, W_U, W_D };
 
 struct DecodeParams {
@@ -150,6 +165,11 @@ struct DecodeParams {
   float attn_scale;
   int mode;
   uint32_t epoch;  // launch counter of the device (the host's): tags of this launch's exchanges
+  // MODE_DEVICE_STEP: token, position and epoch come from *step (advanced by the launch's
+  // last workgroup), and each launch's token is appended to out_ids[step->count]
+  MqDecodeStep* step;
+  int* out_ids;
+  int out_capacity;
 };
 
 // Workgroup barrier without a memory fence: LDS writes are complete once
@@ -649,26 +669,50 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int w = blockIdx.x, g = w & (NXCD - 1), j = w / NXCD;
+  // The XCD-local exchanges (plain stores, L2-coherent loads) need each workgroup's group
+  // g to be the XCD it runs on, so g is read from the hardware. The dispatcher deals
+  // workgroups to the XCDs in turn, starting at an XCD that depends on the launch path
+  // (an ordinary launch starts at 0, a HIP graph node need not): the XCD of workgroup w
+  // is (w + start) % 8 and j = w / 8 numbers the 32 workgroups of each XCD. Were the
+  // deal different, a member slot would stay unfilled and a bounded wait would report
+  // the error; no exchange can complete with a wrong member.
+  uint32_t xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  const int w = blockIdx.x, g = (int)(xcc & (NXCD - 1)), j = w / NXCD;
   uint32_t* ws = P.ws;
   const Buf wsb(ws);
-  const uint32_t epoch = P.epoch;
-  // The XCD-local exchange (plain stores, L2-coherent loads) assumes that the
-  // dispatcher placed workgroup w on XCD w % 8; check it on the hardware.
-  if (tid == 0) {
-    uint32_t xcc;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-    if ((xcc & 15u) != (uint32_t)g) raise_error(ws, ERR_XCD);
+  // token, position, epoch: kernel arguments, or a device-resident step written by the
+  // previous launch's last workgroup (visible at this launch's start)
+  int token = P.token, p = P.position, step_count = 0;
+  uint32_t epoch = P.epoch;
+  if (P.mode & MODE_DEVICE_STEP) {
+    const u32x4 sv = *(const gu32x4*)(const void*)P.step;
+    token = (int)__builtin_amdgcn_readfirstlane(sv.x);
+    p = (int)__builtin_amdgcn_readfirstlane(sv.y);
+    epoch = __builtin_amdgcn_readfirstlane(sv.z);
+    step_count = (int)__builtin_amdgcn_readfirstlane(sv.w);
+    // Every workgroup reads the same step, so all of them leave here together. The first
+    // failing step records its error; later launches find the negative token and return.
+    if (token < 0 || token >= VOCAB || p < 0 || p >= P.max_seq_len || p >= MAX_CTX || (!SPLIT && p >= KV_CAP) ||
+        step_count >= P.out_capacity) {
+      if (w == 0 && tid == 0 && token >= 0 && step_count < P.out_capacity) {
+        P.out_ids[step_count] = -(int)(1u + ERR_STEP);
+        P.step->token = -(int)(1u + ERR_STEP);
+        P.step->count = step_count + 1;
+      }
+      return;
+    }
   }
+  if (tid == 0 && (xcc & 15u) >= (uint32_t)NXCD) raise_error(ws, ERR_XCD);
   const uint32_t lb = WS_LOCAL + g * LOCAL_WORDS;  // this XCD's exchange region
   const int L = P.num_layers;
   const bool lm = !(P.mode & MODE_NO_LMHEAD);
 
   // attention chunking: nsplit chunks of <= 2 KV_CAP positions, chunk j on workgroup (g, j),
   // attended in npass LDS passes of <= KV_CAP positions (rows KV_CAP.. in the second)
-  const int p = P.position, n_ctx = p + 1;
-  const int nsplit = SPLIT ? min(WG_PER_XCD, (n_ctx + KV_CAP - 1) / KV_CAP) : 1;
-  const int CH = (n_ctx + nsplit - 1) / nsplit;
+  const int n_ctx = p + 1;
+  const int nsplit = SPLIT ? plan_nsplit(n_ctx) : 1;
+  const int CH = SPLIT ? plan_chunk(n_ctx) : n_ctx;
   const bool att = j < nsplit;
   const int c0 = j * CH;
   const int nc = att ? min(n_ctx, c0 + CH) - c0 : 0;
@@ -813,8 +857,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         if (!att) burst(layer);
       }
       if (att) {
-        // this wave's K/V copy of the layer has landed (S_LOADS_AFTER_KV loads followed it)
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S_LOADS_AFTER_KV) : "memory");
+        // this wave's K/V copy of the layer has landed: all of the wave's vector-memory
+        // operations are awaited (the copy is inline assembly the compiler does not count;
+        // the o_proj loads issued after it are needed right after the attention anyway)
+        wait_vmem();
         for (int ps = 0; ps < npass; ps++) {
           if (ps == 1) {
             // second pass: rows KV_CAP .. nc-1 of the chunk replace the first pass's rows
@@ -954,7 +1000,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       // ---------------- gather h (each poll wave its half, with the sum of squares), RMSNorm
       float ss;
       if (layer == 0) {
-        const uint16_t* src = (P.mode & MODE_INPUT_HIDDEN) ? P.hidden_in : P.embed + (size_t)P.token * H;
+        const uint16_t* src = (P.mode & MODE_INPUT_HIDDEN) ? P.hidden_in : P.embed + (size_t)token * H;
         ss = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -1246,6 +1292,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     }
     BAR();  // P00
     BAR();  // P0
+    if (SPLIT && j == 0) st4_plain(ws + lb + LX_ATT + 4 * lane, u32x4{0u, 0u, 0u, 0u});
     uint32_t target = 0;
     for (int layer = 0; layer < L; layer++) {
       const uint32_t tag = tag_of(epoch, layer);
@@ -1479,7 +1526,15 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   }
   if (tid == 0) {
     const uint32_t err = wsb.ld1(WS_ERR * 4u);
-    *P.out_token = err ? -(int)(1u + err) : tok;
+    const int res = err ? -(int)(1u + err) : tok;
+    *P.out_token = res;
+    if (P.mode & MODE_DEVICE_STEP) {
+      // the next launch's input: this token at the next position, with the next epoch (a
+      // failed step keeps its position, and its negative token stops the launches after it)
+      P.out_ids[step_count] = res;
+      *reinterpret_cast<u32x4*>(P.step) =
+          u32x4{(uint32_t)res, (uint32_t)(res >= 0 ? p + 1 : p), epoch + 1u, (uint32_t)(step_count + 1)};
+    }
     wsb.st1(0u, WS_ERR * 4u);
     wsb.st1(0u, WS_FINAL_TICKET * 4u);
   }
@@ -1521,23 +1576,29 @@ static int ensure_device(int dev) {
   return d.status = MQ_OK;
 }
 
-static int launch(DecodeParams& P, hipStream_t stream) {
+static std::atomic<int> g_cooperative{0};
+
+// split_instance < 0: chosen from P.position
+static int launch(DecodeParams& P, hipStream_t stream, int split_instance = -1) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return MQ_ERR_HIP;
   const int st = ensure_device(dev);
   if (st != MQ_OK) return st;
   P.ws = g_dev[dev].ws;
-  P.epoch = g_dev[dev].launches.fetch_add(1u, std::memory_order_relaxed) + 1u;
+  if (!(P.mode & MODE_DEVICE_STEP)) P.epoch = g_dev[dev].launches.fetch_add(1u, std::memory_order_relaxed) + 1u;
   if (!P.out_token) P.out_token = reinterpret_cast<int*>(g_dev[dev].ws + WS_WORDS);
   // All NWG workgroups must be resident at once. Each one needs a whole CU
   // (its LDS use exceeds half a CU's), ensure_device() checked that the GPU has
   // NWG such slots, and every inter-workgroup wait in the kernel ends in an
-  // error after a bounded spin, so an ordinary launch is used: a cooperative
-  // launch adds about 18 us of queue synchronisation per token on this stack.
+  // error after a bounded spin, so an ordinary launch is the default. The
+  // cooperative launch (the reference's) is kept as an option, for comparison.
   void* args[] = {&P};
-  const void* kern = P.position < KV_CAP ? reinterpret_cast<const void*>(mq_decode_kernel<false>)
-                                         : reinterpret_cast<const void*>(mq_decode_kernel<true>);
-  const hipError_t e = hipLaunchKernel(kern, dim3(NWG), dim3(NT), args, 0, stream);
+  const bool split = split_instance < 0 ? P.position >= KV_CAP : split_instance != 0;
+  const void* kern = split ? reinterpret_cast<const void*>(mq_decode_kernel<true>)
+                           : reinterpret_cast<const void*>(mq_decode_kernel<false>);
+  const hipError_t e = g_cooperative.load(std::memory_order_relaxed)
+                           ? hipLaunchCooperativeKernel(kern, dim3(NWG), dim3(NT), args, 0, stream)
+                           : hipLaunchKernel(kern, dim3(NWG), dim3(NT), args, 0, stream);
   return e == hipSuccess ? MQ_OK : MQ_ERR_HIP;
 }
 
@@ -1635,6 +1696,82 @@ extern "C" int mq_decode_layer(const void* hidden_in, void* hidden_out, const LD
   // No token output: the kernel's status word goes to the workspace tail.
   P.out_token = nullptr;
   return launch(P, stream);
+}
+
+extern "C" int mq_decode_step_init(MqDecodeStep* step, int token, int position, int capacity, hipStream_t stream) {
+  if (!step || token < 0 || token >= VOCAB || position < 0 || position >= MAX_CTX || capacity < 1) return MQ_ERR_ARG;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return MQ_ERR_HIP;
+  const int st = ensure_device(dev);
+  if (st != MQ_OK) return st;
+  // the epochs first .. first + capacity - 1 belong to these steps alone
+  const uint32_t first = g_dev[dev].launches.fetch_add((uint32_t)capacity, std::memory_order_relaxed) + 1u;
+  const MqDecodeStep h{token, position, first, 0};
+  return hipMemcpyAsync(step, &h, sizeof(h), hipMemcpyHostToDevice, stream) == hipSuccess &&
+                 hipStreamSynchronize(stream) == hipSuccess
+             ? MQ_OK
+             : MQ_ERR_HIP;
+}
+
+extern "C" int mq_decode_step_device(MqDecodeStep* step, int* out_ids, int out_capacity, int split_instance,
+                                     const void* embed_weight, const LDGLayerWeights* layer_weights,
+                                     const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
+                                     const void* sin_table, void* k_cache, void* v_cache, void* hidden_buffer,
+                                     void* g_normalized, int num_layers, int max_seq_len, float attn_scale,
+                                     hipStream_t stream) {
+  if (!step || !out_ids || out_capacity < 1 || !embed_weight || !layer_weights || !final_norm_weight ||
+      !lm_head_weight || !cos_table || !sin_table || !k_cache || !v_cache || !hidden_buffer)
+    return MQ_ERR_ARG;
+  if (num_layers < 1 || num_layers > MAX_LAYERS || max_seq_len < 1 || bad_scale(attn_scale) ||
+      (split_instance != 0 && split_instance != 1))
+    return MQ_ERR_ARG;
+  DecodeParams P{};
+  P.layers = layer_weights;
+  P.embed = static_cast<const uint16_t*>(embed_weight);
+  P.final_norm = static_cast<const uint16_t*>(final_norm_weight);
+  P.lm_head = static_cast<const uint16_t*>(lm_head_weight);
+  P.cos_tab = static_cast<const uint16_t*>(cos_table);
+  P.sin_tab = static_cast<const uint16_t*>(sin_table);
+  P.k_cache = static_cast<uint16_t*>(k_cache);
+  P.v_cache = static_cast<uint16_t*>(v_cache);
+  P.hidden_out = static_cast<uint16_t*>(hidden_buffer);
+  P.normed_out = static_cast<float*>(g_normalized);
+  P.out_token = nullptr;
+  P.num_layers = num_layers;
+  P.max_seq_len = max_seq_len;
+  P.attn_scale = attn_scale;
+  P.mode = MODE_DEVICE_STEP;
+  P.step = step;
+  P.out_ids = out_ids;
+  P.out_capacity = out_capacity;
+  return launch(P, stream, split_instance);
+}
+
+extern "C" int mq_decode_plan(int position, int* instance, int* nsplit, int* chunk, int* npass) {
+  if (position < 0 || position >= MAX_CTX) return MQ_ERR_ARG;
+  const int n = position + 1;
+  const int ns = plan_nsplit(n), ch = plan_chunk(n);
+  if (instance) *instance = position >= KV_CAP ? 1 : 0;
+  if (nsplit) *nsplit = ns;
+  if (chunk) *chunk = ch;
+  if (npass) *npass = (ch + KV_CAP - 1) / KV_CAP;
+  return MQ_OK;
+}
+
+extern "C" int mq_set_launch_mode(int cooperative) {
+  return g_cooperative.exchange(cooperative ? 1 : 0, std::memory_order_relaxed);
+}
+
+extern "C" int mq_debug_set_error(int device, unsigned flags) {
+  const int st = ensure_device(device);
+  if (st != MQ_OK) return st;
+  int cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess) return MQ_ERR_HIP;
+  if (hipSetDevice(device) != hipSuccess) return MQ_ERR_HIP;
+  hipError_t e = hipMemcpy(g_dev[device].ws + WS_ERR, &flags, sizeof(flags), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (hipSetDevice(cur) != hipSuccess) return MQ_ERR_HIP;
+  return e == hipSuccess ? MQ_OK : MQ_ERR_HIP;
 }
 
 extern "C" int mq_reset_workspace(int device) {

@@ -111,3 +111,50 @@ def test_strerror():
     assert b"argument" in L.mq_strerror(-1)
     with pytest.raises(_abi.MegakernelError):
         _abi.check(-1, "x")
+
+
+def test_decode_plan_bounds_every_position():
+    """The kernel's attention split, queried through the C ABI for every accepted position:
+    chunks fit two LDS passes of 256 rows, none is empty and together they cover the
+    context (the kernel also proves this at compile time with a static_assert)."""
+    L = _abi.lib()
+    inst, ns, ch, npass = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    refs = [ctypes.byref(x) for x in (inst, ns, ch, npass)]
+    for p in range(16384):
+        assert L.mq_decode_plan(p, *refs) == _abi.MQ_OK
+        n = p + 1
+        assert inst.value == (0 if p < 256 else 1)
+        assert 1 <= ns.value <= 32 and ch.value <= 512 and npass.value == (ch.value + 255) // 256 <= 2
+        assert ch.value * ns.value >= n and (ns.value - 1) * ch.value < n
+        if p < 256:
+            assert ns.value == 1 and ch.value == n
+    for p in (-1, 16384):
+        assert L.mq_decode_plan(p, *refs) == _abi.MQ_ERR_ARG
+    assert _abi.decode_plan(8447) == {"instance": 1, "nsplit": 32, "chunk": 264, "npass": 2}
+
+
+def test_device_step_entries_reject_invalid_arguments():
+    L = _abi.lib()
+    assert L.mq_decode_step_init(None, 1, 0, 4, None) == _abi.MQ_ERR_ARG
+    assert L.mq_decode_step_init(1, -1, 0, 4, None) == _abi.MQ_ERR_ARG
+    assert L.mq_decode_step_init(1, 151936, 0, 4, None) == _abi.MQ_ERR_ARG
+    assert L.mq_decode_step_init(1, 1, 16384, 4, None) == _abi.MQ_ERR_ARG
+    assert L.mq_decode_step_init(1, 1, 0, 0, None) == _abi.MQ_ERR_ARG
+    good = dict(step=1, out=1, cap=4, split=0)
+
+    def args(**o):
+        a = dict(good, **o)
+        return [a["step"], a["out"], a["cap"], a["split"]] + [1] * 10 + [28, 16, 0.088, None]
+    for bad in (dict(step=None), dict(out=None), dict(cap=0), dict(split=2), dict(split=-1)):
+        assert L.mq_decode_step_device(*args(**bad)) == _abi.MQ_ERR_ARG
+    a = args()
+    a[14] = 0  # num_layers
+    assert L.mq_decode_step_device(*a) == _abi.MQ_ERR_ARG
+    assert ctypes.sizeof(_abi.MqDecodeStep) == 16
+
+
+def test_launch_mode_switch():
+    L = _abi.lib()
+    prev = L.mq_set_launch_mode(1)
+    assert L.mq_set_launch_mode(prev) == 1
+    assert L.mq_set_launch_mode(prev) == prev

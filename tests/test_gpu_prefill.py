@@ -16,7 +16,7 @@ from megaqwen_amd import _abi
 from megaqwen_amd import megakernel_decode as MK
 from megaqwen_amd import rope, weights
 from oracle import qwen3_oracle as O
-from parity_helpers import LOGIT_MAX_ABS, TIE_TOL, f32, hf_tie_set, ulp_close
+from parity_helpers import EXACT_FLOORS, LOGIT_MAX_ABS, TIE_TOL, f32, hf_tie_set, ulp_close
 
 pytestmark = pytest.mark.gpu
 
@@ -175,6 +175,7 @@ def test_config4_prefill_then_decode_vs_hf(prefill_decoder):
             assert g in hf_tie_set(fx, step), (step, g)
         exact += g == r
     print(f"config 4 teacher-forced: {exact}/{len(hf_ids)} ids identical to HF")
+    assert exact >= EXACT_FLOORS["c4_teacher_forced"]
 
 
 def test_config4_free_running(prefill_decoder):
@@ -193,6 +194,7 @@ def test_config4_free_running(prefill_decoder):
     match = next((i for i, (a, b) in enumerate(zip(ids, hf_ids)) if a != b), len(hf_ids))
     print(f"config 4 free-running: identical for {match}/{len(hf_ids)}; first HF near-tie at {first_tie}")
     assert ids[:first_tie] == hf_ids[:first_tie]
+    assert match >= EXACT_FLOORS["c4_free_running"]
 
 
 def test_config5_long_context_vs_hf(gpu_weights):
@@ -218,3 +220,4 @@ def test_config5_long_context_vs_hf(gpu_weights):
             assert g in hf_tie_set(fx, step), (step, g)
         exact += g == r
     print(f"config 5 teacher-forced: {exact}/{len(hf_ids)} ids identical to HF")
+    assert exact >= EXACT_FLOORS["c5_teacher_forced"]
