@@ -89,6 +89,23 @@ int launch_ldg_decode_with_logits(int input_token_id, int* output_token_id, floa
                                   void* block_max_vals, void* block_max_idxs, int num_layers, int position,
                                   int cache_len, int max_seq_len, float attn_scale, hipStream_t stream);
 
+/* launch_ldg_decode without any allocation, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Same arguments and results as
+ * launch_ldg_decode minus the reference's unused scratch pointers (output_token_id,
+ * hidden_buffer and g_normalized are written as there; g_normalized may be NULL). Its
+ * kernels use a file-scope device array of about 1.2 MB (the decode workspace) instead
+ * of the library's allocated workspace: each GPU holds one copy from the first call on
+ * that device until the process ends. The first call on a device does the set-up (a
+ * device query and the array's address); call it once before any graph capture.
+ * Limits: num_layers <= 32, position < 16384 (MQ_ERR_ARG past them). Calls on one GPU
+ * share its array: calls that overlap in time on one device race. */
+int launch_ldg_decode_noalloc(int input_token_id, int* output_token_id, const void* embed_weight,
+                              const LDGLayerWeights* layer_weights, const void* final_norm_weight,
+                              const void* lm_head_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                              void* v_cache, void* hidden_buffer, void* g_normalized, int num_layers, int position,
+                              int cache_len, int max_seq_len, float attn_scale, hipStream_t stream);
+
 /* One decoder block at `position` on a given bf16 hidden vector (no embedding,
  * no LM head): hidden_out = layer(hidden_in); K/V slot `position` of the
  * single-layer caches k_cache/v_cache ([1, 8, max_seq_len, 128]) is written.

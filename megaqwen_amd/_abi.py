@@ -56,6 +56,7 @@ _DECODE_ARGS = [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, 
 SIGNATURES = {
     "launch_ldg_decode": _DECODE_ARGS,
     "launch_ldg_decode_with_logits": _DECODE_ARGS[:2] + [_vp] + _DECODE_ARGS[2:],
+    "launch_ldg_decode_noalloc": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],
     "mq_decode_layer": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _f, _vp],
     # ids, out, seq_len, embed, layers (host array), final norm, lm head, cos, sin, k, v, 17 scratch,
     # num_layers, max_seq_len, scale, stream

@@ -1553,21 +1553,27 @@ struct DeviceState {
 static std::mutex g_mu;
 static DeviceState g_dev[64];
 
+// The device can hold all NWG workgroups of both kernel instances at once (no allocation).
+static int check_device(int dev) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return MQ_ERR_HIP;
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0 || !prop.cooperativeLaunch) return MQ_ERR_DEVICE;
+  for (const void* k : {reinterpret_cast<const void*>(mq_decode_kernel<false>),
+                        reinterpret_cast<const void*>(mq_decode_kernel<true>)}) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NT, 0) != hipSuccess) return MQ_ERR_HIP;
+    if (per_cu * prop.multiProcessorCount < NWG) return MQ_ERR_DEVICE;
+  }
+  return MQ_OK;
+}
+
 static int ensure_device(int dev) {
   if (dev < 0 || dev >= 64) return MQ_ERR_DEVICE;
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState& d = g_dev[dev];
   if (d.init) return d.status;
   d.init = true;
-  hipDeviceProp_t prop;
-  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return d.status = MQ_ERR_HIP;
-  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0 || !prop.cooperativeLaunch) return d.status = MQ_ERR_DEVICE;
-  for (const void* k : {reinterpret_cast<const void*>(mq_decode_kernel<false>),
-                        reinterpret_cast<const void*>(mq_decode_kernel<true>)}) {
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NT, 0) != hipSuccess) return d.status = MQ_ERR_HIP;
-    if (per_cu * prop.multiProcessorCount < NWG) return d.status = MQ_ERR_DEVICE;
-  }
+  if ((d.status = check_device(dev)) != MQ_OK) return d.status;
   void* p = nullptr;
   if (hipMalloc(&p, WS_BYTES) != hipSuccess) return d.status = MQ_ERR_ALLOC;
   if (hipMemset(p, 0, WS_BYTES) != hipSuccess) return d.status = MQ_ERR_HIP;
@@ -1578,15 +1584,55 @@ static int ensure_device(int dev) {
 
 static std::atomic<int> g_cooperative{0};
 
-// split_instance < 0: chosen from P.position
-static int launch(DecodeParams& P, hipStream_t stream, int split_instance = -1) {
+// Workspace of launch_ldg_decode_noalloc: the same layout as the allocated workspace,
+// one copy per GPU (in the code object's global memory, zero when the code object is
+// loaded), kept until the process ends. Host code never passes `scratch` itself: its
+// device address comes from hipGetSymbolAddress, per device.
+static __device__ __align__(256) uint32_t scratch[WS_WORDS];
+
+struct NoAllocState {
+  bool init = false;
+  int status = MQ_OK;
+  uint32_t* ptr = nullptr;  // this device's address of `scratch`
+};
+static NoAllocState g_noalloc[64];
+
+// Set-up of the no-allocation path on device `dev` (current): the device checks and the
+// device address of `scratch`, once per device. Allocates nothing.
+static int noalloc_workspace(int dev, uint32_t** ws) {
+  if (dev < 0 || dev >= 64) return MQ_ERR_DEVICE;
+  std::lock_guard<std::mutex> lk(g_mu);
+  NoAllocState& d = g_noalloc[dev];
+  if (!d.init) {
+    d.init = true;
+    if ((d.status = check_device(dev)) == MQ_OK) {
+      void* p = nullptr;
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+        d.status = MQ_ERR_HIP;
+      else
+        d.ptr = static_cast<uint32_t*>(p);
+    }
+  }
+  *ws = d.ptr;
+  return d.status;
+}
+
+// split_instance < 0: chosen from P.position. noalloc: the `scratch` workspace instead of
+// the allocated one.
+static int launch(DecodeParams& P, hipStream_t stream, int split_instance = -1, bool noalloc = false) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return MQ_ERR_HIP;
-  const int st = ensure_device(dev);
-  if (st != MQ_OK) return st;
-  P.ws = g_dev[dev].ws;
+  if (noalloc) {
+    const int st = noalloc_workspace(dev, &P.ws);
+    if (st != MQ_OK) return st;
+    if (!P.out_token) return MQ_ERR_ARG;
+  } else {
+    const int st = ensure_device(dev);
+    if (st != MQ_OK) return st;
+    P.ws = g_dev[dev].ws;
+    if (!P.out_token) P.out_token = reinterpret_cast<int*>(g_dev[dev].ws + WS_WORDS);
+  }
   if (!(P.mode & MODE_DEVICE_STEP)) P.epoch = g_dev[dev].launches.fetch_add(1u, std::memory_order_relaxed) + 1u;
-  if (!P.out_token) P.out_token = reinterpret_cast<int*>(g_dev[dev].ws + WS_WORDS);
   // All NWG workgroups must be resident at once. Each one needs a whole CU
   // (its LDS use exceeds half a CU's), ensure_device() checked that the GPU has
   // NWG such slots, and every inter-workgroup wait in the kernel ends in an
@@ -1619,17 +1665,13 @@ static bool bad_scale(float s) { return !(s > 0.f) || !isfinite(s); }
 
 using namespace mq;
 
-extern "C" int launch_ldg_decode_with_logits(int input_token_id, int* output_token_id, float* logits_output,
-                                             const void* embed_weight, const LDGLayerWeights* layer_weights,
-                                             const void* final_norm_weight, const void* lm_head_weight,
-                                             const void* cos_table, const void* sin_table, void* k_cache,
-                                             void* v_cache, void* hidden_buffer, void* g_activations, void* g_residual,
-                                             void* g_q, void* g_k, void* g_v, void* g_attn_out,
-                                             void* g_mlp_intermediate, void* g_normalized, void* block_max_vals,
-                                             void* block_max_idxs, int num_layers, int position, int cache_len,
-                                             int max_seq_len, float attn_scale, hipStream_t stream) {
-  (void)g_activations; (void)g_residual; (void)g_q; (void)g_k; (void)g_v; (void)g_attn_out;
-  (void)g_mlp_intermediate; (void)block_max_vals; (void)block_max_idxs;
+// Body of the full-model decode entry points (the reference's unused scratch pointers
+// are not passed on).
+static int decode_entry(int input_token_id, int* output_token_id, float* logits_output, const void* embed_weight,
+                        const LDGLayerWeights* layer_weights, const void* final_norm_weight,
+                        const void* lm_head_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                        void* v_cache, void* hidden_buffer, void* g_normalized, int num_layers, int position,
+                        int cache_len, int max_seq_len, float attn_scale, hipStream_t stream, bool noalloc) {
   if (!output_token_id || !embed_weight || !layer_weights || !final_norm_weight || !lm_head_weight || !cos_table ||
       !sin_table || !k_cache || !v_cache || !hidden_buffer)
     return MQ_ERR_ARG;
@@ -1655,7 +1697,23 @@ extern "C" int launch_ldg_decode_with_logits(int input_token_id, int* output_tok
   P.max_seq_len = max_seq_len;
   P.attn_scale = attn_scale;
   P.mode = logits_output ? MODE_LOGITS : 0;
-  return launch(P, stream);
+  return launch(P, stream, -1, noalloc);
+}
+
+extern "C" int launch_ldg_decode_with_logits(int input_token_id, int* output_token_id, float* logits_output,
+                                             const void* embed_weight, const LDGLayerWeights* layer_weights,
+                                             const void* final_norm_weight, const void* lm_head_weight,
+                                             const void* cos_table, const void* sin_table, void* k_cache,
+                                             void* v_cache, void* hidden_buffer, void* g_activations, void* g_residual,
+                                             void* g_q, void* g_k, void* g_v, void* g_attn_out,
+                                             void* g_mlp_intermediate, void* g_normalized, void* block_max_vals,
+                                             void* block_max_idxs, int num_layers, int position, int cache_len,
+                                             int max_seq_len, float attn_scale, hipStream_t stream) {
+  (void)g_activations; (void)g_residual; (void)g_q; (void)g_k; (void)g_v; (void)g_attn_out;
+  (void)g_mlp_intermediate; (void)block_max_vals; (void)block_max_idxs;
+  return decode_entry(input_token_id, output_token_id, logits_output, embed_weight, layer_weights, final_norm_weight,
+                      lm_head_weight, cos_table, sin_table, k_cache, v_cache, hidden_buffer, g_normalized, num_layers,
+                      position, cache_len, max_seq_len, attn_scale, stream, false);
 }
 
 extern "C" int launch_ldg_decode(int input_token_id, int* output_token_id, const void* embed_weight,
@@ -1671,6 +1729,17 @@ extern "C" int launch_ldg_decode(int input_token_id, int* output_token_id, const
                                        hidden_buffer, g_activations, g_residual, g_q, g_k, g_v, g_attn_out,
                                        g_mlp_intermediate, g_normalized, block_max_vals, block_max_idxs, num_layers,
                                        position, cache_len, max_seq_len, attn_scale, stream);
+}
+
+extern "C" int launch_ldg_decode_noalloc(int input_token_id, int* output_token_id, const void* embed_weight,
+                                         const LDGLayerWeights* layer_weights, const void* final_norm_weight,
+                                         const void* lm_head_weight, const void* cos_table, const void* sin_table,
+                                         void* k_cache, void* v_cache, void* hidden_buffer, void* g_normalized,
+                                         int num_layers, int position, int cache_len, int max_seq_len,
+                                         float attn_scale, hipStream_t stream) {
+  return decode_entry(input_token_id, output_token_id, nullptr, embed_weight, layer_weights, final_norm_weight,
+                      lm_head_weight, cos_table, sin_table, k_cache, v_cache, hidden_buffer, g_normalized, num_layers,
+                      position, cache_len, max_seq_len, attn_scale, stream, true);
 }
 
 extern "C" int mq_decode_layer(const void* hidden_in, void* hidden_out, const LDGLayerWeights* layer_weights,

@@ -158,3 +158,11 @@ def test_launch_mode_switch():
     prev = L.mq_set_launch_mode(1)
     assert L.mq_set_launch_mode(prev) == 1
     assert L.mq_set_launch_mode(prev) == prev
+
+
+def test_noalloc_entry_rejects_sizes_past_its_limit():
+    L = _abi.lib()
+    base = [1, 1] + [1] * 9 + [1]
+    assert L.launch_ldg_decode_noalloc(*(base + [28, 16384, 16385, 20000, 0.088, None])) == _abi.MQ_ERR_ARG
+    assert L.launch_ldg_decode_noalloc(*(base + [33, 0, 1, 16, 0.088, None])) == _abi.MQ_ERR_ARG
+    assert L.launch_ldg_decode_noalloc(*([1, None] + [1] * 9 + [1, 28, 0, 1, 16, 0.088, None])) == _abi.MQ_ERR_ARG
