@@ -1292,7 +1292,15 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     }
     BAR();  // P00
     BAR();  // P0
+    // Every launch writes or clears every exchange word it could ever poll, so that the
+    // content a poll can find before the awaited write is at most one launch old, whose
+    // tags differ from the polled ones: a split launch clears the attention-output words
+    // (read by unsplit launches only), and a workgroup without a chunk partial to store
+    // clears its chunk's record (read by split launches with more chunks).
     if (SPLIT && j == 0) st4_plain(ws + lb + LX_ATT + 4 * lane, u32x4{0u, 0u, 0u, 0u});
+    if (!SPLIT || !att)
+      for (int i = lane; i < 2 * 2 * (int)APART / 4; i += 64)
+        st4_plain(ws + lb + LX_PART + 2 * 2 * APART * j + 4 * i, u32x4{0u, 0u, 0u, 0u});
     uint32_t target = 0;
     for (int layer = 0; layer < L; layer++) {
       const uint32_t tag = tag_of(epoch, layer);
