@@ -38,14 +38,16 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--positions", type=str, default="1,200,1024,2048")
+    ap.add_argument("--positions", type=str, default="1,200,1024,2048,8192,8447")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (for rocprofv3 counter scaling)")
     ap.add_argument("--cpu-decode-tokens", type=int, default=32)
-    ap.add_argument("--prefill-len", type=int, default=512, help="prompt length of the prefill timing (config 4)")
+    ap.add_argument("--prefill-lens", type=str, default="512,8192",
+                    help="prompt lengths of the prefill timings (configs 4 and 5)")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-coop", action="store_true", help="skip the cooperative-launch comparison")
     return ap.parse_args()
 
 
@@ -108,7 +110,8 @@ def time_prefill(dec, ids, steps: int, warmup: int):
 
 
 def e2e_generate(dec, prompt, n_new):
-    """Reference-style generation loop (per-token device->host read), wall-clock tok/s."""
+    """Reference-style generation loop (per-token device->host read), wall-clock tok/s
+    over the whole config-3 run (prompt steps included); returns (tok/s, ids)."""
     import torch
 
     dec.reset()
@@ -116,12 +119,36 @@ def e2e_generate(dec, prompt, n_new):
     t0 = time.perf_counter()
     for t in prompt[:-1]:
         dec.decode_step(t)
-    cur = prompt[-1]
+    cur, ids = prompt[-1], []
     for _ in range(n_new):
         cur = dec.decode_step(cur)
+        ids.append(cur)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    return (len(prompt) - 1 + n_new) / dt
+    return (len(prompt) - 1 + n_new) / dt, ids
+
+
+def e2e_generate_device(dec, prompt, n_new, use_graph=True):
+    """The same run with the device-resident loop: prompt steps launched without host
+    reads, generated tokens fed back on the device, one host read per 64-step chunk
+    (replayed HIP graphs)."""
+    import torch
+
+    dec.reset()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for t in prompt[:-1]:
+        dec.decode_step_async(t)
+    ids = dec.generate_device(prompt[-1], n_new, use_graph=use_graph, chunk=64)
+    end.record()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    n = len(prompt) - 1 + n_new
+    # device time of the same launches (HIP events on their stream): the kernel rate of this
+    # workload, whose positions run from 0 to 2062 (later positions cost more)
+    return n / dt, ids, n / (start.elapsed_time(end) * 1e-3)
 
 
 def cpu_baseline(n_decode: int):
@@ -143,6 +170,7 @@ def cpu_baseline(n_decode: int):
     model = MG.hf_model(sd)
     prompt = weights.random_prompt(8, seed=1)
     runs = []
+    ids = []
     for r in range(4):
         cache = DynamicCache(config=model.config)
         with torch.no_grad():
@@ -150,12 +178,22 @@ def cpu_baseline(n_decode: int):
             out = model(input_ids=torch.tensor([prompt]), past_key_values=cache, use_cache=True)
             t1 = time.perf_counter()
             nxt = int(torch.argmax(out.logits[0, -1].float()))
+            ids = [nxt]
             for _ in range(n_decode):
                 out = model(input_ids=torch.tensor([[nxt]]), past_key_values=cache, use_cache=True)
                 nxt = int(torch.argmax(out.logits[0, -1].float()))
+                ids.append(nxt)
             t2 = time.perf_counter()
         if r > 0:
             runs.append((t1 - t0, (t2 - t1) / n_decode))
+    # HF's own greedy ids on this host against the fixture written on the build host
+    # (tests/golden/greedy_c1.npz): is HF bit-reproducible across CPUs?
+    import numpy as np
+    fx = np.load(os.path.join(ROOT, "tests", "golden", "greedy_c1.npz"), allow_pickle=False)
+    want = fx["ids"].tolist()
+    got = ids[:len(want)]
+    same = sum(a == b for a, b in zip(got, want))
+    first_diff = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), None)
     prefill_s = statistics.median(r[0] for r in runs)
     per_tok = statistics.median(r[1] for r in runs)
     model_name = ""
@@ -175,6 +213,8 @@ def cpu_baseline(n_decode: int):
                    f"(sdpa, use_cache), seeded weights, 8-token prompt then {n_decode} greedy decode steps; "
                    f"median of 3 runs after 1 warm-up; prefill {prefill_s * 1e3:.1f} ms; "
                    f"os.cpu_count()={os.cpu_count()}; cpu='{model_name or platform.processor()}'"),
+        "hf_ids_vs_build_host_fixture": {"same": same, "of": len(want), "first_diff_step": first_diff,
+                                         "ids": got},
     }
 
 
@@ -194,12 +234,13 @@ def main():
     from megaqwen_amd import weights
 
     t0 = time.perf_counter()
-    max_seq = 2048 + 16
+    max_seq = 8448  # config 5: 8192-token prompt + 256 decode steps
+    prefill_lens = [] if args.no_prefill else [int(x) for x in args.prefill_lens.split(",") if x]
     w = MK.load_qwen3_weights(seed=0, max_seq_len=max_seq)
     log(f"weights ready in {time.perf_counter() - t0:.1f}s")
     dec = MK.MegakernelPrefillDecoder(w["embed_weight"], w["layer_weights"], w["final_norm_weight"],
                                       w["lm_head_weight"], w["cos_table"], w["sin_table"], C.NUM_LAYERS, max_seq,
-                                      max(args.prefill_len, 1))
+                                      max(prefill_lens + [1]))
     positions = [int(p) for p in args.positions.split(",")]
     per_pos = {}
     for p in positions:
@@ -210,23 +251,40 @@ def main():
                       "wall_ms": wall_ms}
         log(f"pos {p}: {ms * 1e3:.1f} us/step, {1e3 / ms:.0f} tok/s, "
             f"{per_pos[p]['hbm_gbs']:.0f} GB/s algorithmic ({per_pos[p]['hbm_gbs'] / HBM_PEAK_GBS:.1%} of 8 TB/s)")
-    prefill = None
-    if not args.no_prefill:
-        S = args.prefill_len
-        pms = time_prefill(dec, weights.random_prompt(S, seed=1), steps=10, warmup=2)
+    coop = None
+    if not args.no_coop:
+        from megaqwen_amd import _abi
+
+        prev = _abi.lib().mq_set_launch_mode(1)
+        try:
+            cms, _ = time_decode(dec, 200, max(20, args.steps // 2), args.warmup)
+        finally:
+            _abi.lib().mq_set_launch_mode(prev)
+        coop = {"us_per_step": round(cms * 1e3, 2), "ordinary_us_per_step": round(per_pos[200]["ms"] * 1e3, 2),
+                "extra_us": round((cms - per_pos[200]["ms"]) * 1e3, 2)}
+        log(f"cooperative launch at pos 200: {cms * 1e3:.1f} us/step ({coop['extra_us']:+.1f} us vs ordinary)")
+    prefill = []
+    for S in prefill_lens:
+        pms = time_prefill(dec, weights.random_prompt(S, seed=1), steps=10 if S <= 1024 else 4, warmup=2)
         fl = C.prefill_flops(S)
-        prefill = {"seq_len": S, "ms": round(pms, 4), "tok_s": round(S / (pms * 1e-3), 1),
-                   "tflops": round(fl / (pms * 1e-3) / 1e12, 2), "flops": fl,
-                   "mfma_frac": round(fl / (pms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)}
-        log(f"prefill S={S}: {pms:.3f} ms, {prefill['tok_s']:.0f} tok/s, {prefill['tflops']:.1f} TFLOP/s "
-            f"({prefill['mfma_frac']:.1%} of {MFMA_PEAK_TFLOPS:.0f} dense bf16)")
+        prefill.append({"seq_len": S, "ms": round(pms, 4), "tok_s": round(S / (pms * 1e-3), 1),
+                        "tflops": round(fl / (pms * 1e-3) / 1e12, 2), "flops": fl,
+                        "mfma_frac": round(fl / (pms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)})
+        log(f"prefill S={S}: {pms:.3f} ms, {prefill[-1]['tok_s']:.0f} tok/s, {prefill[-1]['tflops']:.1f} TFLOP/s "
+            f"({prefill[-1]['mfma_frac']:.1%} of {MFMA_PEAK_TFLOPS:.0f} dense bf16)")
     main_p = 200
     ms = per_pos[main_p]["ms"]
     e2e = None
     if not args.no_e2e:
         prompt = weights.random_prompt(16, seed=1)
-        e2e = e2e_generate(dec, prompt, 2048 - 16)
-        log(f"end-to-end generate (16-token prompt + {2048 - 16} tokens, per-token host read): {e2e:.0f} tok/s")
+        host_rate, host_ids = e2e_generate(dec, prompt, 2048 - 16)
+        dev_rate, dev_ids, kern_rate = e2e_generate_device(dec, prompt, 2048 - 16)
+        e2e = {"host_read_per_token_tok_s": round(host_rate, 1), "device_resident_tok_s": round(dev_rate, 1),
+               "kernel_rate_same_workload_tok_s": round(kern_rate, 1), "same_ids": host_ids == dev_ids,
+               "workload": "config 3: 16-token prompt + 2032 greedy tokens, wall clock"}
+        log(f"end-to-end config 3: {host_rate:.0f} tok/s with a host read per token, {dev_rate:.0f} tok/s "
+            f"device-resident (graph replays; device time of the same launches {kern_rate:.0f} tok/s); "
+            f"ids equal: {host_ids == dev_ids}")
     bytes_200 = C.decode_bytes(main_p)
     achieved = bytes_200 / (ms * 1e-3) / 1e9
     traffic = None
@@ -248,14 +306,16 @@ def main():
         "dtype": "bf16",
         "data": "synthetic: seeded random-init Qwen3-0.6B weights N(0,0.02) (seed 0), norms = 1",
         "config": {"workload": "full-model greedy decode step, batch 1, query at position 200 "
-                               "(BASELINE configs[2] decode sweep; other positions below)",
+                               "(BASELINE configs[2] decode sweep; other positions below, 8192/8447 = config 5)",
                    "position": main_p, "num_layers": C.NUM_LAYERS, "max_seq_len": max_seq},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "positions": {str(p): {"tok_s": round(v["tok_s"], 1), "hbm_gbs": round(v["hbm_gbs"], 1),
                                "roofline_frac": round(v["hbm_gbs"] / HBM_PEAK_GBS, 4), "us_per_step": round(v["ms"] * 1e3, 2)}
                       for p, v in per_pos.items()},
-        "e2e_generate_tok_s": None if e2e is None else round(e2e, 1),
+        "e2e_generate_tok_s": None if e2e is None else e2e["device_resident_tok_s"],
+        "e2e": e2e,
+        "cooperative_launch": coop,
         "prefill": prefill,
         "cpu_baseline": cpu,
     }
