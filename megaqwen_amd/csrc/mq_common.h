@@ -49,17 +49,6 @@ __device__ __forceinline__ void unpack8(const u32x4& w, float (&f)[8]) {
   f[4] = bflo(w.z); f[5] = bfhi(w.z);
   f[6] = bflo(w.w); f[7] = bfhi(w.w);
 }
-__device__ __forceinline__ float dot8(const u32x4& w, const float (&x)[8]) {
-  float s = bflo(w.x) * x[0];
-  s = fmaf(bfhi(w.x), x[1], s);
-  s = fmaf(bflo(w.y), x[2], s);
-  s = fmaf(bfhi(w.y), x[3], s);
-  s = fmaf(bflo(w.z), x[4], s);
-  s = fmaf(bfhi(w.z), x[5], s);
-  s = fmaf(bflo(w.w), x[6], s);
-  s = fmaf(bfhi(w.w), x[7], s);
-  return s;
-}
 
 // Two bf16 values (low half first) in one word.
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
@@ -124,9 +113,17 @@ __device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
 #pragma unroll
   for (int k = 0; k < N; k++) v[k] = (readlane(v[k], 0) + readlane(v[k], 16)) + (readlane(v[k], 32) + readlane(v[k], 48));
 }
-// row16_sum of N independent values, interleaved the same way
+// wave_sum of N values at once (N a multiple of 4) with the same additions in the same
+// order as wave_sum, so the results are bitwise identical: the 16-lane butterfly of each
+// row, then rows 0 + 1 and 2 + 3 (lanes l, l + 16 meet through v_permlane16_swap, values
+// k and k + N/4 trading rows), then (0 + 1) + (2 + 3) (lanes l, l + 32 meet through
+// v_permlane32_swap, values k and k + N/2 trading halves). The swaps replace wave_sum's
+// four readlanes and three scalar-sourced adds per value. On return lane l holds in v[k],
+// k < N/4, the total of value k + (l / 16) * (N / 4).
 template <int N>
-__device__ __forceinline__ void row16_sum_n(float (&v)[N]) {
+__device__ __forceinline__ void wave_sum_t(float (&v)[N]) {
+  static_assert(N % 4 == 0, "N must be a multiple of 4");
+  constexpr int H2 = N / 2, H4 = N / 4;
 #pragma unroll
   for (int k = 0; k < N; k++) v[k] += dpp<0xB1>(v[k]);
 #pragma unroll
@@ -135,8 +132,45 @@ __device__ __forceinline__ void row16_sum_n(float (&v)[N]) {
   for (int k = 0; k < N; k++) v[k] += dpp<0x141>(v[k]);
 #pragma unroll
   for (int k = 0; k < N; k++) v[k] += dpp<0x140>(v[k]);
+  // values k and k + N/4 (and k + N/2 and k + 3N/4) trade rows: afterwards row 0 holds
+  // value k as R0 + R1, row 1 value k + N/4 as R0 + R1, rows 2 and 3 the same as R2 + R3
+#pragma unroll
+  for (int k = 0; k < H4; k++)
+#pragma unroll
+    for (int b = 0; b < N; b += H2) {
+      const auto r =
+          __builtin_amdgcn_permlane16_swap(__float_as_uint(v[b + k]), __float_as_uint(v[b + k + H4]), false, false);
+      v[b + k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+  // values k and k + N/2 trade halves: lanes l and l + 32 add (R0 + R1) + (R2 + R3)
+#pragma unroll
+  for (int k = 0; k < H4; k++) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k + H2]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
 }
-// wave_max of N independent values, interleaved like wave_sum_n (results identical to wave_max)
+// Sums of N values (N even) over lanes 0..31 and, separately, over lanes 32..63, as
+// row16_sum followed by rows 0 + 1 and 2 + 3: on return lane l holds in v[k], k < N/2,
+// the total of value k + ((l / 16) & 1) * (N / 2) over lane half l / 32.
+template <int N>
+__device__ __forceinline__ void half_sum_t(float (&v)[N]) {
+  static_assert(N % 2 == 0, "N must be even");
+  constexpr int H2 = N / 2;
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0xB1>(v[k]);
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0x4E>(v[k]);
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0x141>(v[k]);
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] += dpp<0x140>(v[k]);
+#pragma unroll
+  for (int k = 0; k < H2; k++) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k + H2]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+// Wave-wide maxima of N independent values, interleaved like wave_sum_n
 template <int N>
 __device__ __forceinline__ void wave_max_n(float (&v)[N]) {
 #pragma unroll
@@ -150,13 +184,6 @@ __device__ __forceinline__ void wave_max_n(float (&v)[N]) {
 #pragma unroll
   for (int k = 0; k < N; k++)
     v[k] = fmaxf(fmaxf(readlane(v[k], 0), readlane(v[k], 16)), fmaxf(readlane(v[k], 32), readlane(v[k], 48)));
-}
-__device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, dpp<0xB1>(v));
-  v = fmaxf(v, dpp<0x4E>(v));
-  v = fmaxf(v, dpp<0x141>(v));
-  v = fmaxf(v, dpp<0x140>(v));
-  return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
 }
 
 // ------------------------------------------------------------------ global loads
@@ -195,6 +222,9 @@ struct Buf {
       : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000)) {}
   __device__ __forceinline__ u32x4 ld4(uint32_t byte_off) const {
     return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, SC1);
+  }
+  __device__ __forceinline__ u32x2 ld2(uint32_t byte_off) const {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, SC1);
   }
   __device__ __forceinline__ uint32_t ld1(uint32_t byte_off) const {
     return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, SC1);

@@ -6,48 +6,47 @@
 // (csrc/megakernel/fused_decode_ldg.cu:617-887).
 //
 // Chip layout: 256 workgroups of 512 threads, one per CU; workgroup w serves the
-// XCD g it runs on (read from the hardware XCC id) as that XCD's member j = w / 8. XCD g owns KV group g: the 512 q/k/v rows of query heads 2g, 2g+1
-// and KV head g, the attention of those heads, the o_proj columns of those
-// heads (a K-split of o_proj across XCDs) and MLP units 384g .. 384g+383 (a
-// K-split of down_proj). Every workgroup runs four roles, one per wave kind:
-//   * stream waves 0-3 hold the workgroup's weight slice of the next stage in
-//     registers: as soon as a stage's dot products are done the registers are
-//     refilled with the following stage (the first LM-head rows after the last
-//     layer), so each weight byte is requested one stage before it is used.
-//     They also copy the next layer's K/V rows into LDS (LDS DMA). Stream
-//     waves only ever issue loads, so the compiler's in-order vmcnt bookkeeping
-//     stays exact across the layer loop.
-//   * poll waves 4-5 gather the XCD-local exchanges (h, q/k/v, attention
-//     output, h1, m), normalise, apply QK-norm and RoPE, and combine attention
-//     chunks.
-//   * reduce wave 6 sums the eight XCDs' o_proj and down_proj partials of the
-//     workgroup's 32 residual rows and applies the residual adds.
-//   * store wave 7 publishes the stream waves' dot products (handed over
-//     through LDS) and the K/V append. For contexts of at most 256 positions, and
-//     for contexts split over at most three workgroups, the store waves of the
-//     workgroups without attention also warm the XCD's L2 with the attention
-//     workgroups' next K/V rows and weight rows, which they would otherwise copy
-//     from HBM on their critical path.
-// Per layer and workgroup (g, j):
-//   q/k/v : rows 16j .. 16j+15 of the group's [q0; q1; k; v]
-//   attn  : workgroups j < nsplit attend over chunk j (<= 256 positions) for the
-//           group's two query heads; QK^T and PV run on MFMA from LDS
-//   o_proj: partial sums of rows 32j .. 32j+31 over the group's 256 columns
-//   MLP   : gate and up rows of units 384g + 12j .. +11, then down_proj
-//           partial sums of rows 32j .. 32j+31 over the XCD's 384 units
-// so a layer has five XCD-local all-gathers and two cross-XCD reductions. The
-// kernel has two instances: SPLIT = false for contexts of at most 256
+// XCD g it runs on (read from the hardware XCC id) as that XCD's member j = w / 8.
+// XCD g owns KV group g: the 512 q/k/v rows of query heads 2g, 2g+1 and KV head g,
+// the attention of those heads, the o_proj columns of those heads (a K-split of
+// o_proj across XCDs) and MLP units 384g .. 384g+383 (a K-split of down_proj).
+//
+// The 32 workgroups of an XCD form two groups of 16 that take turns on the critical
+// path of a layer:
+//   group A (members 0..15): input RMSNorm, q/k/v rows 32a .. 32a+31 of the group's
+//     [q0; q1; k; v], the attention (members a < nsplit each attend over one chunk of
+//     the context), o_proj partial sums of rows 64a .. 64a+63 over the group's 256
+//     columns, and the cross-XCD reduction of those rows into h1;
+//   group B (members 16..31, b = j - 16): post-attention RMSNorm, gate and up rows of
+//     units 384g + 24b .. +23, down_proj partial sums of rows 64b .. 64b+63 over the
+//     XCD's 384 units, and the cross-XCD reduction of those rows into h.
+// While one group works, the other streams its next layer's weights into registers
+// (and the attention workgroups their next K/V rows into LDS): a CU's loads and its
+// exchange polls complete in order, so a group only ever polls with no weight load
+// in flight. Group B holds its burst until group A has published the next layer's
+// q/k/v, which moves it off the hand-overs that precede the attention.
+//
+// Every workgroup runs four roles, one per wave kind:
+//   * stream waves 0-3 hold the group's weight slice in registers and compute the
+//     dot products, handing them to the store wave through LDS;
+//   * poll waves 4-5 gather the XCD-local exchanges (h, q/k/v, attention output,
+//     h1, m), normalise, apply QK-norm and RoPE, and merge attention chunks;
+//   * reduce wave 6 sums the eight XCDs' partials of the workgroup's 64 residual
+//     rows and applies the residual add;
+//   * store wave 7 publishes the dot products and appends the new K/V row.
+// A layer has five XCD-local all-gathers and two cross-XCD reductions and no grid
+// barrier. The kernel has two instances: SPLIT = false for contexts of at most 256
 // positions (one attention workgroup per XCD, no chunk merge compiled in) and
-// SPLIT = true for the rest.
+// SPLIT = true for the rest (up to 16 chunks of up to four 256-position LDS passes).
 //
 // Exchanges use "tagged words": a bf16 value in the low half of a 32-bit word
 // and a 16-bit tag (launch epoch x 32 + layer) in the high half, or an fp32
 // value with a 32-bit tag in a 64-bit word. A consumer issues all its loads at
 // once and re-polls only stale words, so an exchange costs one memory round
-// trip and no grid barrier. Across XCDs both sides use device-scope (sc1)
-// accesses; inside an XCD producers use plain stores and consumers
-// non-temporal loads, served by the XCD's shared L2. A watchdog bounds every
-// poll and turns a lost producer into an error code instead of a hang.
+// trip. Across XCDs both sides use device-scope (sc1) accesses; inside an XCD
+// producers use plain stores and consumers non-temporal loads, served by the
+// XCD's shared L2. A watchdog bounds every poll and turns a lost producer into an
+// error code instead of a hang.
 //
 // Numerics follow HF Qwen3 in bf16 (transformers/models/qwen3/modeling_qwen3.py):
 // every Linear / norm / RoPE op / residual add / SiLU / product result is
@@ -65,7 +64,7 @@
 #include "../../include/megaqwen_amd.h"
 
 // Instrumentation hooks: MQ_STAMP(slot) marks a point of a layer's timeline
-// (slot = layer * 40 + event; stream events 0..9, poll 12..24, reduce 28..32,
+// (slot = layer * 40 + event; stream events 0..11, poll 12..25, reduce 28..32,
 // store 34..38), MQ_STAMP_DUMP() runs once at the end of the kernel. Both compile
 // to nothing unless a tracing build defines them before including this file.
 #ifndef MQ_STAMP
@@ -82,56 +81,64 @@ constexpr int NT = 512;
 constexpr int NSW = 4;  // stream waves 0..3
 constexpr int NPW = 2;  // poll waves 4..5; wave 6 reduces the cross-XCD partial sums, wave 7 stores
 constexpr int NXCD = 8;
-constexpr int WG_PER_XCD = NWG / NXCD;        // 32
-constexpr int ROWS = H / WG_PER_XCD;          // residual-stream rows owned per workgroup: 32
-constexpr int UNITS = I / NWG;                // MLP units per workgroup: 12
-constexpr int XUNITS = I / NXCD;              // MLP units per XCD: 384
-constexpr int KV_CAP = 256;                       // positions per LDS pass of an attention workgroup
-constexpr int MAX_CTX = 2 * WG_PER_XCD * KV_CAP;  // 16384: at most two passes per workgroup
-constexpr int SPLIT_WARM_MAX = 3;  // split contexts whose next-layer rows are warmed in L2
-constexpr int LM_PRE = 4;                     // LM-head rows each stream wave loads during the last layer
+constexpr int WG_PER_XCD = NWG / NXCD;  // 32
+constexpr int NGA = 16;                  // group-A workgroups per XCD
+constexpr int NGB = WG_PER_XCD - NGA;    // group-B workgroups per XCD
+constexpr int ROWS = H / NGA;            // residual rows a workgroup reduces: 64 (A: h1, B: h)
+static_assert(H / NGB == ROWS, "both groups reduce the same number of rows");
+constexpr int QROWS = 4 * HD / NGA;      // q/k/v rows per A workgroup: 32
+constexpr int XUNITS = I / NXCD;         // MLP units per XCD: 384
+constexpr int UNITS = XUNITS / NGB;      // MLP units per B workgroup: 24
+constexpr int KV_CAP = 256;              // positions per LDS pass of an attention workgroup
+constexpr int MAX_PASS = 4;              // LDS passes per attention workgroup
+constexpr int MAX_CTX = NGA * MAX_PASS * KV_CAP;  // 16384
 
 // Attention split of a context of n positions (the query at n - 1): nsplit chunks of at
-// most `chunk` positions, chunk j on workgroup (g, j) of every XCD g, each attended in
+// most `chunk` positions, chunk a on A workgroup (g, a) of every XCD g, each attended in
 // passes of at most KV_CAP positions (the LDS copy holds KV_CAP rows).
 __host__ __device__ constexpr int plan_nsplit(int n) {
-  return (n + KV_CAP - 1) / KV_CAP < WG_PER_XCD ? (n + KV_CAP - 1) / KV_CAP : WG_PER_XCD;
+  return (n + KV_CAP - 1) / KV_CAP < NGA ? (n + KV_CAP - 1) / KV_CAP : NGA;
 }
 __host__ __device__ constexpr int plan_chunk(int n) { return (n + plan_nsplit(n) - 1) / plan_nsplit(n); }
-// Every context length the kernel accepts (1 .. MAX_CTX) gives chunks of at most two LDS
-// passes, none of them empty, covering all n positions.
+// Every context length the kernel accepts (1 .. MAX_CTX) gives chunks of at most MAX_PASS
+// LDS passes, none of them empty, covering all n positions.
 constexpr bool plan_is_sound() {
   for (int n = 1; n <= MAX_CTX; n++) {
     const int ns = plan_nsplit(n), ch = plan_chunk(n);
-    if (ns < 1 || ns > WG_PER_XCD || ch > 2 * KV_CAP || ch * ns < n || (ns - 1) * ch >= n) return false;
+    if (ns < 1 || ns > NGA || ch > MAX_PASS * KV_CAP || ch * ns < n || (ns - 1) * ch >= n) return false;
   }
   return true;
 }
-static_assert(plan_is_sound(), "attention chunks must fit two LDS passes and cover the context");
+static_assert(plan_is_sound(), "attention chunks must fit MAX_PASS LDS passes and cover the context");
 
 // Workspace layout, in 32-bit words.
 constexpr uint32_t WS_RESERVED = 0;  // (words 0..31 unused)
 constexpr uint32_t WS_ERR = 32;
 constexpr uint32_t WS_FINAL_TICKET = 64;
 // word WS_PREFILL_ERR (96) belongs to the prefill kernels
-// per-XCD regions of tagged bf16 words, written and read only by that XCD's workgroups
+// per-XCD regions of tagged words, written and read only by that XCD's workgroups
 constexpr uint32_t WS_LOCAL = 1024;
 constexpr uint32_t LOCAL_WORDS = 32768;
-constexpr uint32_t LX_H = 0;        // [1024] residual stream after the layer (a full copy per XCD)
-constexpr uint32_t LX_H1 = 1024;    // [1024] residual stream after attention
+constexpr uint32_t LX_H = 0;        // [1024] residual stream after the layer (from B)
+constexpr uint32_t LX_H1 = 1024;    // [1024] residual stream after attention (from A)
 constexpr uint32_t LX_QKV = 2048;   // [512]  raw q0, q1, k, v rows of the XCD's KV group
 constexpr uint32_t LX_ATT = 2560;   // [256]  attention output of the group's two query heads
 constexpr uint32_t LX_M = 2816;     // [384]  SiLU(gate) * up of the XCD's MLP units
-constexpr uint32_t LX_HSS = 3200;   // [32] (fp32, tag) pairs: sum of squares of workgroup j's rows of h
-constexpr uint32_t LX_H1SS = 3264;  // [32] the same for h1
+// cue words (a 16-bit tag each): group A member 0 writes LX_CUE_A after its o_proj
+// partials, group B member 0 writes LX_CUE_B after its down_proj partials. The other group
+// watches the cue (one word) before it polls the residual stream (2 KB a wave), which
+// keeps the long waits off the XCD's L2; the gathered data carry their own tags.
+constexpr uint32_t LX_CUE_A = 3200;
+constexpr uint32_t LX_CUE_B = 3232;
 constexpr uint32_t APART = 130;     // attention partial of one head: m, l, acc[128]
-constexpr uint32_t LX_PART = 4096;  // [32 chunks][2 heads][APART] (fp32, tag) pairs
-// cross-XCD partial sums: [j][row][xcd] (fp32, tag) pairs
+constexpr uint32_t LX_PART = 4096;  // [16 chunks][2 heads][APART] (fp32, tag) pairs
+// cross-XCD partial sums: [member][xcd][row] (fp32, tag) pairs
 constexpr uint32_t X_OPART = WS_LOCAL + NXCD * LOCAL_WORDS;
-constexpr uint32_t X_DPART = X_OPART + 2 * WG_PER_XCD * ROWS * NXCD;
-constexpr uint32_t WS_LMPART = X_DPART + 2 * WG_PER_XCD * ROWS * NXCD;  // [NWG][2]: best logit, index
+constexpr uint32_t X_DPART = X_OPART + 2 * NGA * ROWS * NXCD;
+constexpr uint32_t WS_LMPART = X_DPART + 2 * NGB * ROWS * NXCD;  // [NWG][2]: best logit, index
 constexpr uint32_t WS_WORDS = WS_LMPART + NWG * 2;
 constexpr size_t WS_BYTES = ((WS_WORDS * 4 + 4 + 65535) / 65536) * 65536;
+static_assert(LX_PART + 2 * NGA * 2 * APART <= LOCAL_WORDS, "per-XCD region overflow");
 
 constexpr uint32_t POLL_LIMIT = 1u << 21;  // ~1 s of polling before the watchdog fires
 constexpr uint32_t ERR_POLL = 1u;
@@ -139,6 +146,7 @@ constexpr uint32_t ERR_XCD = 2u;  // a workgroup ran on an XCD numbered 8 or abo
 constexpr uint32_t ERR_STEP = 4u;  // a device-resident step found an invalid token, position or count
 
 constexpr int NT_LD = 2;  // non-temporal cache policy: bypasses the CU's L1, served by the XCD's L2
+
 
 enum : int { MODE_INPUT_HIDDEN = 1, MODE_NO_LMHEAD = 2, MODE_LOGITS = 4, MODE_DEVICE_STEP = 8 };
 enum { W_IN = 0, W_Q, W_K, W_V, W_QN, W_KN, W_O, W_POST, W_G, W_U, W_D };
@@ -203,32 +211,7 @@ __device__ __forceinline__ bool watchdog(const Buf& wsb, uint32_t* ws, uint32_t 
   return false;
 }
 
-// ---- cross-XCD exchange: device-scope (sc1) loads and stores
-__device__ __forceinline__ u32x4 xld4(const Buf& b, uint32_t word) { return b.ld4(word * 4u); }
-__device__ __forceinline__ void xst4(const Buf& b, uint32_t word, u32x4 v) { b.st4(v, word * 4u); }
-__device__ __forceinline__ void xst1(const Buf& b, uint32_t word, uint32_t v) { b.st1(v, word * 4u); }
-__device__ __forceinline__ u32x4 xrepoll4(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, u32x4 v) {
-  uint32_t spins = 0;
-  while (!tags_ok(v, tag)) {
-    if (watchdog(b, ws, ++spins)) break;
-    __builtin_amdgcn_s_sleep(1);
-    v = xld4(b, word);
-  }
-  return v;
-}
-
-// two (fp32, tag) pairs in one 16-byte load
-__device__ __forceinline__ u32x4 xrepoll64x2(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, u32x4 v) {
-  uint32_t spins = 0;
-  while ((v.y != tag) | (v.w != tag)) {
-    if (watchdog(b, ws, ++spins)) break;
-    __builtin_amdgcn_s_sleep(1);
-    v = xld4(b, word);
-  }
-  return v;
-}
-
-// ---- XCD-local exchange: plain stores, non-temporal loads (L2)
+// ---- XCD-local exchange: plain stores, non-temporal loads (served by the XCD's L2)
 __device__ __forceinline__ u32x4 ldl4(const Buf& b, uint32_t word) {
   return __builtin_amdgcn_raw_buffer_load_b128(b.r, word * 4u, 0, NT_LD);
 }
@@ -243,137 +226,6 @@ __device__ __forceinline__ u32x4 repoll_l4(const Buf& b, uint32_t* ws, uint32_t 
 }
 __device__ __forceinline__ uint32_t ldl1(const Buf& b, uint32_t word) {
   return __builtin_amdgcn_raw_buffer_load_b32(b.r, word * 4u, 0, NT_LD);
-}
-__device__ __forceinline__ u32x2 ldl64(const Buf& b, uint32_t word) {
-  return __builtin_amdgcn_raw_buffer_load_b64(b.r, word * 4u, 0, NT_LD);
-}
-__device__ __forceinline__ void stl4(const Buf& b, uint32_t word, u32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(v, b.r, word * 4u, 0, 0);
-}
-__device__ __forceinline__ void stl64(const Buf& b, uint32_t word, float v, uint32_t tag) {
-  u32x2 x;
-  x.x = __float_as_uint(v);
-  x.y = tag;
-  __builtin_amdgcn_raw_buffer_store_b64(x, b.r, word * 4u, 0, 0);
-}
-__device__ __forceinline__ uint32_t repoll_l1(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, uint32_t v) {
-  uint32_t spins = 0;
-  while ((v >> 16) != tag) {
-    if (watchdog(b, ws, ++spins)) break;
-    __builtin_amdgcn_s_sleep(1);
-    v = ldl1(b, word);
-  }
-  return v;
-}
-__device__ __forceinline__ float repoll_l64(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag, u32x2 v) {
-  uint32_t spins = 0;
-  while (v.y != tag) {
-    if (watchdog(b, ws, ++spins)) break;
-    __builtin_amdgcn_s_sleep(1);
-    v = ldl64(b, word);
-  }
-  return __uint_as_float(v.x);
-}
-
-// L2 warm-up of the K/V rows [0, p) of (layer, group g) for the XCD's attention
-// workgroup: one 4-byte LDS DMA per 64-byte line, so one instruction touches 64
-// lines. Instruction t of the ceil(p / 8) needed (K lines, then V lines) goes to
-// worker t % nworkers; a worker is the store wave of one of the XCD's other
-// workgroups, whose LDS K/V area is otherwise unused and takes the dead data.
-// The issuing wave awaits the copies before that area is reused.
-__device__ __forceinline__ void kv_warm(const DecodeParams& P, int layer, int g, int p, uint32_t lds, int wk,
-                                        int nworkers, int lane) {
-  const size_t base = (size_t)(layer * NKV + g) * P.max_seq_len * HD;
-  const uint8_t* kb = reinterpret_cast<const uint8_t*>(P.k_cache + base);
-  const uint8_t* vb = reinterpret_cast<const uint8_t*>(P.v_cache + base);
-  const int nlk = 4 * p;  // 64-byte lines of K rows 0 .. p-1
-  const int ninst = (2 * nlk + 63) >> 6;
-  for (int t = wk; t < ninst; t += nworkers) {
-    const int li = 64 * t + lane;
-    if (li < 2 * nlk) {
-      const uint8_t* gp = li < nlk ? kb + 64 * (size_t)li : vb + 64 * (size_t)(li - nlk);
-      uint32_t saved;
-      asm volatile(
-          "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-          : "=&s"(saved)
-          : "v"(gp), "s"(lds)
-          : "memory");
-    }
-  }
-}
-
-// L2 warm-up of the weight rows that XCD g's attention workgroup (j = 0) loads during
-// this layer after its attention (gate and up rows 384g .. 384g+11; down_proj rows 0..31,
-// columns 384g .. 384g+383) and at the end of it for the next layer (q rows 256g ..
-// 256g+15; o_proj rows 0..31, columns 256g .. 256g+255): 960 128-byte lines, one 4-byte
-// LDS DMA each, line t on worker t % nworkers (the same workers as kv_warm).
-// `wl` is the layer's and `wn` the next layer's weight-pointer row.
-__device__ __forceinline__ void att_weight_warm(const uint16_t* const* wl, const uint16_t* const* wn, int g,
-                                                uint32_t lds, int wk, int nworkers, int lane) {
-  constexpr int NQL = 16 * 16, NOL = 32 * 4, NGL = 12 * 16, NDL = 32 * 6;  // lines per part
-  constexpr int NL = NQL + NOL + 2 * NGL + NDL;
-  for (int t = 64 * wk + lane; t < NL; t += 64 * nworkers) {
-    const uint8_t* a;
-    if (t < NQL) {
-      a = reinterpret_cast<const uint8_t*>(uniform_ptr(wn[W_Q]) + (size_t)256 * g * H) + 128 * t;
-    } else if (t < NQL + NOL) {
-      const int u = t - NQL;
-      a = reinterpret_cast<const uint8_t*>(uniform_ptr(wn[W_O]) + (size_t)(u >> 2) * QS + 256 * g) + 128 * (u & 3);
-    } else if (t < NQL + NOL + 2 * NGL) {
-      const int u = t - NQL - NOL;
-      const uint16_t* w = uniform_ptr(wl[u < NGL ? W_G : W_U]);
-      a = reinterpret_cast<const uint8_t*>(w + (size_t)XUNITS * g * H) + 128 * (u < NGL ? u : u - NGL);
-    } else {
-      const int u = t - NQL - NOL - 2 * NGL, row = u / 6;
-      a = reinterpret_cast<const uint8_t*>(uniform_ptr(wl[W_D]) + (size_t)row * I + XUNITS * g) + 128 * (u - 6 * row);
-    }
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "v"(a), "s"(lds)
-                 : "memory");
-  }
-}
-
-// The same for the attention workgroups j < na of a split context: the weight rows that
-// they load during this layer after their attention (gate and up rows 384g + 12j .. +11; down_proj rows
-// 32j .. 32j+31, columns 384g .. 384g+383) and at the end of it for the next layer (the
-// q/k/v rows 16j .. 16j+15 of the group's [q0; q1; k; v]; o_proj rows 32j .. 32j+31,
-// columns 256g .. 256g+255): 960 128-byte lines per workgroup, one 4-byte LDS DMA each,
-// line t on worker t % nworkers (the same workers as kv_warm).
-// `wl` is the layer's and `wn` the next layer's weight-pointer row.
-__device__ __forceinline__ void att_weight_warm_n(const uint16_t* const* wl, const uint16_t* const* wn, int g, int na,
-                                                uint32_t lds, int wk, int nworkers, int lane) {
-  constexpr int NQL = 16 * 16, NOL = 32 * 4, NGL = 12 * 16, NDL = 32 * 6;  // lines per part
-  constexpr int NL = NQL + NOL + 2 * NGL + NDL;
-  for (int t = 64 * wk + lane; t < na * NL; t += 64 * nworkers) {
-    const int ja = t / NL, v = t - NL * ja;
-    const uint8_t* a;
-    if (v < NQL) {
-      const int r = 16 * ja;
-      const uint16_t* w = r < 256   ? uniform_ptr(wn[W_Q]) + (size_t)(256 * g + r) * H
-                          : r < 384 ? uniform_ptr(wn[W_K]) + (size_t)(128 * g + r - 256) * H
-                                    : uniform_ptr(wn[W_V]) + (size_t)(128 * g + r - 384) * H;
-      a = reinterpret_cast<const uint8_t*>(w) + 128 * v;
-    } else if (v < NQL + NOL) {
-      const int u = v - NQL;
-      a = reinterpret_cast<const uint8_t*>(uniform_ptr(wn[W_O]) + (size_t)(ROWS * ja + (u >> 2)) * QS + 256 * g) +
-          128 * (u & 3);
-    } else if (v < NQL + NOL + 2 * NGL) {
-      const int u = v - NQL - NOL;
-      const uint16_t* w = uniform_ptr(wl[u < NGL ? W_G : W_U]);
-      a = reinterpret_cast<const uint8_t*>(w + (size_t)(XUNITS * g + UNITS * ja) * H) + 128 * (u < NGL ? u : u - NGL);
-    } else {
-      const int u = v - NQL - NOL - 2 * NGL, row = u / 6;
-      a = reinterpret_cast<const uint8_t*>(uniform_ptr(wl[W_D]) + (size_t)(ROWS * ja + row) * I + XUNITS * g) +
-          128 * (u - 6 * row);
-    }
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "v"(a), "s"(lds)
-                 : "memory");
-  }
 }
 
 // K/V rows of a chunk live in LDS as [row][16 chunks of 8 dims], chunk c of row r
@@ -399,29 +251,17 @@ __device__ __forceinline__ void kv_dma(const DecodeParams& P, int layer, int g, 
   }
 }
 
-// ---- stream-wave stores: inline assembly, so that the compiler's vmcnt
-// bookkeeping for the stream waves' register loads ignores them (each makes a
-// later wait at most one instruction longer). The exchange waves never store
-// inside the layer loop, so their polls never queue behind a store's write
-// acknowledgement. `dev` stores (sc1) write through to memory for readers on
-// other XCDs; plain stores stay in this XCD's L2.
-__device__ __forceinline__ void st1_dev(uint32_t* p, uint32_t v) {
-  asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
-}
+// ---- exchange stores: inline assembly, so that the compiler's vmcnt bookkeeping for
+// the stream waves' register loads ignores them (each makes a later wait at most one
+// instruction longer). Only the store and reduce waves store inside the layer loop, and
+// each of them stores after its last poll of the stage, so no poll queues behind a
+// store's write acknowledgement. `dev` stores (sc1) write through to memory for readers
+// on other XCDs; plain stores stay in this XCD's L2.
 __device__ __forceinline__ void st2_dev(uint32_t* p, u32x2 v) {
   asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
-__device__ __forceinline__ void st3_dev(uint32_t* p, u32x3 v) {
-  asm volatile("global_store_dwordx3 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ void st4_dev(uint32_t* p, u32x4 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
-}
 __device__ __forceinline__ void st1_plain(uint32_t* p, uint32_t v) {
   asm volatile("global_store_dword %0, %1, off" ::"v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ void st2_plain(uint32_t* p, u32x2 v) {
-  asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
 }
 __device__ __forceinline__ void st4_plain(uint32_t* p, u32x4 v) {
   asm volatile("global_store_dwordx4 %0, %1, off" ::"v"(p), "v"(v) : "memory");
@@ -567,27 +407,18 @@ __device__ __forceinline__ void attn_pv(const uint8_t* s_kv, const uint16_t* s_p
   }
 }
 
-// LM-head row r: bf16 logit of x (two 16-byte chunks per lane) against the row's
-// chunks w0, w1; tracks this wave's best (first index on ties) and records the logit.
-__device__ __forceinline__ void lm_score(int r, int r0, const u32x4& w0, const u32x4& w1, const u32x4& x0,
-                                         const u32x4& x1, float* s_lg, int lane, float& bestv, int& besti) {
-  const float v = rbf(wave_sum(dot_chunk(w0, x0, dot_chunk(w1, x1, 0.f))));
-  if (lane == 0) s_lg[r - r0] = v;
-  if (v > bestv) {
-    bestv = v;
-    besti = r;
-  }
-}
-
-// Stream-wave weight registers: one stage's slice each.
-struct StreamRegs {
-  u32x4 a[8];    // q/k/v: 4 rows x 2 chunks
-  u32x4 o[4];    // o_proj partials: 4 rows x 1 chunk
-  u32x4 gu[12];  // gate rows of 3 units, then their up rows: 6 rows x 2 chunks
-  u32x4 d[8];    // down_proj partials: 8 rows x 1 chunk
+// Stream-wave weight registers: group A holds a layer's q/k/v rows and o_proj partial rows,
+// group B its gate/up rows and down_proj partial rows.
+struct ARegs {
+  u32x4 a[16];   // q/k/v: 8 rows x 2 chunks
+  u32x4 o[8];    // o_proj partials: 16 rows as 8 pairs of rows, one chunk per lane
   u32x2 wln;     // input_layernorm elements 4t .. 4t+3
-  u32x2 wpost;   // post_attention_layernorm elements 4t .. 4t+3
   uint32_t qkn;  // q_norm (t < 64) / k_norm (t >= 64) elements 2t, 2t+1 (mod 128)
+};
+struct BRegs {
+  u32x4 gu[24];  // gate rows of 6 units, then their up rows: 12 rows x 2 chunks
+  u32x4 d[16];   // down_proj partials: 16 rows, one chunk per lane (lanes < 48)
+  u32x2 wpost;   // post_attention_layernorm elements 4t .. 4t+3
 };
 
 // Exchange waves: one 16-byte chunk (4 tagged words) as fp32 values.
@@ -598,36 +429,45 @@ __device__ __forceinline__ void unpack_tagged(const u32x4& v, float* f) {
   f[3] = bflo(v.w);
 }
 
-// This poll wave's half of a gathered residual stream (chunks lane + 128c into v0 and
-// lane + 128c + 64 into v1) and the stream's sum of squares, added up from the 32 per-workgroup
-// sums of squares published with it (the same order in both poll waves, so their norms
-// agree bit for bit).
-__device__ __forceinline__ float gather_half(const Buf& b, uint32_t* ws, uint32_t base, uint32_t ssbase, uint32_t tag,
-                                             uint32_t tag64, int c, int lane, u32x4& v0, u32x4& v1) {
-  const uint32_t w0 = base + 4 * (lane + 128 * c), w1 = w0 + 4 * 64;
-  const uint32_t wq = ssbase + 4 * (lane & 15);  // the sums of workgroups 2 (lane % 16) and +1
-  // poll only the 32 sums of squares (each producer stores its sum after its rows): a
-  // third of the polling traffic of polling rows and sums together, which measured 6 us
-  // faster per token; then load the rows once and re-poll any that are still stale
-  u32x4 q = ldl4(b, wq);
-  auto fresh = [&](const u32x4& x) { return (x.y == tag64) & (x.w == tag64); };
-  uint32_t spins = 0;
-  while (!fresh(q)) {
+// Wait until the cue word carries `tag` (all lanes load the same word: one request).
+__device__ __forceinline__ void wait_cue(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag) {
+  uint32_t v = ldl1(b, word), spins = 0;
+  while (v != tag) {
     if (watchdog(b, ws, ++spins)) break;
-    __builtin_amdgcn_s_sleep(1);
-    q = ldl4(b, wq);
+    __builtin_amdgcn_s_sleep(2);
+    v = ldl1(b, word);
   }
+}
+
+// This poll wave's half of a gathered residual stream (chunks lane + 128c into v0 and
+// lane + 128c + 64 into v1) and the stream's sum of squares: each poll wave adds up the
+// squares of its half, and the two halves' sums meet in LDS and are added in a fixed
+// order (half 0 first), so both waves' norms agree bit for bit. `target` is the number
+// of half sums the LDS counter holds once this exchange is complete.
+__device__ __forceinline__ float gather_half(const Buf& b, uint32_t* ws, uint32_t base, uint32_t tag, int c, int lane,
+                                             u32x4& v0, u32x4& v1, float* s_ssx, uint32_t* s_ssn, uint32_t target) {
+  const uint32_t w0 = base + 4 * (lane + 128 * c), w1 = w0 + 4 * 64;
   u32x4 a = ldl4(b, w0), e = ldl4(b, w1);
-  while (!(tags_ok(a, tag) & tags_ok(e, tag) & fresh(q))) {
+  uint32_t spins = 0;
+  while (!(tags_ok(a, tag) & tags_ok(e, tag))) {
     if (watchdog(b, ws, ++spins)) break;
     __builtin_amdgcn_s_sleep(1);
     if (!tags_ok(a, tag)) a = ldl4(b, w0);
     if (!tags_ok(e, tag)) e = ldl4(b, w1);
-    if (!fresh(q)) q = ldl4(b, wq);
   }
   v0 = a;
   v1 = e;
-  return wave_sum(lane < 16 ? __uint_as_float(q.x) + __uint_as_float(q.z) : 0.f);
+  float fa[4], fe[4];
+  unpack_tagged(a, fa);
+  unpack_tagged(e, fe);
+  const float part = wave_sum(((fa[0] * fa[0] + fa[1] * fa[1]) + (fa[2] * fa[2] + fa[3] * fa[3])) +
+                              ((fe[0] * fe[0] + fe[1] * fe[1]) + (fe[2] * fe[2] + fe[3] * fe[3])));
+  if (lane == 0) {
+    s_ssx[c] = part;
+    signal_store(s_ssn);
+  }
+  wait_count(s_ssn, target);
+  return s_ssx[0] + s_ssx[1];
 }
 
 // HF Qwen3RMSNorm (modeling_qwen3.py:59-64) of one chunk: y = bf16(w * bf16(x * rstd)),
@@ -637,17 +477,40 @@ __device__ __forceinline__ void norm_chunk(const float* x, float rstd, uint32_t 
   dst[1] = pack_bf2(rbf(bflo(w1) * rbf(x[2] * rstd)), rbf(bfhi(w1) * rbf(x[3] * rstd)));
 }
 
+// Sum of the eight XCDs' (fp32, tag) partials of one row, in XCD order, from the
+// cross-XCD array at `part` (pairs [member][xcd][row], so that each producer writes, and
+// each of the consumer's loads reads, one contiguous 512-byte run): lane = row.
+__device__ __forceinline__ float reduce_row8(const Buf& wsb, uint32_t* ws, uint32_t wd, uint32_t tag64) {
+  auto ok = [&](const u32x2& v) { return v.y == tag64; };
+  uint32_t spins = 0;
+  u32x2 q[NXCD];
+#pragma unroll
+  for (int x = 0; x < NXCD; x++) q[x] = wsb.ld2((wd + 2 * ROWS * x) * 4u);
+  // re-poll the stale XCDs' pairs together (one round trip per iteration)
+  for (;;) {
+    bool all = true;
+#pragma unroll
+    for (int x = 0; x < NXCD; x++) all &= ok(q[x]);
+    if (all || watchdog(wsb, ws, ++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int x = 0; x < NXCD; x++)
+      if (!ok(q[x])) q[x] = wsb.ld2((wd + 2 * ROWS * x) * 4u);
+  }
+  auto f = [&](int x) { return __uint_as_float(q[x].x); };
+  return ((f(0) + f(1)) + (f(2) + f(3))) + ((f(4) + f(5)) + (f(6) + f(7)));
+}
+
 // ---------------------------------------------------------------- the kernel
 // SPLIT = false is the instance for contexts of at most KV_CAP positions (one
-// attention workgroup per XCD, one LDS pass): the chunk-merge and two-pass code
+// attention workgroup per XCD, one LDS pass): the chunk-merge and multi-pass code
 // is compiled out of it. SPLIT = true handles every context length.
 template <bool SPLIT>
 __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ __align__(16) uint8_t s_kv[2 * KV_CAP * HD * 2];  // K rows, then V rows of the chunk
-  __shared__ __align__(16) uint32_t s_x0[H / 2];               // normed h or h1 (bf16 pairs)
-  __shared__ __align__(16) uint32_t s_x1[XUNITS / 2];          // attention output or m of the XCD (bf16 pairs)
-  __shared__ __align__(16) uint32_t s_wln[H / 2];              // input_layernorm weights
-  __shared__ __align__(16) uint32_t s_wpost[H / 2];            // post_attention_layernorm weights
+  __shared__ __align__(16) uint32_t s_x0[H / 2];               // normed h (A) or h1 (B) (bf16 pairs)
+  __shared__ __align__(16) uint32_t s_x1[XUNITS / 2];          // attention output (A) or m (B) of the XCD
+  __shared__ __align__(16) uint32_t s_wn[H / 2];               // A: input_layernorm, B: post_attention_layernorm
   __shared__ __align__(16) uint32_t s_wfn[H / 2];              // final norm weights
   __shared__ uint32_t s_qkn[HD];                               // q_norm words, then k_norm words
   __shared__ float s_cos[HD], s_sin[HD];
@@ -655,12 +518,15 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ __align__(16) uint16_t s_p[2 * KV_CAP];  // bf16 softmax numerators
   __shared__ float s_sc[2][KV_CAP];                    // attention scores
   __shared__ float s_ao[2][HD];                        // attention output (or unnormalised partial)
-  __shared__ float s_ao1[2][HD];                       // second LDS pass's unnormalised partial
+  __shared__ float s_ao1[2][HD];                       // a later LDS pass's unnormalised partial
   __shared__ float s_mx[8][2], s_l[8][2];              // per-wave score maxima and softmax sums
-  __shared__ float s_hrow[ROWS];                       // residual rows 32j .. 32j+31 of h
+  __shared__ float s_hrow[ROWS];                       // the residual rows this workgroup reduces
   __shared__ float s_res[ROWS];                        // stream-wave dot products for the store wave
   __shared__ uint32_t s_cnt;                           // stream-wave results published so far
-  __shared__ uint32_t s_attst;                         // attention-output stores issued by the store wave
+  __shared__ uint32_t s_red;                           // reductions stored by the reduce wave
+  __shared__ uint32_t s_nrm;                           // norm-weight sets written by the stream waves
+  __shared__ float s_ssx[2];                           // the poll waves' half sums of squares
+  __shared__ uint32_t s_ssn;                           // half sums written so far
   __shared__ const uint16_t* s_lw[MAX_LAYERS][11];    // weight pointers, copied once per launch
   __shared__ float s_bestv[8];
   __shared__ int s_besti[8];
@@ -679,6 +545,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   uint32_t xcc;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
   const int w = blockIdx.x, g = (int)(xcc & (NXCD - 1)), j = w / NXCD;
+  const bool ga = j < NGA;                 // group A (else B)
+  const int m = ga ? j : j - NGA;          // member index within the group
   uint32_t* ws = P.ws;
   const Buf wsb(ws);
   // token, position, epoch: kernel arguments, or a device-resident step written by the
@@ -708,19 +576,20 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   const int L = P.num_layers;
   const bool lm = !(P.mode & MODE_NO_LMHEAD);
 
-  // attention chunking: nsplit chunks of <= 2 KV_CAP positions, chunk j on workgroup (g, j),
-  // attended in npass LDS passes of <= KV_CAP positions (rows KV_CAP.. in the second)
+  // attention chunking: nsplit chunks, chunk a on A workgroup (g, a), attended in npass LDS
+  // passes of <= KV_CAP positions
   const int n_ctx = p + 1;
   const int nsplit = SPLIT ? plan_nsplit(n_ctx) : 1;
   const int CH = SPLIT ? plan_chunk(n_ctx) : n_ctx;
-  const bool att = j < nsplit;
-  const int c0 = j * CH;
+  const bool att = ga && m < nsplit;
+  const int c0 = m * CH;
   const int nc = att ? min(n_ctx, c0 + CH) - c0 : 0;
   const int npass = SPLIT ? (nc + KV_CAP - 1) / KV_CAP : 1;
   const int nc0 = min(nc, KV_CAP);
   const bool own_p = att && p >= c0 && p < c0 + nc;  // p is always in the last pass
   const int prow = p - c0 - KV_CAP * (npass - 1);     // its LDS row there
   const uint32_t lds_kv = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)s_kv;
+  auto pass_rows = [&](int ps) { return ps == npass - 1 ? nc - KV_CAP * ps : KV_CAP; };
 
   // LM-head rows of this workgroup: 594 for w < 128, 593 after (151936 in total)
   const int r0 = w < 128 ? w * 594 : 128 * 594 + (w - 128) * 593;
@@ -740,224 +609,220 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     for (int i = st; i < L * 11; i += NSW * 64)
       s_lw[i / 11][i % 11] = reinterpret_cast<const uint16_t* const*>(P.layers)[i];
     BAR();  // P00: pointer table visible
-    // Weight pointer k of layer l; l >= L (the next-layer loads of the last layer)
-    // maps to layer 0.
-    auto wp = [&](int l, int k) -> const uint16_t* { return uniform_ptr(s_lw[l < L ? l : 0][k]); };
-    // During the last layer the registers are refilled with this wave's first LM-head rows.
-    const uint16_t* lmb = P.lm_head + (size_t)(r0 + LM_PRE * s) * H;
-    const bool lmnext = lm;
-    // o_proj: this lane's 16-byte chunk c of the group's 256 columns, rows 8s + rg + 2i
-    const int oc = lane & 31, org = lane >> 5;
-    // down_proj: lanes < 48 take chunk `lane` of the XCD's 384 columns (the others re-read chunk 47
-    // and are multiplied by zero)
-    const int dch = lane < 48 ? lane : 47;
-
-    StreamRegs R;
-    auto load_a = [&](int l) {
-      const int r = 16 * j + 4 * s;  // this wave's 4 rows of the group's [q0; q1; k; v]
-      const uint16_t* pa = (l >= L && lmnext) ? lmb
-                           : r < 256          ? wp(l, W_Q) + (size_t)(256 * g + r) * H
-                           : r < 384          ? wp(l, W_K) + (size_t)(128 * g + r - 256) * H
-                                              : wp(l, W_V) + (size_t)(128 * g + r - 384) * H;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        R.a[2 * k] = ldw(pa + k * H + 8 * lane);
-        R.a[2 * k + 1] = ldw(pa + k * H + 512 + 8 * lane);
-      }
-    };
-    auto load_o = [&](int l) {
-      const bool lmr = l >= L && lmnext;
-      // LM rows 4, 5 of this wave as chunks lane, lane + 64 of two consecutive rows
-      const uint16_t* po = lmr ? lmb + 4 * H : wp(l, W_O) + (size_t)(ROWS * j + 8 * s + org) * QS + 256 * g + 8 * oc;
-#pragma unroll
-      for (int i = 0; i < 4; i++) R.o[i] = ldw(po + (lmr ? 8 * (lane + 64 * i) : (size_t)(2 * i) * QS));
-    };
-    auto load_gu = [&](int l) {
-      R.wln = ldw2(wp(l + 1, W_IN) + 4 * st);  // the next layer's input norm and q/k norms
-      R.qkn = ldw1(wp(l + 1, st < 64 ? W_QN : W_KN) + 2 * (st & 63));
-      const bool lmr = l >= L && lmnext;
-      const uint16_t* pg = lmr ? lmb + 6 * H : wp(l, W_G) + (size_t)(XUNITS * g + UNITS * j + 3 * s) * H;
-      const uint16_t* pu = lmr ? lmb + 9 * H : wp(l, W_U) + (size_t)(XUNITS * g + UNITS * j + 3 * s) * H;
-#pragma unroll
-      for (int k = 0; k < 3; k++) {
-        R.gu[2 * k] = ldw(pg + k * H + 8 * lane);
-        R.gu[2 * k + 1] = ldw(pg + k * H + 512 + 8 * lane);
-      }
-#pragma unroll
-      for (int k = 0; k < 3; k++) {
-        R.gu[6 + 2 * k] = ldw(pu + k * H + 8 * lane);
-        R.gu[7 + 2 * k] = ldw(pu + k * H + 512 + 8 * lane);
-      }
-    };
-    auto load_d = [&](int l) {
-      R.wpost = ldw2(wp(l + 1, W_POST) + 4 * st);  // the next layer's post-attention norm
-      const bool lmr = l >= L && lmnext;
-      // LM rows 12 .. 15 of this wave as chunks lane, lane + 64 of four consecutive rows
-      const uint16_t* pd = lmr ? lmb + 12 * H : wp(l, W_D) + (size_t)(ROWS * j + 8 * s) * I + XUNITS * g + 8 * dch;
-#pragma unroll
-      for (int i = 0; i < 8; i++) R.d[i] = ldw(pd + (lmr ? 8 * (lane + 64 * i) : (size_t)i * I));
-    };
-
-    auto burst = [&](int l) {
-      load_o(l);
-      load_gu(l);
-      load_d(l);
-      load_a(l + 1);
-    };
-
-    // ---- prologue: layer-0 norms to LDS, layer-0 K/V copy, layer-0 weights in flight
-    {
-      const u32x2 ln0 = ldw2(wp(0, W_IN) + 4 * st);
-      const uint32_t qk0 = ldw1(wp(0, st < 64 ? W_QN : W_KN) + 2 * (st & 63));
-      const u32x2 pn0 = ldw2(wp(0, W_POST) + 4 * st);
-      s_wln[2 * st] = ln0.x;
-      s_wln[2 * st + 1] = ln0.y;
-      s_wpost[2 * st] = pn0.x;
-      s_wpost[2 * st + 1] = pn0.y;
-      if (st < 128) s_qkn[st] = qk0;
-      if (lm) {
-        const u32x2 fn = ldw2(P.final_norm + 4 * st);
-        s_wfn[2 * st] = fn.x;
-        s_wfn[2 * st + 1] = fn.y;
-      }
+    auto wp = [&](int l, int k) -> const uint16_t* { return uniform_ptr(s_lw[l][k]); };
+    if (lm) {
+      const u32x2 fn = ldw2(P.final_norm + 4 * st);
+      s_wfn[2 * st] = fn.x;
+      s_wfn[2 * st + 1] = fn.y;
     }
-    if (att) kv_dma(P, 0, g, c0, nc0, p, lds_kv, s, lane);
-    load_a(0);
-    if (att) load_o(0);
-    BAR();  // P0
-
-    for (int layer = 0; layer < L; layer++) {
-      const int nl = layer + 1;
-      // ---------------- q/k/v rows 16j + 4s .. +3 of the group's [q0; q1; k; v]
-      BAR();  // A1: normed h in s_x0
-      MQ_STAMP(layer * 40 + 0);
-      {
-        if (layer > 0) {
-          s_wpost[2 * st] = R.wpost.x;  // this layer's post-attention norm
-          s_wpost[2 * st + 1] = R.wpost.y;
-        }
-        const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
-        float r[4];
+    // the norm weights of layer l into LDS for the poll waves, then counted (the poll waves
+    // read them only after the count shows the set complete)
+    auto publish_norms = [&]() {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (lane == 0) signal_store(&s_nrm);
+    };
+    if (ga) {
+      // ================================================================ group A
+      ARegs R;
+      const int oc = lane & 31, org = lane >> 5;  // o_proj: chunk oc of the group's 256 columns, row pair half
+      auto load_a = [&](int l) {
+        const int r = QROWS * m + 8 * s;  // this wave's 8 rows of the group's [q0; q1; k; v]
+        const uint16_t* pa = r < 256   ? wp(l, W_Q) + (size_t)(256 * g + r) * H
+                             : r < 384 ? wp(l, W_K) + (size_t)(128 * g + r - 256) * H
+                                       : wp(l, W_V) + (size_t)(128 * g + r - 384) * H;
 #pragma unroll
-        for (int k = 0; k < 4; k++) r[k] = dot_chunk(R.a[2 * k], x0, dot_chunk(R.a[2 * k + 1], x1, 0.f));
-        wave_sum_n(r);
-        if (lane == 0) {
-#pragma unroll
-          for (int k = 0; k < 4; k++) s_res[4 * s + k] = r[k];
-          signal_store(&s_cnt);
+        for (int k = 0; k < 8; k++) {
+          R.a[2 * k] = ldw(pa + k * H + 8 * lane);
+          R.a[2 * k + 1] = ldw(pa + k * H + 512 + 8 * lane);
         }
-        AFTER(r[0] + r[1] + r[2] + r[3]);
-        MQ_STAMP(layer * 40 + 1);
-        // Workgroups without attention load the rest of the layer's weights and the next
-        // layer's q/k/v in one burst: it drains while attention runs elsewhere, so the
-        // exchanges after attention find this CU's vector-memory pipeline idle (a poll queued
-        // behind in-flight HBM loads waits for them). Attention workgroups poll q/k/v right
-        // after this stage: they load o_proj at the end of the previous layer and the rest
-        // once attention is done.
-        if (!att) burst(layer);
-      }
-      if (att) {
-        // this wave's K/V copy of the layer has landed: all of the wave's vector-memory
-        // operations are awaited (the copy is inline assembly the compiler does not count;
-        // the o_proj loads issued after it are needed right after the attention anyway)
-        wait_vmem();
-        for (int ps = 0; ps < npass; ps++) {
-          if (ps == 1) {
-            // second pass: rows KV_CAP .. nc-1 of the chunk replace the first pass's rows
-            kv_dma(P, layer, g, c0 + KV_CAP, nc - KV_CAP, p, lds_kv, s, lane);
-            wait_vmem();
-          }
-          const int ncp = ps ? nc - KV_CAP : nc0;
-          BAR();  // B1: q, the new k/v row and the K/V rows are in LDS
-          MQ_STAMP(layer * 40 + 2);
-          attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
-          BAR();  // B2
-          MQ_STAMP(layer * 40 + 10);
-          float M0, M1, L0, L1;
-          attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
-          BAR();  // B3
-          MQ_STAMP(layer * 40 + 11);
-          attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
-          BAR();  // B4: K/V rows consumed
-          MQ_STAMP(layer * 40 + 3);
-        }
-        // the store wave's attention-output store goes first: a CU's vector-memory
-        // instructions leave in order, so behind these loads it reached L2 late for
-        // the 31 workgroups that wait on it
-        wait_count(&s_attst, (uint32_t)layer + 1u);
-        load_gu(layer);
-      }
-      // ---------------- o_proj partials: rows 32j + 8s + 2i + rg over the group's 256 columns
-      BAR();  // C1: attention output of the group in s_x1
-      MQ_STAMP(layer * 40 + 4);
-      {
-        const u32x4 xa = x1v[oc];
-        float r[4];
+      };
+      auto load_o = [&](int l) {  // rows 64m + 16s + 2i + org
+        const uint16_t* po = wp(l, W_O) + (size_t)(ROWS * m + 16 * s + org) * QS + 256 * g + 8 * oc;
 #pragma unroll
-        for (int i = 0; i < 4; i++) r[i] = dot_chunk(R.o[i], xa, 0.f);
-        row16_sum_n(r);
-        if (lane == 0) {
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            s_res[8 * s + 2 * i] = readlane(r[i], 0) + readlane(r[i], 16);
-            s_res[8 * s + 2 * i + 1] = readlane(r[i], 32) + readlane(r[i], 48);
-          }
-          signal_store(&s_cnt);
-        }
-        AFTER(r[0] + r[1] + r[2] + r[3]);
-        MQ_STAMP(layer * 40 + 5);
-        if (att) load_d(layer);
-      }
-      // ---------------- gate/up rows of units 384g + 12j + 3s .. +2
-      BAR();  // D1: normed h1 in s_x0
-      MQ_STAMP(layer * 40 + 6);
-      {
-        s_wln[2 * st] = R.wln.x;  // the next layer's input norm and q/k norms
-        s_wln[2 * st + 1] = R.wln.y;
+        for (int i = 0; i < 8; i++) R.o[i] = ldw(po + (size_t)(2 * i) * QS);
+      };
+      auto load_norms = [&](int l) {
+        R.wln = ldw2(wp(l, W_IN) + 4 * st);
+        R.qkn = ldw1(wp(l, st < 64 ? W_QN : W_KN) + 2 * (st & 63));
+      };
+      auto put_norms = [&]() {
+        s_wn[2 * st] = R.wln.x;
+        s_wn[2 * st + 1] = R.wln.y;
         if (st < 128) s_qkn[st] = R.qkn;
-        const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
-        float r[6];
+        publish_norms();
+      };
+      // ---- prologue: layer-0 norms, weights and K/V rows
+      load_norms(0);
+      load_a(0);
+      load_o(0);
+      put_norms();
+      if (att) kv_dma(P, 0, g, c0, nc0, p, lds_kv, s, lane);
+      BAR();  // P0
+      for (int layer = 0; layer < L; layer++) {
+        // ---------------- q/k/v rows 32m + 8s .. +7 of the group's [q0; q1; k; v]
+        BAR();  // A1: normed h in s_x0
+        MQ_STAMP(layer * 40 + 0);
+        {
+          const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
+          float r[8];
 #pragma unroll
-        for (int k = 0; k < 6; k++) r[k] = dot_chunk(R.gu[2 * k], x0, dot_chunk(R.gu[2 * k + 1], x1, 0.f));
-        wave_sum_n(r);
-        if (lane == 0) {
-#pragma unroll
-          for (int k = 0; k < 6; k++) s_res[6 * s + k] = r[k];
-          signal_store(&s_cnt);
+          for (int k = 0; k < 8; k++) r[k] = dot_chunk(R.a[2 * k], x0, dot_chunk(R.a[2 * k + 1], x1, 0.f));
+          wave_sum_t(r);  // lane 16q holds rows 2q, 2q + 1
+          if ((lane & 15) == 0) {
+            s_res[8 * s + 2 * (lane >> 4)] = r[0];
+            s_res[8 * s + 2 * (lane >> 4) + 1] = r[1];
+          }
+          if (lane == 0) signal_store(&s_cnt);
+          AFTER(r[0] + r[1]);
+          MQ_STAMP(layer * 40 + 1);
         }
-        AFTER(r[0] + r[1] + r[2] + r[3] + r[4] + r[5]);
-        MQ_STAMP(layer * 40 + 7);
-        if (att) load_a(nl);
-        // the next layer's K/V rows: the LDS copy is free since B4, and its completion is
-        // first needed behind the next layer's q/k/v weights
-        if (att && nl < L) kv_dma(P, nl, g, c0, nc0, p, lds_kv, s, lane);
+        if (att) {
+          // this wave's K/V copy of the layer has landed (issued in the previous layer's
+          // quiet window; all of the wave's vector-memory operations are awaited)
+          wait_vmem();
+          for (int ps = 0; ps < npass; ps++) {
+            if (ps > 0) {
+              // rows KV_CAP * ps .. of the chunk replace the previous pass's rows
+              kv_dma(P, layer, g, c0 + KV_CAP * ps, pass_rows(ps), p, lds_kv, s, lane);
+              wait_vmem();
+            }
+            const int ncp = pass_rows(ps);
+            BAR();  // B1: q, the new k/v row and the K/V rows are in LDS
+            MQ_STAMP(layer * 40 + 2);
+            attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
+            BAR();  // B2
+            float M0, M1, L0, L1;
+            attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
+            BAR();  // B3
+            attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+            BAR();  // B4: K/V rows consumed
+            MQ_STAMP(layer * 40 + 3);
+          }
+        }
+        // ---------------- o_proj partials: rows 64m + 16s + 2i + org over the group's 256 columns
+        BAR();  // C1: attention output of the group in s_x1
+        MQ_STAMP(layer * 40 + 4);
+        {
+          const u32x4 xa = x1v[oc];
+          float r[8];
+#pragma unroll
+          for (int i = 0; i < 8; i++) r[i] = dot_chunk(R.o[i], xa, 0.f);
+          half_sum_t(r);  // lane 16q holds pairs i + 4 (q & 1), i < 4, of row half q >> 1
+          if ((lane & 15) == 0) {
+            const int q = lane >> 4;
+#pragma unroll
+            for (int i = 0; i < 4; i++) s_res[16 * s + 2 * (i + 4 * (q & 1)) + (q >> 1)] = r[i];
+          }
+          if (lane == 0) signal_store(&s_cnt);
+          AFTER(r[0] + r[1] + r[2] + r[3]);
+          MQ_STAMP(layer * 40 + 5);
+        }
+        // group A's quiet window: once this workgroup's reduce wave has stored its h1 rows,
+        // group B carries the layer, and this workgroup streams its next layer's weights
+        wait_count(&s_red, (uint32_t)layer + 1u);
+        if (layer + 1 < L) {
+          load_norms(layer + 1);
+          load_a(layer + 1);
+          load_o(layer + 1);
+          put_norms();
+          if (att) kv_dma(P, layer + 1, g, c0, nc0, p, lds_kv, s, lane);
+        }
       }
-      // ---------------- down_proj partials: rows 32j + 8s + i over the XCD's 384 units
-      BAR();  // E1: m of the XCD in s_x1
-      MQ_STAMP(layer * 40 + 8);
-      {
-        const u32x4 xm = lane < 48 ? x1v[lane] : u32x4{0u, 0u, 0u, 0u};
-        float r[8];
+    } else {
+      // ================================================================ group B
+      BRegs R;
+      // down_proj: lanes < 48 take chunk `lane` of the XCD's 384 columns (the others re-read
+      // chunk 47 and are multiplied by zero)
+      const int dch = lane < 48 ? lane : 47;
+      auto load_gu = [&](int l) {  // gate and up rows of units 384g + 24m + 6s .. +5
+        const uint16_t* pg = wp(l, W_G) + (size_t)(XUNITS * g + UNITS * m + 6 * s) * H;
+        const uint16_t* pu = wp(l, W_U) + (size_t)(XUNITS * g + UNITS * m + 6 * s) * H;
 #pragma unroll
-        for (int i = 0; i < 8; i++) r[i] = dot_chunk(R.d[i], xm, 0.f);
-        wave_sum_n(r);
-        if (lane == 0) {
-#pragma unroll
-          for (int i = 0; i < 8; i++) s_res[8 * s + i] = r[i];
-          signal_store(&s_cnt);
+        for (int k = 0; k < 6; k++) {
+          R.gu[2 * k] = ldw(pg + k * H + 8 * lane);
+          R.gu[2 * k + 1] = ldw(pg + k * H + 512 + 8 * lane);
         }
-        AFTER(r[0] + r[1] + r[2] + r[3] + r[4] + r[5] + r[6] + r[7]);
-        MQ_STAMP(layer * 40 + 9);
-        if (att && nl < L) load_o(nl);
+#pragma unroll
+        for (int k = 0; k < 6; k++) {
+          R.gu[12 + 2 * k] = ldw(pu + k * H + 8 * lane);
+          R.gu[13 + 2 * k] = ldw(pu + k * H + 512 + 8 * lane);
+        }
+      };
+      auto load_d = [&](int l) {  // rows 64m + 16s .. +15, the XCD's 384 columns
+        const uint16_t* pd = wp(l, W_D) + (size_t)(ROWS * m + 16 * s) * I + XUNITS * g + 8 * dch;
+#pragma unroll
+        for (int i = 0; i < 16; i++) R.d[i] = ldw(pd + (size_t)i * I);
+      };
+      auto put_norms = [&]() {
+        s_wn[2 * st] = R.wpost.x;
+        s_wn[2 * st + 1] = R.wpost.y;
+        publish_norms();
+      };
+      // ---- prologue: layer-0 post-attention norm and weights (streamed during group A's
+      // first layer)
+      R.wpost = ldw2(wp(0, W_POST) + 4 * st);
+      load_gu(0);
+      load_d(0);
+      put_norms();
+      BAR();  // P0
+      for (int layer = 0; layer < L; layer++) {
+        // ---------------- gate/up rows of units 384g + 24m + 6s .. +5
+        BAR();  // D1: normed h1 in s_x0
+        MQ_STAMP(layer * 40 + 6);
+        {
+          const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
+          float r[12];
+#pragma unroll
+          for (int k = 0; k < 12; k++) r[k] = dot_chunk(R.gu[2 * k], x0, dot_chunk(R.gu[2 * k + 1], x1, 0.f));
+          wave_sum_t(r);  // lane 16q holds rows 3q .. 3q + 2
+          if ((lane & 15) == 0) {
+#pragma unroll
+            for (int k = 0; k < 3; k++) s_res[12 * s + 3 * (lane >> 4) + k] = r[k];
+          }
+          if (lane == 0) signal_store(&s_cnt);
+          AFTER(r[0] + r[1] + r[2]);
+          MQ_STAMP(layer * 40 + 7);
+        }
+        // ---------------- down_proj partials: rows 64m + 16s .. +15 over the XCD's 384 units
+        BAR();  // E1: m of the XCD in s_x1
+        MQ_STAMP(layer * 40 + 8);
+        {
+          const u32x4 xm = lane < 48 ? x1v[lane] : u32x4{0u, 0u, 0u, 0u};
+          float r[16];
+#pragma unroll
+          for (int i = 0; i < 16; i++) r[i] = dot_chunk(R.d[i], xm, 0.f);
+          wave_sum_t(r);  // lane 16q holds rows 4q .. 4q + 3
+          if ((lane & 15) == 0) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) s_res[16 * s + 4 * (lane >> 4) + k] = r[k];
+          }
+          if (lane == 0) signal_store(&s_cnt);
+          AFTER(r[0] + r[1] + r[2] + r[3]);
+          MQ_STAMP(layer * 40 + 9);
+        }
+        // group B's quiet window: once this workgroup's reduce wave has stored its h rows,
+        // group A carries the next layer, and this workgroup streams its next MLP weights
+        wait_count(&s_red, (uint32_t)layer + 1u);
+        if (layer + 1 < L) {
+          // hold the burst until group A has published the next layer's q/k/v rows (its
+          // member 0's first word), so that it runs during A's attention
+          {
+            const uint32_t want = tag_of(epoch, layer + 1);
+            uint32_t v = ldl1(wsb, lb + LX_QKV), spins = 0;
+            while ((v >> 16) != want) {
+              if (watchdog(wsb, ws, ++spins)) break;
+              __builtin_amdgcn_s_sleep(4);
+              v = ldl1(wsb, lb + LX_QKV);
+            }
+          }
+          R.wpost = ldw2(wp(layer + 1, W_POST) + 4 * st);
+          load_gu(layer + 1);
+          load_d(layer + 1);
+          put_norms();
+        }
       }
     }
     BAR();  // F1: final normed h in s_x0
-    if (lm) {
-      const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
-      const int rb = r0 + LM_PRE * s;
-#pragma unroll
-      for (int k = 0; k < 4; k++) lm_score(rb + k, r0, R.a[2 * k], R.a[2 * k + 1], x0, x1, s_lg, lane, bestv, besti);
-    }
   } else if (wave < NSW + NPW) {
     // ==================================================================== poll waves
     const int c = wave - NSW, pt = tid - NSW * 64;  // pt: poll thread 0..127
@@ -981,224 +846,237 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         norm_chunk(f, rstd, wn[2 * ch], wn[2 * ch + 1], s_x0 + 2 * ch);
       }
     };
-    // rows 32j .. 32j+31 (chunks 8j .. 8j+7, all in block k = j / 8) for the reduce wave
-    auto keep_rows = [&](const u32x4& hv0, const u32x4& hv1, float* dst) {
-      const int q = lane - ((8 * j) & 63);
-      if (c == (j >> 4) && q >= 0 && q < 8) {  // block j / 8 is in this wave's half
+    // rows 64m .. 64m+63 (chunks 16m .. 16m+15, all in block k = m / 4) for the reduce wave
+    auto keep_rows = [&](const u32x4& hv0, const u32x4& hv1) {
+      const int q = lane - ((16 * m) & 63);
+      if (c == (m >> 3) && q >= 0 && q < 16) {  // block m / 4 is in this wave's half
         float f[4];
-        unpack_tagged((j >> 3) & 1 ? hv1 : hv0, f);
+        unpack_tagged((m >> 2) & 1 ? hv1 : hv0, f);
 #pragma unroll
-        for (int e = 0; e < 4; e++) dst[4 * q + e] = f[e];
+        for (int e = 0; e < 4; e++) s_hrow[4 * q + e] = f[e];
       }
     };
+    // norm weights of layer l published by the stream waves (NSW per layer, from layer 0)
+    auto wait_norms = [&](int l) { wait_count(&s_nrm, (uint32_t)(NSW * (l + 1))); };
 
     u32x4 hv0, hv1;  // this wave's half of the residual stream: chunks lane + 128c and lane + 128c + 64
-    for (int layer = 0; layer < L; layer++) {
-      const uint32_t tag = tag_of(epoch, layer);
-      const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
-      MQ_STAMP(layer * 40 + 12);
-      // ---------------- gather h (each poll wave its half, with the sum of squares), RMSNorm
-      float ss;
-      if (layer == 0) {
-        const uint16_t* src = (P.mode & MODE_INPUT_HIDDEN) ? P.hidden_in : P.embed + (size_t)token * H;
-        ss = 0.f;
+    uint32_t ngat = 0;  // residual-stream gathers so far
+    if (ga) {
+      // ================================================================ group A
+      for (int layer = 0; layer < L; layer++) {
+        const uint32_t tag = tag_of(epoch, layer);
+        const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
+        MQ_STAMP(layer * 40 + 12);
+        // ---------------- gather h (each poll wave its half, with the sum of squares), RMSNorm
+        float ss;
+        if (layer == 0) {
+          const uint16_t* src = (P.mode & MODE_INPUT_HIDDEN) ? P.hidden_in : P.embed + (size_t)token * H;
+          ss = 0.f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const u32x2 v = ldw2(src + 4 * (lane + 64 * k));
-          // widen the raw bf16 values to the tagged layout so every layer reads hv alike
-          const u32x4 t = u32x4{v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16};
-          if (k == 2 * c) hv0 = t;
-          if (k == 2 * c + 1) hv1 = t;
-          float f[4];
-          unpack_tagged(t, f);
-          ss += (f[0] * f[0] + f[1] * f[1]) + (f[2] * f[2] + f[3] * f[3]);
-        }
-        ss = wave_sum(ss);
-      } else {
-        ss = gather_half(wsb, ws, lb + LX_H, lb + LX_HSS, tag_of(epoch, layer - 1), epoch * 32u + (uint32_t)layer, c, lane,
-                         hv0, hv1);
-      }
-      MQ_STAMP(layer * 40 + 13);
-      norm_out(hv0, hv1, ss, s_wln);
-      MQ_STAMP(layer * 40 + 26);
-      keep_rows(hv0, hv1, s_hrow);
-      BAR();  // A1
-      MQ_STAMP(layer * 40 + 14);
-      if (att) {
-        // ---------------- QK-norm, RoPE, K/V row p, attention
-        // wave 0: q heads 2g and 2g+1; wave 1: k and v; lane holds dims lane, lane + 64
-        uint32_t u[4];
-        const uint32_t wq = lb + LX_QKV + 2 * HD * c;
-#pragma unroll
-        for (int q = 0; q < 4; q++) u[q] = ldl1(wsb, wq + 64 * q + lane);
-        {
-          uint32_t spins = 0;
-          while (((u[0] >> 16) != tag) | ((u[1] >> 16) != tag) | ((u[2] >> 16) != tag) | ((u[3] >> 16) != tag)) {
-            if (watchdog(wsb, ws, ++spins)) break;
-            __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-              if ((u[q] >> 16) != tag) u[q] = ldl1(wsb, wq + 64 * q + lane);
+          for (int k = 0; k < 4; k++) {
+            const u32x2 v = ldw2(src + 4 * (lane + 64 * k));
+            // widen the raw bf16 values to the tagged layout so every layer reads hv alike
+            const u32x4 t = u32x4{v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16};
+            if (k == 2 * c) hv0 = t;
+            if (k == 2 * c + 1) hv1 = t;
+            float f[4];
+            unpack_tagged(t, f);
+            ss += (f[0] * f[0] + f[1] * f[1]) + (f[2] * f[2] + f[3] * f[3]);
           }
+          ss = wave_sum(ss);
+        } else {
+          ngat++;
+          wait_cue(wsb, ws, lb + LX_CUE_B, tag_of(epoch, layer - 1));
+          ss = gather_half(wsb, ws, lb + LX_H, tag_of(epoch, layer - 1), c, lane, hv0, hv1, s_ssx, &s_ssn, 2u * ngat);
         }
-        MQ_STAMP(layer * 40 + 15);
-        // HF: q_norm/k_norm over 128 (modeling_qwen3.py:252-253), then apply_rotary_pos_emb (:147-170)
-        const int nseg = c == 0 ? 2 : 1;  // segments that get QK-norm and RoPE
-        float fr[2][2];
+        MQ_STAMP(layer * 40 + 13);
+        wait_norms(layer);
+        norm_out(hv0, hv1, ss, s_wn);
+        keep_rows(hv0, hv1);
+        BAR();  // A1
+        MQ_STAMP(layer * 40 + 14);
+        if (att) {
+          // ---------------- QK-norm, RoPE, K/V row p, attention
+          // wave 0: q heads 2g and 2g+1; wave 1: k and v; lane holds dims lane, lane + 64
+          uint32_t u[4];
+          const uint32_t wq = lb + LX_QKV + 2 * HD * c;
 #pragma unroll
-        for (int sg = 0; sg < 2; sg++) {
-          float fa = bflo(u[2 * sg]), fb = bflo(u[2 * sg + 1]);
-          if (sg < nseg) {
-            const float ssq = wave_sum(fa * fa + fb * fb);
-            const float rstd = 1.0f / sqrtf(ssq * (1.0f / HD) + EPS);
-            const int nw0 = c == 1 ? 64 : 0;
-            const uint32_t na = s_qkn[nw0 + (lane >> 1)], nb = s_qkn[nw0 + 32 + (lane >> 1)];
-            const float wa = (lane & 1) ? bfhi(na) : bflo(na), wb = (lane & 1) ? bfhi(nb) : bflo(nb);
-            fa = rbf(wa * rbf(fa * rstd));
-            fb = rbf(wb * rbf(fb * rstd));
-            const float ra = rbf(rbf(fa * s_cos[lane]) - rbf(fb * s_sin[lane]));
-            const float rb = rbf(rbf(fb * s_cos[lane + 64]) + rbf(fa * s_sin[lane + 64]));
-            fa = ra;
-            fb = rb;
+          for (int q = 0; q < 4; q++) u[q] = ldl1(wsb, wq + 64 * q + lane);
+          {
+            uint32_t spins = 0;
+            while (((u[0] >> 16) != tag) | ((u[1] >> 16) != tag) | ((u[2] >> 16) != tag) | ((u[3] >> 16) != tag)) {
+              if (watchdog(wsb, ws, ++spins)) break;
+              __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+              for (int q = 0; q < 4; q++)
+                if ((u[q] >> 16) != tag) u[q] = ldl1(wsb, wq + 64 * q + lane);
+            }
           }
-          fr[sg][0] = fa;
-          fr[sg][1] = fb;
-        }
-        if (c == 0) {
+          MQ_STAMP(layer * 40 + 15);
+          // HF: q_norm/k_norm over 128 (modeling_qwen3.py:252-253), then apply_rotary_pos_emb (:147-170)
+          const int nseg = c == 0 ? 2 : 1;  // segments that get QK-norm and RoPE
+          float fr[2][2];
 #pragma unroll
           for (int sg = 0; sg < 2; sg++) {
-            s_q[sg * HD + lane] = (uint16_t)f2bf(fr[sg][0]);
-            s_q[sg * HD + 64 + lane] = (uint16_t)f2bf(fr[sg][1]);
+            float fa = bflo(u[2 * sg]), fb = bflo(u[2 * sg + 1]);
+            if (sg < nseg) {
+              const float ssq = wave_sum(fa * fa + fb * fb);
+              const float rstd = 1.0f / sqrtf(ssq * (1.0f / HD) + EPS);
+              const int nw0 = c == 1 ? 64 : 0;
+              const uint32_t na = s_qkn[nw0 + (lane >> 1)], nb = s_qkn[nw0 + 32 + (lane >> 1)];
+              const float wa = (lane & 1) ? bfhi(na) : bflo(na), wb = (lane & 1) ? bfhi(nb) : bflo(nb);
+              fa = rbf(wa * rbf(fa * rstd));
+              fb = rbf(wb * rbf(fb * rstd));
+              const float ra = rbf(rbf(fa * s_cos[lane]) - rbf(fb * s_sin[lane]));
+              const float rb = rbf(rbf(fb * s_cos[lane + 64]) + rbf(fa * s_sin[lane + 64]));
+              fa = ra;
+              fb = rb;
+            }
+            fr[sg][0] = fa;
+            fr[sg][1] = fb;
           }
-        }
-        MQ_STAMP(layer * 40 + 25);
-        for (int ps = 0; ps < npass; ps++) {
-          if (c == 1 && own_p && ps == npass - 1) {
-            // the new k and v rows into the LDS copy of the pass that holds position p (the
-            // store wave appends them to the cache); a second pass's copy excludes that row
-            const int o0 = kv_off(prow, lane >> 3) + 2 * (lane & 7);
-            const int o1 = kv_off(prow, 8 + (lane >> 3)) + 2 * (lane & 7);
+          if (c == 0) {
 #pragma unroll
             for (int sg = 0; sg < 2; sg++) {
-              uint8_t* base = s_kv + sg * (KV_CAP * 256);
-              *reinterpret_cast<uint16_t*>(base + o0) = (uint16_t)f2bf(fr[sg][0]);
-              *reinterpret_cast<uint16_t*>(base + o1) = (uint16_t)f2bf(fr[sg][1]);
+              s_q[sg * HD + lane] = (uint16_t)f2bf(fr[sg][0]);
+              s_q[sg * HD + 64 + lane] = (uint16_t)f2bf(fr[sg][1]);
             }
           }
-          const int ncp = ps ? nc - KV_CAP : nc0;
-          BAR();  // B1
-          MQ_STAMP(layer * 40 + 16);
-          attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
-          BAR();  // B2
-          float M0, M1, L0, L1;
-          attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
-          BAR();  // B3
-          attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
-          BAR();  // B4
-        }
-        MQ_STAMP(layer * 40 + 17);
-      }
-      // ---------------- o_proj input: the group's 256 attention outputs as bf16 pairs in s_x1
-      if (nsplit == 1) {
-        // poll wave 0: the attention workgroup has them in LDS, the others gather them
-        if (c == 0) {
-          if (att) {
-            const int hh = lane >> 5, dim = 4 * (lane & 31);
-            const float* src = &s_ao[hh][dim];
-            reinterpret_cast<u32x2*>(s_x1)[lane] =
-                u32x2{pack_bf2(rbf(src[0]), rbf(src[1])), pack_bf2(rbf(src[2]), rbf(src[3]))};
-          } else {
-            u32x4 v = ldl4(wsb, lb + LX_ATT + 4 * lane);
-            v = repoll_l4(wsb, ws, lb + LX_ATT + 4 * lane, tag, v);
-            reinterpret_cast<u32x2*>(s_x1)[lane] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
+          MQ_STAMP(layer * 40 + 25);
+          for (int ps = 0; ps < npass; ps++) {
+            if (c == 1 && own_p && ps == npass - 1) {
+              // the new k and v rows into the LDS copy of the pass that holds position p (the
+              // store wave appends them to the cache); the passes' copies exclude that row
+              const int o0 = kv_off(prow, lane >> 3) + 2 * (lane & 7);
+              const int o1 = kv_off(prow, 8 + (lane >> 3)) + 2 * (lane & 7);
+#pragma unroll
+              for (int sg = 0; sg < 2; sg++) {
+                uint8_t* base = s_kv + sg * (KV_CAP * 256);
+                *reinterpret_cast<uint16_t*>(base + o0) = (uint16_t)f2bf(fr[sg][0]);
+                *reinterpret_cast<uint16_t*>(base + o1) = (uint16_t)f2bf(fr[sg][1]);
+              }
+            }
+            const int ncp = pass_rows(ps);
+            BAR();  // B1
+            MQ_STAMP(layer * 40 + 16);
+            attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
+            BAR();  // B2
+            float M0, M1, L0, L1;
+            attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
+            BAR();  // B3
+            attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+            BAR();  // B4
           }
+          MQ_STAMP(layer * 40 + 17);
         }
-      } else {
-        // every workgroup merges the XCD's chunk partials itself, straight into its o_proj
-        // input: thread pt takes dims d0, d0 + 1 of head hh (a poll wave per head), CG chunks
-        // per round; lane q loads chunk q's (m, l), which the wave then reads by readlane
-        const int hh = pt >> 6, d0 = 2 * (pt & 63);
-        float Mc = -INFINITY, Lc = 0.f, O0 = 0.f, O1 = 0.f;
-        // nine chunks a round: contexts up to 2303 positions merge in one round (2048 and
-        // past take nine chunks); measured against 4 and 12 a round, and 6, 8 and 16 spill
-        constexpr int CG = 9;
-        for (int s0 = 0; s0 < nsplit; s0 += CG) {
-          const int nq = min(CG, nsplit - s0);
-          const uint32_t b0 = lb + LX_PART + 2 * ((s0 * 2 + hh) * APART);
-          const bool mlane = lane < nq;
-          const uint32_t bml = b0 + 4 * min(lane, nq - 1) * APART;
-          u32x4 ml, ov[CG];  // this lane's chunk (m, tag, l, tag); (acc[d0], tag, acc[d0 + 1], tag) per chunk
-          ml = ldl4(wsb, bml);
-          auto fresh = [&](const u32x4& v) { return (v.y == tag64) & (v.w == tag64); };
-          uint32_t spins = 0;
-          // the chunks' (m, l) first (each stored after its chunk's accumulators, and polled
-          // by one lane per chunk): far less polling traffic than polling every
-          // accumulator pair, 5-14 us per token at split contexts
-          while (mlane && !fresh(ml)) {
-            if (watchdog(wsb, ws, ++spins)) break;
-            __builtin_amdgcn_s_sleep(1);
+        // ---------------- o_proj input: the group's 256 attention outputs as bf16 pairs in s_x1
+        if (nsplit == 1) {
+          // poll wave 0: the attention workgroup has them in LDS, the others gather them
+          if (c == 0) {
+            if (att) {
+              const int hh = lane >> 5, dim = 4 * (lane & 31);
+              const float* src = &s_ao[hh][dim];
+              reinterpret_cast<u32x2*>(s_x1)[lane] =
+                  u32x2{pack_bf2(rbf(src[0]), rbf(src[1])), pack_bf2(rbf(src[2]), rbf(src[3]))};
+            } else {
+              u32x4 v = ldl4(wsb, lb + LX_ATT + 4 * lane);
+              v = repoll_l4(wsb, ws, lb + LX_ATT + 4 * lane, tag, v);
+              reinterpret_cast<u32x2*>(s_x1)[lane] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
+            }
+          }
+        } else {
+          // every A workgroup merges the XCD's chunk partials itself, straight into its o_proj
+          // input: thread pt takes dims d0, d0 + 1 of head hh (a poll wave per head), CG chunks
+          // per round; lane q loads chunk q's (m, l), which the wave then reads by readlane
+          const int hh = pt >> 6, d0 = 2 * (pt & 63);
+          float Mc = -INFINITY, Lc = 0.f, O0 = 0.f, O1 = 0.f;
+          constexpr int CG = 9;
+          for (int s0 = 0; s0 < nsplit; s0 += CG) {
+            const int nq = min(CG, nsplit - s0);
+            const uint32_t b0 = lb + LX_PART + 2 * ((s0 * 2 + hh) * APART);
+            const bool mlane = lane < nq;
+            const uint32_t bml = b0 + 4 * min(lane, nq - 1) * APART;
+            u32x4 ml, ov[CG];  // this lane's chunk (m, tag, l, tag); (acc[d0], tag, acc[d0 + 1], tag) per chunk
             ml = ldl4(wsb, bml);
-          }
-#pragma unroll
-          for (int q = 0; q < CG; q++)
-            if (q < nq) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
-          for (;;) {
-            bool ok = !mlane || fresh(ml);
-#pragma unroll
-            for (int q = 0; q < CG; q++) ok &= q >= nq || fresh(ov[q]);
-            if (ok || watchdog(wsb, ws, ++spins)) break;
-            __builtin_amdgcn_s_sleep(1);
-            if (mlane && !fresh(ml)) ml = ldl4(wsb, bml);
+            auto fresh = [&](const u32x4& v) { return (v.y == tag64) & (v.w == tag64); };
+            uint32_t spins = 0;
+            // the chunks' (m, l) first (each stored after its chunk's accumulators, and polled
+            // by one lane per chunk), then the accumulator pairs
+            while (mlane && !fresh(ml)) {
+              if (watchdog(wsb, ws, ++spins)) break;
+              __builtin_amdgcn_s_sleep(1);
+              ml = ldl4(wsb, bml);
+            }
 #pragma unroll
             for (int q = 0; q < CG; q++)
-              if (q < nq && !fresh(ov[q])) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
-          }
+              if (q < nq) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
+            for (;;) {
+              bool ok = !mlane || fresh(ml);
 #pragma unroll
-          for (int q = 0; q < CG; q++)
-            if (q < nq) {
-              const float m = __uint_as_float(__builtin_amdgcn_readlane(ml.x, q));
-              const float l = __uint_as_float(__builtin_amdgcn_readlane(ml.z, q));
-              const float nm = fmaxf(Mc, m);
-              const float ea = Mc == -INFINITY ? 0.f : expf(Mc - nm), eb = expf(m - nm);
-              Lc = Lc * ea + l * eb;
-              O0 = O0 * ea + __uint_as_float(ov[q].x) * eb;
-              O1 = O1 * ea + __uint_as_float(ov[q].z) * eb;
-              Mc = nm;
+              for (int q = 0; q < CG; q++) ok &= q >= nq || fresh(ov[q]);
+              if (ok || watchdog(wsb, ws, ++spins)) break;
+              __builtin_amdgcn_s_sleep(1);
+              if (mlane && !fresh(ml)) ml = ldl4(wsb, bml);
+#pragma unroll
+              for (int q = 0; q < CG; q++)
+                if (q < nq && !fresh(ov[q])) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
             }
+#pragma unroll
+            for (int q = 0; q < CG; q++)
+              if (q < nq) {
+                const float mq = __uint_as_float(__builtin_amdgcn_readlane(ml.x, q));
+                const float lq = __uint_as_float(__builtin_amdgcn_readlane(ml.z, q));
+                const float nm = fmaxf(Mc, mq);
+                const float ea = Mc == -INFINITY ? 0.f : expf(Mc - nm), eb = expf(mq - nm);
+                Lc = Lc * ea + lq * eb;
+                O0 = O0 * ea + __uint_as_float(ov[q].x) * eb;
+                O1 = O1 * ea + __uint_as_float(ov[q].z) * eb;
+                Mc = nm;
+              }
+          }
+          const float rl = 1.0f / Lc;
+          s_x1[pt] = pack_bf2(rbf(O0 * rl), rbf(O1 * rl));
         }
-        const float rl = 1.0f / Lc;
-        s_x1[pt] = pack_bf2(rbf(O0 * rl), rbf(O1 * rl));
+        MQ_STAMP(layer * 40 + 19);
+        BAR();  // C1
+        MQ_STAMP(layer * 40 + 20);
       }
-      MQ_STAMP(layer * 40 + 19);
-      BAR();  // C1
-      MQ_STAMP(layer * 40 + 20);
-      // ---------------- gather h1; post-attention RMSNorm
-      {
-        const float ss1 = gather_half(wsb, ws, lb + LX_H1, lb + LX_H1SS, tag, tag64, c, lane, hv0, hv1);
+    } else {
+      // ================================================================ group B
+      for (int layer = 0; layer < L; layer++) {
+        const uint32_t tag = tag_of(epoch, layer);
+        const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
+        MQ_STAMP(layer * 40 + 12);
+        // ---------------- gather h1; post-attention RMSNorm
+        ngat++;
+        wait_cue(wsb, ws, lb + LX_CUE_A, tag);
+        const float ss1 = gather_half(wsb, ws, lb + LX_H1, tag, c, lane, hv0, hv1, s_ssx, &s_ssn, 2u * ngat);
         MQ_STAMP(layer * 40 + 21);
-        norm_out(hv0, hv1, ss1, s_wpost);
-        MQ_STAMP(layer * 40 + 27);
-      }
-      BAR();  // D1
-      MQ_STAMP(layer * 40 + 22);
-      // ---------------- down_proj input: m of the XCD's 384 units (96 chunks)
-      {
-        const int q = pt;  // chunks pt, pt + 128 (< 96 only for pt < 96)
-        if (q < XUNITS / 4) {
-          u32x4 v = ldl4(wsb, lb + LX_M + 4 * q);
-          v = repoll_l4(wsb, ws, lb + LX_M + 4 * q, tag, v);
-          reinterpret_cast<u32x2*>(s_x1)[q] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
+        wait_norms(layer);
+        norm_out(hv0, hv1, ss1, s_wn);
+        keep_rows(hv0, hv1);
+        BAR();  // D1
+        MQ_STAMP(layer * 40 + 22);
+        // ---------------- down_proj input: m of the XCD's 384 units (96 chunks)
+        {
+          const int q = pt;
+          if (q < XUNITS / 4) {
+            u32x4 v = ldl4(wsb, lb + LX_M + 4 * q);
+            v = repoll_l4(wsb, ws, lb + LX_M + 4 * q, tag, v);
+            reinterpret_cast<u32x2*>(s_x1)[q] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
+          }
         }
+        MQ_STAMP(layer * 40 + 23);
+        BAR();  // E1
+        MQ_STAMP(layer * 40 + 24);
       }
-      MQ_STAMP(layer * 40 + 23);
-      BAR();  // E1
-      MQ_STAMP(layer * 40 + 24);
     }
 
-    // ---------------- final norm
+    // ---------------- final norm (both groups)
     {
-      const float ss = gather_half(wsb, ws, lb + LX_H, lb + LX_HSS, tag_of(epoch, L - 1), epoch * 32u + (uint32_t)L, c, lane,
-                                   hv0, hv1);
+      ngat++;
+      wait_cue(wsb, ws, lb + LX_CUE_B, tag_of(epoch, L - 1));
+      const float ss = gather_half(wsb, ws, lb + LX_H, tag_of(epoch, L - 1), c, lane, hv0, hv1, s_ssx, &s_ssn, 2u * ngat);
       MQ_STAMP(32 * 40);
       if (lm) norm_out(hv0, hv1, ss, s_wfn);
       if (w == 0) {
@@ -1220,204 +1098,176 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     BAR();  // F1
   } else if (wave == NSW + NPW) {
     // ==================================================================== reduce wave
-    // Residual rows 32j .. 32j+31 from the 8 XCDs' partial sums (identical on every XCD):
-    // lane -> row lane >> 1, XCDs 4 (lane & 1) .. +3.
+    // The workgroup's 64 residual rows (lane = row) from the 8 XCDs' partial sums
+    // (identical on every XCD): group A reduces o_proj into h1, group B down_proj into h.
     BAR();  // P00
     BAR();  // P0
-    const int rr = lane >> 1, hx = lane & 1;
-    float h1v = 0.f;  // h1 row rr (kept for the down_proj residual)
-    // sum of the 8 partials of row rr of `part` in XCD order, identical in both lanes of the pair
-    auto reduce_row = [&](uint32_t part, uint32_t tag64) -> float {
-      const uint32_t wd = part + 2 * ((j * ROWS + rr) * NXCD + 4 * hx);
-      auto ok = [&](const u32x4& v) { return (v.y == tag64) & (v.w == tag64); };
-      uint32_t spins = 0;
-      u32x4 a = xld4(wsb, wd), b = xld4(wsb, wd + 4);
-      // re-poll both stale halves at once (one round trip per iteration)
-      while (!(ok(a) & ok(b))) {
-        if (watchdog(wsb, ws, ++spins)) break;
-        __builtin_amdgcn_s_sleep(1);
-        if (!ok(a)) a = xld4(wsb, wd);
-        if (!ok(b)) b = xld4(wsb, wd + 4);
-      }
-      const float s4 = (__uint_as_float(a.x) + __uint_as_float(a.z)) + (__uint_as_float(b.x) + __uint_as_float(b.z));
-      return s4 + dpp<0xB1>(s4);  // (XCDs 0..3) + (XCDs 4..7), commutative: same bits in both lanes
-    };
+    const int row = ROWS * m + lane;
     for (int layer = 0; layer < L; layer++) {
       const uint32_t tag = tag_of(epoch, layer);
       const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
-      BAR();  // A1: h rows in s_hrow
-      MQ_STAMP(layer * 40 + 28);
-      const float hrow = s_hrow[rr];
-      if (att) {
-        for (int ps = 0; ps < npass; ps++) {
-          const int ncp = ps ? nc - KV_CAP : nc0;
-          BAR();  // B1
-          attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
-          BAR();  // B2
-          float M0, M1, L0, L1;
-          attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
-          BAR();  // B3
-          attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
-          BAR();  // B4
+      if (ga) {
+        BAR();  // A1: h rows in s_hrow
+        MQ_STAMP(layer * 40 + 28);
+        const float hrow = s_hrow[lane];
+        if (att) {
+          for (int ps = 0; ps < npass; ps++) {
+            const int ncp = pass_rows(ps);
+            BAR();  // B1
+            attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
+            BAR();  // B2
+            float M0, M1, L0, L1;
+            attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
+            BAR();  // B3
+            attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+            BAR();  // B4
+          }
         }
+        BAR();  // C1
+        MQ_STAMP(layer * 40 + 29);
+        // h1 = bf16(h + bf16(o)) (modeling_qwen3.py:297-298)
+        const float h1v = rbf(hrow + rbf(reduce_row8(wsb, ws, X_OPART + 2 * (m * NXCD * ROWS + lane), tag64)));
+        st1_plain(ws + lb + LX_H1 + row, tagged(tag, h1v));
+        // the stream waves' next weight loads go behind this store
+        if (lane == 0) signal_store(&s_red);
+        MQ_STAMP(layer * 40 + 30);
+      } else {
+        BAR();  // D1: h1 rows in s_hrow
+        const float h1row = s_hrow[lane];
+        BAR();  // E1
+        MQ_STAMP(layer * 40 + 31);
+        // h' = bf16(h1 + bf16(down)) (modeling_qwen3.py:303-304)
+        const float hn = rbf(h1row + rbf(reduce_row8(wsb, ws, X_DPART + 2 * (m * NXCD * ROWS + lane), tag64)));
+        st1_plain(ws + lb + LX_H + row, tagged(tag, hn));
+        if (lane == 0) signal_store(&s_red);
+        MQ_STAMP(layer * 40 + 32);
       }
-      BAR();  // C1
-      MQ_STAMP(layer * 40 + 29);
-      // h1 = bf16(h + bf16(o)) (modeling_qwen3.py:297-298)
-      h1v = rbf(hrow + rbf(reduce_row(X_OPART, tag64)));
-      if (hx == 0) st1_plain(ws + lb + LX_H1 + ROWS * j + rr, tagged(tag, h1v));
-      {
-        const float ssr = wave_sum(hx == 0 ? h1v * h1v : 0.f);
-        if (lane == 0) st2_plain(ws + lb + LX_H1SS + 2 * j, u32x2{__float_as_uint(ssr), tag64});
-      }
-      MQ_STAMP(layer * 40 + 30);
-      BAR();  // D1
-      BAR();  // E1
-      MQ_STAMP(layer * 40 + 31);
-      // h' = bf16(h1 + bf16(down)) (modeling_qwen3.py:303-304)
-      const float hn = rbf(h1v + rbf(reduce_row(X_DPART, tag64)));
-      if (hx == 0) st1_plain(ws + lb + LX_H + ROWS * j + rr, tagged(tag, hn));
-      {
-        const float ssr = wave_sum(hx == 0 ? hn * hn : 0.f);
-        if (lane == 0) st2_plain(ws + lb + LX_HSS + 2 * j, u32x2{__float_as_uint(ssr), tag64});
-      }
-      MQ_STAMP(layer * 40 + 32);
     }
     BAR();  // F1
   } else {
     // ==================================================================== store wave
     if (lane == 0) {
       s_cnt = 0u;
-      s_attst = 0u;
+      s_red = 0u;
+      s_nrm = 0u;
+      s_ssn = 0u;
     }
     BAR();  // P00
     BAR();  // P0
     // Every launch writes or clears every exchange word it could ever poll, so that the
     // content a poll can find before the awaited write is at most one launch old, whose
     // tags differ from the polled ones: a split launch clears the attention-output words
-    // (read by unsplit launches only), and a workgroup without a chunk partial to store
+    // (read by unsplit launches only), and an A workgroup without a chunk partial to store
     // clears its chunk's record (read by split launches with more chunks).
-    if (SPLIT && j == 0) st4_plain(ws + lb + LX_ATT + 4 * lane, u32x4{0u, 0u, 0u, 0u});
-    if (!SPLIT || !att)
+    if (SPLIT && ga && m == 0) st4_plain(ws + lb + LX_ATT + 4 * lane, u32x4{0u, 0u, 0u, 0u});
+    if (ga && (!SPLIT || !att))
       for (int i = lane; i < 2 * 2 * (int)APART / 4; i += 64)
-        st4_plain(ws + lb + LX_PART + 2 * 2 * APART * j + 4 * i, u32x4{0u, 0u, 0u, 0u});
+        st4_plain(ws + lb + LX_PART + 2 * 2 * APART * m + 4 * i, u32x4{0u, 0u, 0u, 0u});
     uint32_t target = 0;
     for (int layer = 0; layer < L; layer++) {
       const uint32_t tag = tag_of(epoch, layer);
       const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
-      BAR();  // A1
-      target += NSW;
-      wait_count(&s_cnt, target);
-      if (lane < 16) st1_plain(ws + lb + LX_QKV + 16 * j + lane, tagged(tag, rbf(s_res[lane])));
-      MQ_STAMP(layer * 40 + 34);
-      // the next layer's K/V rows into this XCD's L2 ahead of the attention workgroup's
-      // LDS copy at its gate/up stage: copying them from HBM there held up its down_proj
-      // partials, the last input of the layer's final reduction
-      if (!SPLIT && !att && layer + 1 < L) {
-        kv_warm(P, layer + 1, g, p, lds_kv, j - 1, WG_PER_XCD - 1, lane);
-        // and the attention workgroup's weight rows of its stages after attention
-        att_weight_warm(s_lw[layer], s_lw[layer + 1], g, lds_kv, j - 1, WG_PER_XCD - 1, lane);
-      }
-      // the same for a context split over at most SPLIT_WARM_MAX workgroups (measured: it
-      // gains at two and three, and costs from five up, where the copies grow and the
-      // workers fall to 27 or fewer)
-      if (SPLIT && !att && nsplit <= SPLIT_WARM_MAX && layer + 1 < L) {
-        kv_warm(P, layer + 1, g, p, lds_kv, j - nsplit, WG_PER_XCD - nsplit, lane);
-        att_weight_warm_n(s_lw[layer], s_lw[layer + 1], g, nsplit, lds_kv, j - nsplit, WG_PER_XCD - nsplit, lane);
-      }
-      if (att) {
-        float M0 = 0.f, M1 = 0.f, L0 = 0.f, L1 = 0.f, Ma0 = 0.f, Ma1 = 0.f, La0 = 0.f, La1 = 0.f;
-        for (int ps = 0; ps < npass; ps++) {
-          const int ncp = ps ? nc - KV_CAP : nc0;
-          BAR();  // B1
-          if (own_p && ps == npass - 1) {
-            // K/V-cache append at slot p (bf16 [L][8][max_seq][128]): lane -> dims 2 lane, 2 lane + 1
-            const size_t slot = ((size_t)(layer * NKV + g) * P.max_seq_len + p) * HD;
-            const uint32_t k2 = *reinterpret_cast<const uint32_t*>(s_kv + kv_off(prow, lane >> 2) + 4 * (lane & 3));
-            const uint32_t v2 =
-                *reinterpret_cast<const uint32_t*>(s_kv + KV_CAP * 256 + kv_off(prow, lane >> 2) + 4 * (lane & 3));
-            st1_plain(reinterpret_cast<uint32_t*>(P.k_cache + slot) + lane, k2);
-            st1_plain(reinterpret_cast<uint32_t*>(P.v_cache + slot) + lane, v2);
-          }
-          attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
-          BAR();  // B2
-          attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
-          BAR();  // B3
-          attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
-          BAR();  // B4
-          if (ps == 0) {
-            Ma0 = M0;
-            Ma1 = M1;
-            La0 = L0;
-            La1 = L1;
-          }
-        }
-        // lane -> outputs 4 lane .. 4 lane + 3 of head hh = lane / 32
-        const int hh = lane >> 5, dim = 4 * (lane & 31);
-        if (npass == 2) {
-          // merge the two passes exactly: rescale both to the larger maximum
-#pragma unroll
-          for (int h2 = 0; h2 < 2; h2++) {
-            const float ma = h2 ? Ma1 : Ma0, mb = h2 ? M1 : M0, mm = fmaxf(ma, mb);
-            const float ea = expf(ma - mm), eb = expf(mb - mm);
-            if (h2 == hh)
-#pragma unroll
-              for (int e = 0; e < 4; e++) s_ao[hh][dim + e] = s_ao[hh][dim + e] * ea + s_ao1[hh][dim + e] * eb;
-            const float lm2 = (h2 ? La1 : La0) * ea + (h2 ? L1 : L0) * eb;
-            if (h2) {
-              M1 = mm;
-              L1 = lm2;
+      if (ga) {
+        BAR();  // A1
+        target += NSW;
+        wait_count(&s_cnt, target);
+        if (lane < QROWS) st1_plain(ws + lb + LX_QKV + QROWS * m + lane, tagged(tag, rbf(s_res[lane])));
+        MQ_STAMP(layer * 40 + 34);
+        if (att) {
+          float Mr0 = 0.f, Mr1 = 0.f, Lr0 = 0.f, Lr1 = 0.f;  // running max / sum over the passes
+          for (int ps = 0; ps < npass; ps++) {
+            const int ncp = pass_rows(ps);
+            BAR();  // B1
+            if (own_p && ps == npass - 1) {
+              // K/V-cache append at slot p (bf16 [L][8][max_seq][128]): lane -> dims 2 lane, 2 lane + 1
+              const size_t slot = ((size_t)(layer * NKV + g) * P.max_seq_len + p) * HD;
+              const uint32_t k2 = *reinterpret_cast<const uint32_t*>(s_kv + kv_off(prow, lane >> 2) + 4 * (lane & 3));
+              const uint32_t v2 =
+                  *reinterpret_cast<const uint32_t*>(s_kv + KV_CAP * 256 + kv_off(prow, lane >> 2) + 4 * (lane & 3));
+              st1_plain(reinterpret_cast<uint32_t*>(P.k_cache + slot) + lane, k2);
+              st1_plain(reinterpret_cast<uint32_t*>(P.v_cache + slot) + lane, v2);
+            }
+            attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
+            BAR();  // B2
+            float M0, M1, L0, L1;
+            attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
+            BAR();  // B3
+            attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+            BAR();  // B4
+            if (ps == 0) {
+              Mr0 = M0;
+              Mr1 = M1;
+              Lr0 = L0;
+              Lr1 = L1;
             } else {
-              M0 = mm;
-              L0 = lm2;
+              // merge this pass into the running partial exactly: rescale both to the larger
+              // maximum (lane -> outputs 4 lane .. 4 lane + 3 of head lane / 32); done before
+              // the next pass's P.V rewrites s_ao1, which waits for this wave at B1
+              const int hh = lane >> 5, dim = 4 * (lane & 31);
+#pragma unroll
+              for (int h2 = 0; h2 < 2; h2++) {
+                const float ma = h2 ? Mr1 : Mr0, mb = h2 ? M1 : M0, mm = fmaxf(ma, mb);
+                const float ea = expf(ma - mm), eb = expf(mb - mm);
+                if (h2 == hh)
+#pragma unroll
+                  for (int e = 0; e < 4; e++) s_ao[hh][dim + e] = s_ao[hh][dim + e] * ea + s_ao1[hh][dim + e] * eb;
+                const float lm2 = (h2 ? Lr1 : Lr0) * ea + (h2 ? L1 : L0) * eb;
+                if (h2) {
+                  Mr1 = mm;
+                  Lr1 = lm2;
+                } else {
+                  Mr0 = mm;
+                  Lr0 = lm2;
+                }
+              }
             }
           }
+          const int hh = lane >> 5, dim = 4 * (lane & 31);
+          if (nsplit == 1) {
+            st4_plain(ws + lb + LX_ATT + hh * HD + dim,
+                      u32x4{tagged(tag, rbf(s_ao[hh][dim])), tagged(tag, rbf(s_ao[hh][dim + 1])),
+                            tagged(tag, rbf(s_ao[hh][dim + 2])), tagged(tag, rbf(s_ao[hh][dim + 3]))});
+          } else {
+            // chunk partial (m, l, unnormalised acc) as (fp32, tag) pairs; every A workgroup of
+            // the XCD merges them
+            uint32_t* pb = ws + lb + LX_PART + 2 * ((m * 2 + hh) * APART);
+            st4_plain(pb + 2 * (2 + dim), u32x4{__float_as_uint(s_ao[hh][dim]), tag64,
+                                                __float_as_uint(s_ao[hh][dim + 1]), tag64});
+            st4_plain(pb + 2 * (4 + dim), u32x4{__float_as_uint(s_ao[hh][dim + 2]), tag64,
+                                                __float_as_uint(s_ao[hh][dim + 3]), tag64});
+            if (dim == 0)
+              st4_plain(pb, u32x4{__float_as_uint(hh ? Mr1 : Mr0), tag64, __float_as_uint(hh ? Lr1 : Lr0), tag64});
+          }
         }
-        if (nsplit == 1) {
-          st4_plain(ws + lb + LX_ATT + hh * HD + dim,
-                    u32x4{tagged(tag, rbf(s_ao[hh][dim])), tagged(tag, rbf(s_ao[hh][dim + 1])),
-                          tagged(tag, rbf(s_ao[hh][dim + 2])), tagged(tag, rbf(s_ao[hh][dim + 3]))});
-        } else {
-          // chunk partial (m, l, unnormalised acc) as (fp32, tag) pairs; every workgroup of the
-          // XCD merges them
-          uint32_t* pb = ws + lb + LX_PART + 2 * ((j * 2 + hh) * APART);
-          st4_plain(pb + 2 * (2 + dim), u32x4{__float_as_uint(s_ao[hh][dim]), tag64,
-                                              __float_as_uint(s_ao[hh][dim + 1]), tag64});
-          st4_plain(pb + 2 * (4 + dim), u32x4{__float_as_uint(s_ao[hh][dim + 2]), tag64,
-                                              __float_as_uint(s_ao[hh][dim + 3]), tag64});
-          if (dim == 0)
-            st4_plain(pb, u32x4{__float_as_uint(hh ? M1 : M0), tag64, __float_as_uint(hh ? L1 : L0), tag64});
-        }
-        // tells the stream waves that this store is ahead of their next weight loads
-        if (lane == 0) signal_store(&s_attst);
-      }
-      MQ_STAMP(layer * 40 + 35);
-      // o_proj partials of rows 32j .. 32j+31 over this XCD's two heads
-      BAR();  // C1
-      target += NSW;
-      wait_count(&s_cnt, target);
-      if (lane < ROWS)
-        st2_dev(ws + X_OPART + 2 * ((j * ROWS + lane) * NXCD + g), u32x2{__float_as_uint(s_res[lane]), tag64});
+        MQ_STAMP(layer * 40 + 35);
+        // o_proj partials of rows 64m .. 64m+63 over this XCD's two heads
+        BAR();  // C1
+        target += NSW;
+        wait_count(&s_cnt, target);
+        st2_dev(ws + X_OPART + 2 * ((m * NXCD + g) * ROWS + lane), u32x2{__float_as_uint(s_res[lane]), tag64});
+        if (m == 0 && lane == 0) st1_plain(ws + lb + LX_CUE_A, tag);
         MQ_STAMP(layer * 40 + 36);
-      // HF Qwen3MLP (modeling_qwen3.py:81-83): m = bf16(bf16(silu(gate)) * up)
-      BAR();  // D1
-      target += NSW;
-      wait_count(&s_cnt, target);
-      if (lane < UNITS) {
-        const int sw = lane / 3, u = lane - 3 * sw;  // stream wave sw holds gate / up rows 3 sw + u
-        const float gt = rbf(s_res[6 * sw + u]), up = rbf(s_res[6 * sw + 3 + u]);
-        st1_plain(ws + lb + LX_M + UNITS * j + lane, tagged(tag, rbf(rbf(gt / (1.0f + expf(-gt))) * up)));
-      }
-      MQ_STAMP(layer * 40 + 37);
-      // down_proj partials of rows 32j .. 32j+31 over this XCD's 384 units
-      BAR();  // E1
-      target += NSW;
-      wait_count(&s_cnt, target);
-      if (lane < ROWS)
-        st2_dev(ws + X_DPART + 2 * ((j * ROWS + lane) * NXCD + g), u32x2{__float_as_uint(s_res[lane]), tag64});
+      } else {
+        // HF Qwen3MLP (modeling_qwen3.py:81-83): m = bf16(bf16(silu(gate)) * up)
+        BAR();  // D1
+        target += NSW;
+        wait_count(&s_cnt, target);
+        if (lane < UNITS) {
+          const int sw = lane / 6, u = lane - 6 * sw;  // stream wave sw holds gate / up rows 6 sw + u
+          const float gt = rbf(s_res[12 * sw + u]), up = rbf(s_res[12 * sw + 6 + u]);
+          st1_plain(ws + lb + LX_M + UNITS * m + lane, tagged(tag, rbf(rbf(gt / (1.0f + expf(-gt))) * up)));
+        }
+        MQ_STAMP(layer * 40 + 37);
+        // down_proj partials of rows 64m .. 64m+63 over this XCD's 384 units
+        BAR();  // E1
+        target += NSW;
+        wait_count(&s_cnt, target);
+        st2_dev(ws + X_DPART + 2 * ((m * NXCD + g) * ROWS + lane), u32x2{__float_as_uint(s_res[lane]), tag64});
+        if (m == 0 && lane == 0) st1_plain(ws + lb + LX_CUE_B, tag);
         MQ_STAMP(layer * 40 + 38);
+      }
     }
-    wait_vmem();  // the warm-up copies have landed before the LM head reuses their LDS
+    wait_vmem();
     BAR();  // F1
   }
 
@@ -1425,15 +1275,15 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   MQ_STAMP(32 * 40 + 1);
   if (lm) {
     const u32x4 x0 = x0v[lane], x1 = x0v[64 + lane];
-    // rows r0 + NSW * LM_PRE + wave + 8i: four rows per batch, two batches in flight
+    // rows r0 + wave + 8i: four rows per batch, two batches in flight
     auto load_rows = [&](int rb, u32x4 (&Wr)[4][2]) {
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int r = rb + 8 * u;
         if (r < r1) {
-          const uint16_t* row = P.lm_head + (size_t)r * H;
-          Wr[u][0] = ldw(row + 8 * lane);
-          Wr[u][1] = ldw(row + 512 + 8 * lane);
+          const uint16_t* rowp = P.lm_head + (size_t)r * H;
+          Wr[u][0] = ldw(rowp + 8 * lane);
+          Wr[u][1] = ldw(rowp + 512 + 8 * lane);
         }
       }
     };
@@ -1458,7 +1308,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       }
     };
     u32x4 WA[4][2], WB[4][2];
-    const int rs = r0 + NSW * LM_PRE + wave;
+    const int rs = r0 + wave;
     load_rows(rs, WA);
     for (int rb = rs; rb < r1; rb += 64) {
       load_rows(rb + 32, WB);
@@ -1489,6 +1339,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     if (P.mode & MODE_LOGITS)
       for (int i = tid; i < r1 - r0; i += NT) P.logits_out[r0 + i] = s_lg[i];
   }
+
 
   // ---- completion ticket: the last workgroup reduces and resets the workspace
   wait_vmem();

@@ -29,11 +29,14 @@ DECODE_PATH_FLOORS = {
     "c1d": {"teacher_forced": 31, "free_running": 1},
     "c1g": {"teacher_forced": 31, "free_running": 26},
 }
+# Re-measured when the decode kernel's residual-norm sums of squares moved from 32
+# per-workgroup sums to two per-wave half sums (the matvec sums kept their order): c3
+# 1986 -> 1988, c4 117 -> 118, c5 242 -> 247; c1 unchanged.
 EXACT_FLOORS = {
     "c1_teacher_forced": 32, "c1_free_running": 32,
-    "c3_teacher_forced": 1986,
-    "c4_teacher_forced": 117, "c4_free_running": 7,
-    "c5_teacher_forced": 242,
+    "c3_teacher_forced": 1988,
+    "c4_teacher_forced": 118, "c4_free_running": 7,
+    "c5_teacher_forced": 247,
 }
 
 

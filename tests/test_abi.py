@@ -115,8 +115,9 @@ def test_strerror():
 
 def test_decode_plan_bounds_every_position():
     """The kernel's attention split, queried through the C ABI for every accepted position:
-    chunks fit two LDS passes of 256 rows, none is empty and together they cover the
-    context (the kernel also proves this at compile time with a static_assert)."""
+    at most 16 chunks (one per group-A workgroup of an XCD), each within four LDS passes of
+    256 rows, none empty, together covering the context (the kernel also proves this at
+    compile time with a static_assert)."""
     L = _abi.lib()
     inst, ns, ch, npass = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     refs = [ctypes.byref(x) for x in (inst, ns, ch, npass)]
@@ -124,13 +125,15 @@ def test_decode_plan_bounds_every_position():
         assert L.mq_decode_plan(p, *refs) == _abi.MQ_OK
         n = p + 1
         assert inst.value == (0 if p < 256 else 1)
-        assert 1 <= ns.value <= 32 and ch.value <= 512 and npass.value == (ch.value + 255) // 256 <= 2
+        assert 1 <= ns.value <= 16 and ch.value <= 1024 and npass.value == (ch.value + 255) // 256 <= 4
         assert ch.value * ns.value >= n and (ns.value - 1) * ch.value < n
         if p < 256:
             assert ns.value == 1 and ch.value == n
     for p in (-1, 16384):
         assert L.mq_decode_plan(p, *refs) == _abi.MQ_ERR_ARG
-    assert _abi.decode_plan(8447) == {"instance": 1, "nsplit": 32, "chunk": 264, "npass": 2}
+    assert _abi.decode_plan(8447) == {"instance": 1, "nsplit": 16, "chunk": 528, "npass": 3}
+    assert _abi.decode_plan(16383) == {"instance": 1, "nsplit": 16, "chunk": 1024, "npass": 4}
+    assert _abi.decode_plan(1023) == {"instance": 1, "nsplit": 4, "chunk": 256, "npass": 1}
 
 
 def test_device_step_entries_reject_invalid_arguments():

@@ -24,7 +24,10 @@ import itertools
 import pytest
 
 NWG, NXCD, WGX = 256, 8, 32
-ROWS, UNITS, XUNITS = 32, 12, 384
+NGA = NGB = 16          # group-A and group-B workgroups per XCD
+ROWS, QROWS = 64, 32    # residual rows a workgroup reduces; q/k/v rows of an A workgroup
+UNITS, XUNITS = 24, 384  # MLP units of a B workgroup; of an XCD
+MAX_CHUNKS = 16
 L_FULL = 28
 MAX_LAYERS = 32
 
@@ -41,22 +44,26 @@ def tag32(epoch, layer_plus_one):
 # "unsplit"/"split": only launches of that instance write it at every layer, the others
 # clear it (tag 0) at their start; "chunks": chunk j is written at every layer by split
 # launches with j < nsplit, and cleared at the start of every launch that does not write it.
+# LX_H and LX_CUE_B are written by group B (h and its cue), LX_H1, LX_QKV, LX_ATT,
+# LX_PART and LX_CUE_A by group A, LX_M by group B; the cross-XCD arrays by both.
 REGIONS = {
     "LX_H": ("16", "every"), "LX_H1": ("16", "every"), "LX_QKV": ("16", "every"), "LX_M": ("16", "every"),
+    "LX_CUE_A": ("16", "every"), "LX_CUE_B": ("16", "every"),
     "LX_ATT": ("16", "unsplit"),
-    "LX_HSS": ("32", "every"), "LX_H1SS": ("32", "every"),
     "X_OPART": ("32", "every"), "X_DPART": ("32", "every"),
     "LX_PART": ("32", "chunks"),
 }
+# regions gathered at layer l from the previous layer's write (and after the last layer)
+FROM_PREVIOUS_LAYER = ("LX_H", "LX_CUE_B")
 
 
 def expected_tag(region, epoch, layer, L):
-    """Tag a consumer polls for at `layer` (layer == L: the final-norm gather)."""
+    """Tag a consumer polls for at `layer` (layer == L: the final-norm gather). Group B's
+    stream waves also poll LX_QKV word 0 for layer l + 1 before streaming: that is the read
+    of layer l + 1 below, made earlier, against the same stale content."""
     kind = REGIONS[region][0]
-    if region == "LX_H":  # gathered at layer l (> 0) from layer l - 1, and after the last layer
+    if region in FROM_PREVIOUS_LAYER:
         return tag16(epoch, layer - 1)
-    if region == "LX_HSS":
-        return tag32(epoch, layer)
     return tag16(epoch, layer) if kind == "16" else tag32(epoch, layer + 1)
 
 
@@ -67,12 +74,12 @@ def written_tag(region, epoch, layer):
 
 def fresh_write_layer(region, layer):
     """The layer whose write a poll at `layer` waits for."""
-    return layer - 1 if region in ("LX_H", "LX_HSS") else layer
+    return layer - 1 if region in FROM_PREVIOUS_LAYER else layer
 
 
 def reads(region, L):
     """Layers at which a launch of L layers polls the region (L: the final-norm gather)."""
-    if region in ("LX_H", "LX_HSS"):
+    if region in FROM_PREVIOUS_LAYER:
         return range(1, L + 1)
     return range(L)
 
@@ -126,24 +133,20 @@ def test_clears_are_needed_for_the_regions_only_some_launches_write():
 
 # ---------------------------------------------------------------- word coverage
 
-def _qkv_words():
-    return {16 * j + lane for j in range(WGX) for lane in range(16)}
+def _qkv_words():  # store wave of A workgroup a, lanes < 32
+    return {QROWS * a + lane for a in range(NGA) for lane in range(QROWS)}
 
 
-def _rows_words():  # LX_H / LX_H1: reduce wave of workgroup j, lanes with hx == 0 -> row lane >> 1
-    return {ROWS * j + (lane >> 1) for j in range(WGX) for lane in range(64) if (lane & 1) == 0}
+def _rows_words():  # LX_H (B) / LX_H1 (A): reduce wave of member m, lane -> row 64 m + lane
+    return {ROWS * m + lane for m in range(NGA) for lane in range(64)}
 
 
-def _m_words():
-    return {UNITS * j + lane for j in range(WGX) for lane in range(UNITS)}
+def _m_words():  # store wave of B workgroup b, lanes < 24
+    return {UNITS * b + lane for b in range(NGB) for lane in range(UNITS)}
 
 
 def _att_words():  # store wave: lane -> 4 words at hh * 128 + 4 (lane & 31)
     return {(lane >> 5) * 128 + 4 * (lane & 31) + e for lane in range(64) for e in range(4)}
-
-
-def _ss_words():  # one (sum, tag) pair per workgroup j
-    return {2 * j for j in range(WGX)}
 
 
 def _part_words(nsplit):
@@ -161,13 +164,23 @@ def _part_words(nsplit):
     return words
 
 
+def _gather_half_words(c):
+    """Poll wave c of the residual-stream gather: chunks lane + 128 c and lane + 128 c + 64
+    (4 tagged words each)."""
+    return {4 * (ch) + e for lane in range(64) for ch in (lane + 128 * c, lane + 128 * c + 64) for e in range(4)}
+
+
 def test_every_polled_word_is_written_at_every_layer():
     assert _qkv_words() == set(range(512))
     assert _rows_words() == set(range(1024))
     assert _m_words() == set(range(XUNITS))
     assert _att_words() == set(range(256))
-    assert _ss_words() == {2 * j for j in range(WGX)}
-    for nsplit in (1, 2, 9, 32):
+    # the two poll waves' halves of a gather are disjoint and cover the 1024 rows
+    assert _gather_half_words(0) | _gather_half_words(1) == set(range(1024))
+    assert not _gather_half_words(0) & _gather_half_words(1)
+    # the m gather: poll thread q < 96 loads words 4q .. 4q + 3
+    assert {4 * q + e for q in range(XUNITS // 4) for e in range(4)} == _m_words()
+    for nsplit in (1, 2, 9, MAX_CHUNKS):
         words = _part_words(nsplit)
         # the merge polls, for each chunk j < nsplit and head, (m, l) and accumulator pairs
         # of dims d0, d0 + 1 for every d0 = 2 t, t < 64
@@ -177,11 +190,19 @@ def test_every_polled_word_is_written_at_every_layer():
             for t in range(64):
                 d0 = 2 * t
                 assert {base + 4 + 2 * d0 + w for w in range(4)} <= words
+    # the chunk records fit the XCD's region: LX_PART (4096) + 16 chunks x 2 heads x 130 pairs
+    assert 4096 + 2 * MAX_CHUNKS * 2 * 130 <= 32768
 
 
 def test_cross_xcd_partials_cover_every_row():
-    """X_OPART / X_DPART: workgroup (g, j) stores lane < 32 at [j][row lane][xcd g]; the reduce
-    wave of (g', j) polls [j][row rr][xcd 4 hx .. 4 hx + 3] for rr < 32, hx < 2."""
-    written = {(j, r, g) for g in range(NXCD) for j in range(WGX) for r in range(ROWS)}
-    polled = {(j, lane >> 1, 4 * (lane & 1) + x) for j in range(WGX) for lane in range(64) for x in range(4)}
+    """X_OPART / X_DPART ([member][xcd][row] pairs): the store wave of workgroup (g, m)
+    stores lane < 64 at [m][g][lane] (one contiguous 512-byte run); the reduce wave of
+    (g', m) polls [m][x][lane] for every XCD x, lane < 64, one 8-byte pair per load."""
+    written = {(m, g, r) for g in range(NXCD) for m in range(NGA) for r in range(ROWS)}
+    polled = {(m, x, lane) for m in range(NGA) for x in range(NXCD) for lane in range(64)}
     assert polled == written
+    # word offsets: producer 2 ((m 8 + g) 64 + lane), consumer 2 (m 8 64 + lane) + 2 64 x
+    for m, g, lane in itertools.product(range(NGA), range(NXCD), range(64)):
+        assert 2 * ((m * NXCD + g) * ROWS + lane) == 2 * (m * NXCD * ROWS + lane) + 2 * ROWS * g
+    # both arrays fit between the per-XCD regions and the LM-head partials
+    assert 2 * NGA * ROWS * NXCD + 2 * NGB * ROWS * NXCD == 32768
