@@ -34,11 +34,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float bf2f(uint32_t b16) { return __uint_as_float(b16 << 16); }
 __device__ __forceinline__ float bflo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bfhi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-// fp32 -> bf16 bits, round to nearest even (inputs are finite).
-__device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
+typedef __bf16 bfv2 __attribute__((ext_vector_type(2)));
+// fp32 -> bf16 bits, round to nearest even (gfx950's v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t f2bf(float f) { return __builtin_bit_cast(unsigned short, (__bf16)f); }
 // Round an fp32 value to the nearest bf16 value (kept in fp32).
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
@@ -50,8 +48,17 @@ __device__ __forceinline__ void unpack8(const u32x4& w, float (&f)[8]) {
   f[6] = bflo(w.w); f[7] = bfhi(w.w);
 }
 
-// Two bf16 values (low half first) in one word.
-__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+// Two bf16 values (low half first) in one word: one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  const bfv2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+// Round two fp32 values to bf16 (kept in fp32) with one conversion.
+__device__ __forceinline__ void rbf2(float& a, float& b) {
+  const uint32_t p = pack_bf2(a, b);
+  a = bflo(p);
+  b = bfhi(p);
+}
 
 // acc + w.lo * x.lo + w.hi * x.hi on one word of bf16 pairs (v_dot2_f32_bf16: the
 // products are exact in fp32, the sum is accumulated in fp32).

@@ -473,8 +473,11 @@ __device__ __forceinline__ float gather_half(const Buf& b, uint32_t* ws, uint32_
 // HF Qwen3RMSNorm (modeling_qwen3.py:59-64) of one chunk: y = bf16(w * bf16(x * rstd)),
 // written as two bf16 pairs.
 __device__ __forceinline__ void norm_chunk(const float* x, float rstd, uint32_t w0, uint32_t w1, uint32_t* dst) {
-  dst[0] = pack_bf2(rbf(bflo(w0) * rbf(x[0] * rstd)), rbf(bfhi(w0) * rbf(x[1] * rstd)));
-  dst[1] = pack_bf2(rbf(bflo(w1) * rbf(x[2] * rstd)), rbf(bfhi(w1) * rbf(x[3] * rstd)));
+  float a = x[0] * rstd, b = x[1] * rstd, c = x[2] * rstd, d = x[3] * rstd;
+  rbf2(a, b);
+  rbf2(c, d);
+  dst[0] = pack_bf2(bflo(w0) * a, bfhi(w0) * b);
+  dst[1] = pack_bf2(bflo(w1) * c, bfhi(w1) * d);
 }
 
 // Sum of the eight XCDs' (fp32, tag) partials of one row, in XCD order, from the
@@ -914,26 +917,39 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           }
           MQ_STAMP(layer * 40 + 15);
           // HF: q_norm/k_norm over 128 (modeling_qwen3.py:252-253), then apply_rotary_pos_emb (:147-170)
-          const int nseg = c == 0 ? 2 : 1;  // segments that get QK-norm and RoPE
+          // Both waves run both segments without a branch, so that the two dependency chains
+          // interleave; wave 1's second segment (v) keeps its raw values.
           float fr[2][2];
+          {
+            const int nw0 = c == 1 ? 64 : 0;
+            const uint32_t na = s_qkn[nw0 + (lane >> 1)], nb = s_qkn[nw0 + 32 + (lane >> 1)];
+            const float wa = (lane & 1) ? bfhi(na) : bflo(na), wb = (lane & 1) ? bfhi(nb) : bflo(nb);
+            const float ca = s_cos[lane], sa = s_sin[lane], cb = s_cos[lane + 64], sb = s_sin[lane + 64];
+            float x[2][2], ss[2];
 #pragma unroll
-          for (int sg = 0; sg < 2; sg++) {
-            float fa = bflo(u[2 * sg]), fb = bflo(u[2 * sg + 1]);
-            if (sg < nseg) {
-              const float ssq = wave_sum(fa * fa + fb * fb);
-              const float rstd = 1.0f / sqrtf(ssq * (1.0f / HD) + EPS);
-              const int nw0 = c == 1 ? 64 : 0;
-              const uint32_t na = s_qkn[nw0 + (lane >> 1)], nb = s_qkn[nw0 + 32 + (lane >> 1)];
-              const float wa = (lane & 1) ? bfhi(na) : bflo(na), wb = (lane & 1) ? bfhi(nb) : bflo(nb);
-              fa = rbf(wa * rbf(fa * rstd));
-              fb = rbf(wb * rbf(fb * rstd));
-              const float ra = rbf(rbf(fa * s_cos[lane]) - rbf(fb * s_sin[lane]));
-              const float rb = rbf(rbf(fb * s_cos[lane + 64]) + rbf(fa * s_sin[lane + 64]));
-              fa = ra;
-              fb = rb;
+            for (int sg = 0; sg < 2; sg++) {
+              x[sg][0] = bflo(u[2 * sg]);
+              x[sg][1] = bflo(u[2 * sg + 1]);
+              ss[sg] = x[sg][0] * x[sg][0] + x[sg][1] * x[sg][1];
             }
-            fr[sg][0] = fa;
-            fr[sg][1] = fb;
+            wave_sum_n(ss);
+#pragma unroll
+            for (int sg = 0; sg < 2; sg++) {
+              const float rstd = 1.0f / sqrtf(ss[sg] * (1.0f / HD) + EPS);
+              float fa = x[sg][0] * rstd, fb = x[sg][1] * rstd;
+              rbf2(fa, fb);
+              fa *= wa;
+              fb *= wb;
+              rbf2(fa, fb);
+              float p0 = fa * ca, p1 = fb * sa, p2 = fb * cb, p3 = fa * sb;
+              rbf2(p0, p1);
+              rbf2(p2, p3);
+              float ra = p0 - p1, rb = p2 + p3;
+              rbf2(ra, rb);
+              const bool raw = c == 1 && sg == 1;
+              fr[sg][0] = raw ? x[sg][0] : ra;
+              fr[sg][1] = raw ? x[sg][1] : rb;
+            }
           }
           if (c == 0) {
 #pragma unroll
