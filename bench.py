@@ -251,18 +251,23 @@ def main():
                       "wall_ms": wall_ms}
         log(f"pos {p}: {ms * 1e3:.1f} us/step, {1e3 / ms:.0f} tok/s, "
             f"{per_pos[p]['hbm_gbs']:.0f} GB/s algorithmic ({per_pos[p]['hbm_gbs'] / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+    if not per_pos:
+        raise SystemExit(f"no decode position below max_seq_len {max_seq}")
+    # the headline position (BASELINE's decode sweep at 200), or the first one measured
+    main_p = 200 if 200 in per_pos else next(iter(per_pos))
     coop = None
     if not args.no_coop:
         from megaqwen_amd import _abi
 
         prev = _abi.lib().mq_set_launch_mode(1)
         try:
-            cms, _ = time_decode(dec, 200, max(20, args.steps // 2), args.warmup)
+            cms, _ = time_decode(dec, main_p, max(20, args.steps // 2), args.warmup)
         finally:
             _abi.lib().mq_set_launch_mode(prev)
-        coop = {"us_per_step": round(cms * 1e3, 2), "ordinary_us_per_step": round(per_pos[200]["ms"] * 1e3, 2),
-                "extra_us": round((cms - per_pos[200]["ms"]) * 1e3, 2)}
-        log(f"cooperative launch at pos 200: {cms * 1e3:.1f} us/step ({coop['extra_us']:+.1f} us vs ordinary)")
+        coop = {"position": main_p, "us_per_step": round(cms * 1e3, 2),
+                "ordinary_us_per_step": round(per_pos[main_p]["ms"] * 1e3, 2),
+                "extra_us": round((cms - per_pos[main_p]["ms"]) * 1e3, 2)}
+        log(f"cooperative launch at pos {main_p}: {cms * 1e3:.1f} us/step ({coop['extra_us']:+.1f} us vs ordinary)")
     prefill = []
     for S in prefill_lens:
         pms = time_prefill(dec, weights.random_prompt(S, seed=1), steps=10 if S <= 1024 else 4, warmup=2)
@@ -272,7 +277,6 @@ def main():
                         "mfma_frac": round(fl / (pms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)})
         log(f"prefill S={S}: {pms:.3f} ms, {prefill[-1]['tok_s']:.0f} tok/s, {prefill[-1]['tflops']:.1f} TFLOP/s "
             f"({prefill[-1]['mfma_frac']:.1%} of {MFMA_PEAK_TFLOPS:.0f} dense bf16)")
-    main_p = 200
     ms = per_pos[main_p]["ms"]
     e2e = None
     if not args.no_e2e:
@@ -289,7 +293,7 @@ def main():
     achieved = bytes_200 / (ms * 1e-3) / 1e9
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "decode_pos200_traffic.json")
-    if os.path.exists(tpath):
+    if os.path.exists(tpath) and main_p == 200:
         traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_decode_tokens)
     out = {
@@ -305,7 +309,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: seeded random-init Qwen3-0.6B weights N(0,0.02) (seed 0), norms = 1",
-        "config": {"workload": "full-model greedy decode step, batch 1, query at position 200 "
+        "config": {"workload": f"full-model greedy decode step, batch 1, query at position {main_p} "
                                "(BASELINE configs[2] decode sweep; other positions below, 8192/8447 = config 5)",
                    "position": main_p, "num_layers": C.NUM_LAYERS, "max_seq_len": max_seq},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -49,5 +49,26 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+TRACE_SRC = os.path.join(CSRC, "trace", "mq_decode_trace.cpp")
+TRACE_BIN = os.path.join(CSRC, "trace", "mq_decode_trace")
+
+
+def build_trace(verbose: bool = False) -> str:
+    """Compile the tracing build of the decode kernel (a stand-alone executable that prints
+    the per-stage critical path of a layer); returns its path."""
+    flags = [f for f in FLAGS if f not in ("-fPIC", "-shared")]
+    cmd = [HIPCC, *flags, TRACE_SRC, "-o", TRACE_BIN]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
+    return TRACE_BIN
+
+
 if __name__ == "__main__":
-    print(build(verbose=True))
+    if "--trace" in sys.argv[1:]:
+        print(build_trace(verbose=True))
+    else:
+        print(build(verbose=True))

@@ -64,9 +64,10 @@
 #include "../../include/megaqwen_amd.h"
 
 // Instrumentation hooks: MQ_STAMP(slot) marks a point of a layer's timeline
-// (slot = layer * 40 + event; stream events 0..11, poll 12..25, reduce 28..32,
-// store 34..38), MQ_STAMP_DUMP() runs once at the end of the kernel. Both compile
-// to nothing unless a tracing build defines them before including this file.
+// (slot = layer * 40 + event; stream events 0..11, poll 12..27, reduce 28..32,
+// store 34..38; slots 32 * 40 .. +3 the final norm and LM head), MQ_STAMP_DUMP()
+// runs once at the end of the kernel. Both compile to nothing unless a tracing build
+// (csrc/trace/mq_decode_trace.cpp) defines them before including this file.
 #ifndef MQ_STAMP
 #define MQ_STAMP(i) ((void)0)
 #endif
@@ -729,6 +730,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           load_o(layer + 1);
           put_norms();
           if (att) kv_dma(P, layer + 1, g, c0, nc0, p, lds_kv, s, lane);
+          MQ_STAMP(layer * 40 + 10);
         }
       }
     } else {
@@ -822,6 +824,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           load_gu(layer + 1);
           load_d(layer + 1);
           put_norms();
+          MQ_STAMP(layer * 40 + 11);
         }
       }
     }
@@ -977,9 +980,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             MQ_STAMP(layer * 40 + 16);
             attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
             BAR();  // B2
+            MQ_STAMP(layer * 40 + 26);
             float M0, M1, L0, L1;
             attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
             BAR();  // B3
+            MQ_STAMP(layer * 40 + 27);
             attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
             BAR();  // B4
           }

@@ -1,0 +1,206 @@
+// Tracing build of the decode kernel: every role stamps the points of its layer timeline
+// with s_memrealtime (100 MHz) into LDS, and the stamps are dumped per workgroup at the end
+// of the launch. The driver runs the kernel on synthetic weights at one position and prints
+// the per-stage critical path of a layer as a markdown table.
+//
+//   python -m megaqwen_amd.build --trace && megaqwen_amd/csrc/trace/mq_decode_trace 200
+//
+// Times are means over layers 3..26 and over the XCDs. A stage's end is taken at the last
+// workgroup of the XCD to reach it (the one the next stage waits for), measured from the
+// XCD's last h store of the previous layer. Workgroup w runs on XCD w % 8 (an ordinary
+// launch deals workgroups to the XCDs in turn from XCD 0).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+__shared__ uint32_t g_str[32 * 40 + 8];
+__device__ unsigned long long* g_trace;
+#define MQ_STAMP(i)                                                                   \
+  do {                                                                                \
+    const int t_ = threadIdx.x;                                                       \
+    if (t_ == 0 || t_ == 256 || t_ == 384 || t_ == 448) {                             \
+      unsigned long long c_;                                                          \
+      asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(c_)::"memory"); \
+      g_str[(i)] = (uint32_t)c_;                                                      \
+    }                                                                                 \
+  } while (0)
+#define MQ_STAMP_DUMP()                                                \
+  do {                                                                 \
+    for (int i_ = threadIdx.x; i_ < 32 * 40 + 8; i_ += blockDim.x)     \
+      g_trace[(size_t)blockIdx.x * 2048 + i_] = g_str[i_];             \
+  } while (0)
+#include "../mq_decode.hip"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+#define CK(x)                                                                     \
+  do {                                                                            \
+    hipError_t e_ = (x);                                                          \
+    if (e_ != hipSuccess) {                                                       \
+      printf("HIP error %s at line %d\n", hipGetErrorString(e_), __LINE__);       \
+      exit(1);                                                                    \
+    }                                                                             \
+  } while (0)
+
+static void* alloc_fill(size_t n, uint16_t v) {
+  void* p;
+  CK(hipMalloc(&p, n * 2));
+  CK(hipMemsetD16((hipDeviceptr_t)p, v, n));
+  return p;
+}
+
+int main(int argc, char** argv) {
+  const int pos = argc > 1 ? atoi(argv[1]) : 200;
+  const int L = 28, MS = pos + 64 > 2304 ? pos + 64 : 2304;
+  if (pos < 0 || pos >= mq::MAX_CTX) {
+    printf("position must be in [0, %d)\n", mq::MAX_CTX);
+    return 2;
+  }
+  // synthetic weights: bf16 constants (1.0 norms, 2^-7 elsewhere), cos = sin = 0.5
+  std::vector<LDGLayerWeights> lw(L);
+  for (int l = 0; l < L; l++) {
+    lw[l].input_layernorm_weight = alloc_fill(1024, 0x3f80);
+    lw[l].q_proj_weight = alloc_fill(2048 * 1024, 0x3c00);
+    lw[l].k_proj_weight = alloc_fill(1024 * 1024, 0x3c00);
+    lw[l].v_proj_weight = alloc_fill(1024 * 1024, 0x3c00);
+    lw[l].q_norm_weight = alloc_fill(128, 0x3f80);
+    lw[l].k_norm_weight = alloc_fill(128, 0x3f80);
+    lw[l].o_proj_weight = alloc_fill(1024 * 2048, 0x3c00);
+    lw[l].post_attn_layernorm_weight = alloc_fill(1024, 0x3f80);
+    lw[l].gate_proj_weight = alloc_fill(3072 * 1024, 0x3c00);
+    lw[l].up_proj_weight = alloc_fill(3072 * 1024, 0x3c00);
+    lw[l].down_proj_weight = alloc_fill(1024 * 3072, 0x3c00);
+  }
+  LDGLayerWeights* dlw;
+  CK(hipMalloc(&dlw, sizeof(LDGLayerWeights) * L));
+  CK(hipMemcpy(dlw, lw.data(), sizeof(LDGLayerWeights) * L, hipMemcpyHostToDevice));
+  void* embed = alloc_fill((size_t)151936 * 1024, 0x3c00);
+  void* fnorm = alloc_fill(1024, 0x3f80);
+  void* cosb = alloc_fill((size_t)MS * 128, 0x3f00);
+  void* sinb = alloc_fill((size_t)MS * 128, 0x3f00);
+  void* kc = alloc_fill((size_t)L * 8 * MS * 128, 0x3c00);
+  void* vc = alloc_fill((size_t)L * 8 * MS * 128, 0x3c00);
+  void* hid = alloc_fill(1024, 0);
+  float* normed;
+  CK(hipMalloc(&normed, 4096));
+  int* tok;
+  CK(hipMalloc(&tok, 4));
+  unsigned long long* tr;
+  CK(hipMalloc(&tr, 256 * 2048 * 8));
+  CK(hipMemset(tr, 0, 256 * 2048 * 8));
+  CK(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &tr, sizeof(tr)));
+  hipEvent_t e0, e1;
+  CK(hipEventCreate(&e0));
+  CK(hipEventCreate(&e1));
+  float ms = 0;
+  for (int it = 0; it < 10; it++) {
+    CK(hipEventRecord(e0));
+    const int st = launch_ldg_decode(1234, tok, embed, dlw, fnorm, embed, cosb, sinb, kc, vc, hid, nullptr, nullptr,
+                                     nullptr, nullptr, nullptr, nullptr, nullptr, normed, nullptr, nullptr, L, pos,
+                                     pos + 1, MS, 0.0883883f, 0);
+    CK(hipEventRecord(e1));
+    CK(hipEventSynchronize(e1));
+    CK(hipEventElapsedTime(&ms, e0, e1));
+    if (st) {
+      printf("launch status %d\n", st);
+      return 1;
+    }
+  }
+  int htok;
+  CK(hipMemcpy(&htok, tok, 4, hipMemcpyDeviceToHost));
+  if (htok < 0) {
+    printf("kernel error %d\n", htok);
+    return 1;
+  }
+  std::vector<unsigned long long> h(256 * 2048);
+  CK(hipMemcpy(h.data(), tr, h.size() * 8, hipMemcpyDeviceToHost));
+  auto T = [&](int w, int l, int k) { return (int64_t)(uint32_t)h[(size_t)w * 2048 + l * 40 + k]; };
+  const int nsplit = mq::plan_nsplit(pos + 1);
+
+  // the last of a member set of XCD g to reach event k of layer l
+  auto last = [&](int g, int l, int k, int j0, int j1) {
+    int64_t t = INT64_MIN;
+    for (int j = j0; j < j1; j++) t = std::max(t, T(8 * j + g, l, k));
+    return t;
+  };
+  auto T0 = [&](int l, int g) { return last(g, l - 1, 32, 16, 32); };  // the XCD's last h store of layer l - 1
+
+  struct Stage {
+    const char* name;
+    int k, j0, j1;  // event slot, member range whose last arrival ends the stage
+    const char* what;
+  };
+  const int A0 = 0, A1 = 16, B0 = 16, B1 = 32;
+  const Stage st[] = {
+      {"h gathered (group A poll waves)", 13, A0, A1, "hop: XCD-local all-gather of h, sum of squares"},
+      {"A1: input RMSNorm done", 14, A0, A1, "compute: RMSNorm, barrier"},
+      {"q/k/v dot products handed over", 1, A0, A1, "compute: 32 rows x 1024 per workgroup"},
+      {"q/k/v stored", 34, A0, A1, "store wave"},
+      {"q/k/v polled by the attention workgroup", 15, 0, nsplit, "hop: XCD-local"},
+      {"QK-norm + RoPE done", 25, 0, nsplit, "compute"},
+      {"B1: q, k, v in LDS", 16, 0, nsplit, "barrier"},
+      {"B2: scores", 26, 0, nsplit, "compute: MFMA QK^T (first LDS pass)"},
+      {"B3: softmax", 27, 0, nsplit, "compute"},
+      {"attention done", 17, 0, nsplit, "compute: MFMA P.V (all passes)"},
+      {"attention output stored", 35, 0, nsplit, "store wave"},
+      {"o_proj input ready (all group A)", 19, A0, A1, "hop: XCD-local hand-out (or chunk merge)"},
+      {"C1", 20, A0, A1, "barrier"},
+      {"o_proj dot products handed over", 5, A0, A1, "compute: 64 rows x 256 per workgroup"},
+      {"o_proj partials stored", 36, A0, A1, "store wave (sc1)"},
+      {"h1 rows stored (reduce waves)", 30, A0, A1, "hop: cross-XCD reduction of 8 partials"},
+      {"h1 gathered (group B poll waves)", 21, B0, B1, "hop: XCD-local all-gather of h1"},
+      {"D1: post-attention RMSNorm done", 22, B0, B1, "compute: RMSNorm, barrier"},
+      {"gate/up dot products handed over", 7, B0, B1, "compute: 48 rows x 1024 per workgroup"},
+      {"m stored", 37, B0, B1, "store wave: SiLU(gate) * up"},
+      {"m gathered", 23, B0, B1, "hop: XCD-local all-gather of m"},
+      {"E1", 24, B0, B1, "barrier"},
+      {"down_proj dot products handed over", 9, B0, B1, "compute: 64 rows x 384 per workgroup"},
+      {"down_proj partials stored", 38, B0, B1, "store wave (sc1)"},
+      {"h rows stored (reduce waves)", 32, B0, B1, "hop: cross-XCD reduction of 8 partials"},
+  };
+  const int nst = sizeof(st) / sizeof(st[0]);
+  std::vector<double> end(nst, 0.0);
+  int n = 0;
+  for (int l = 3; l <= 26; l++)
+    for (int g = 0; g < 8; g++) {
+      const int64_t t0 = T0(l, g);
+      for (int i = 0; i < nst; i++) end[i] += (double)(int32_t)(last(g, l, st[i].k, st[i].j0, st[i].j1) - t0) * 0.01;
+      n++;
+    }
+  for (auto& e : end) e /= n;
+  double per = 0;
+  int np = 0;
+  for (int l = 3; l <= 26; l++)
+    for (int g = 0; g < 8; g++) {
+      per += (double)(int32_t)(T0(l + 1, g) - T0(l, g)) * 0.01;
+      np++;
+    }
+  per /= np;
+
+  printf("Decode kernel trace at position %d: %.1f us per launch (tracing build), %d attention chunk(s) per XCD\n\n",
+         pos, ms * 1e3, nsplit);
+  printf("| # | stage ends when | what | end (us) | stage (us) |\n|---|---|---|---|---|\n");
+  double prev = 0, hop = 0;
+  for (int i = 0; i < nst; i++) {
+    const double d = end[i] - prev;
+    printf("| %d | %s | %s | %.2f | %.2f |\n", i + 1, st[i].name, st[i].what, end[i], d);
+    if (st[i].what[0] == 'h' && st[i].what[1] == 'o') hop += d;
+    prev = end[i];
+  }
+  printf("\nLayer period (XCD's last h store to the next): %.2f us; hop stages add up to %.2f us.\n", per, hop);
+  // final norm and LM head
+  double fin = 0, lm = 0;
+  int64_t first = INT64_MAX, lastf2 = INT64_MIN;
+  for (int w = 0; w < 256; w++) {
+    fin += (double)(int32_t)(T(w, 32, 0) - T0(28, w % 8)) * 0.01;
+    lm += (double)(int32_t)(T(w, 32, 2) - T(w, 32, 1)) * 0.01;
+    first = std::min(first, T(w, 0, 12));
+    lastf2 = std::max(lastf2, T(w, 32, 3));
+  }
+  printf("Final gather and norm %.2f us after the last h store; LM-head loop %.2f us (workgroup mean); "
+         "first layer start to the last workgroup's LM head end %.1f us.\n",
+         fin / 256, lm / 256, (lastf2 - first) * 0.01);
+  return 0;
+}
