@@ -23,7 +23,7 @@ extern "C" {
 #define MQ_OK 0
 #define MQ_ERR_ARG (-1)      /* invalid argument (checked on the host before any HIP call) */
 #define MQ_ERR_HIP (-2)      /* a HIP runtime call failed */
-#define MQ_ERR_DEVICE (-3)   /* device cannot run the cooperative grid */
+#define MQ_ERR_DEVICE (-3)   /* device cannot hold the decode grid (256 resident workgroups) */
 #define MQ_ERR_ALLOC (-4)    /* workspace allocation failed */
 
 /* Per-layer weight pointers, bf16, HF nn.Linear layout [out, in].
