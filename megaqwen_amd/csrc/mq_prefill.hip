@@ -5,7 +5,8 @@
 // slots 0..S-1 of every layer are written, and the greedy next token is taken
 // from the last row. After embed_rows and the first layer's rmsnorm_rows, per layer:
 //   gemm_nt (q, k, v in one launch; its epilogue applies QK-norm and RoPE and appends K/V)
-//   -> attn_prefill (causal, MFMA) -> gemm_nt (o_proj, k split four ways)
+//   -> attn_prefill or, past 1024 tokens, attn_prefill_fa (causal, MFMA)
+//   -> gemm_nt (o_proj, k split four ways)
 //   -> resid_norm_rows (partials + residual, post-attention RMSNorm)
 //   -> gemm_nt (gate and up, SiLU(gate) * up epilogue) -> gemm_nt (down_proj, k split)
 //   -> resid_norm_rows (partials + residual, the next layer's input RMSNorm)
@@ -615,6 +616,207 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
 #undef AWAIT
 #undef ABAR
 
+// ------------------------------------------------------------------ causal attention, flash form
+// Workgroup (KV group g, query block): query rows r0 .. r0 + 16 RT - 1 of both query heads of
+// the group (2g, 2g + 1), one wave per (head, 16-row tile), 2 RT waves. Every K/V chunk
+// copied into LDS therefore serves 32 RT query rows. Keys run in blocks of 512 (torch's CPU
+// flash blocks) with a running maximum, as attn_prefill.
+//
+// Scores are computed transposed, S^T = K Q^T (K rows from LDS as the A operand, the wave's
+// Q rows as the B operand, held in registers): lane (r16, kg) holds the scores of query row
+// r16 against keys 16 t + 4 kg + e of tile t. So a whole block's scores stay in registers
+// (32 tiles), the softmax of a query row is the lane's own plus a reduction over its four
+// lane groups, and the bf16 probabilities are already the B operand of O^T = V^T P^T: keys
+// 4 kg + i of tiles 2j, 2j + 1 (i < 4) form k-slots 8 kg + i of key step j, and V^T is read
+// in the same key order by LDS transpose reads. No score or probability goes through LDS.
+//
+// K and V reach LDS in 64-key chunks (16 KB, 1 KB DMA instructions) through a ring of FNB
+// buffers, two chunks ahead: for each 512-key block its K chunks, then its V chunks.
+constexpr int FK = 64, FNB = 4, FKB = 512;
+constexpr int FLASH_MIN_S = 1024;  // prompts longer than this take the flash form
+
+__device__ __forceinline__ float lane_group_max(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float lane_group_sum(float v) {
+  // (g0 + g2) + (g1 + g3) in every lane group, the same order everywhere
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int RT>
+__global__ void __launch_bounds__(128 * RT) attn_prefill_fa(const uint16_t* q, const uint16_t* kc,
+                                                            const uint16_t* vc, uint16_t* out, int S, int max_seq,
+                                                            float scale) {
+  constexpr int NW = 2 * RT, QB = 16 * RT, PER = 16 / NW;  // waves, query rows, DMA instructions per chunk and wave
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  __shared__ __align__(16) uint8_t s_kv[FNB][FK * 256];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int hh = wv / RT, rt = wv - RT * hh;
+  // XCD-aware order: workgroup id runs on XCD id % 8, made the KV group; the longest query
+  // blocks (the most keys) are dispatched first
+  const int id = blockIdx.x, g = id & 7, nqb = gridDim.x >> 3;
+  const int r0 = (nqb - 1 - (id >> 3)) * QB, h = 2 * g + hh;
+  const int r16 = lane & 15, kg = lane >> 4;
+  const int row = r0 + 16 * rt + r16;       // this lane's query row
+  const int wrow1 = r0 + 16 * rt + 15;  // the wave's last query row
+  const int nkey = min(S, r0 + QB);
+  const int nblk = (nkey + FKB - 1) / FKB;
+  const int nch_last = (nkey - FKB * (nblk - 1) + FK - 1) / FK;
+  const int total = 2 * (8 * (nblk - 1) + nch_last);  // chunks: K then V of every block
+  const uint16_t* K = kc + (size_t)g * max_seq * HD;
+  const uint16_t* V = vc + (size_t)g * max_seq * HD;
+  const uint32_t kv0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_kv[0][0];
+
+  // chunk n of the sequence into ring buffer n % FNB: instruction i of wave wv moves rows
+  // 4 q .. 4 q + 3 (q = wv + NW i; lane -> row 4 q + lane / 16, slot lane % 16); rows past
+  // the block's last key repeat it
+  auto issue = [&](int n) {
+    if (n >= total) return;
+    int b = n >> 4, rem = n & 15, nchb = 8;
+    if (b >= nblk - 1) {
+      b = nblk - 1;
+      rem = n - 16 * b;
+      nchb = nch_last;
+    }
+    const bool isv = rem >= nchb;
+    const int c = isv ? rem - nchb : rem;
+    const int kb0 = FKB * b, klast = min(nkey, kb0 + FKB) - 1;
+    const uint16_t* src = isv ? V : K;
+    const uint32_t lds = kv0 + (uint32_t)(n % FNB) * (FK * 256);
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int qq = wv + NW * i, r = 4 * qq + (lane >> 4), chunk = (lane & 15) ^ (r & 15);
+      dma16(src + (size_t)min(kb0 + FK * c + r, klast) * HD + 8 * chunk, __builtin_amdgcn_readfirstlane(lds + 1024u * qq));
+    }
+  };
+  // chunk n has landed for every wave (chunks up to n + 1 are in flight), and every wave is
+  // done with chunk n - 1, whose successor in the ring the caller may then refill
+  auto arrive = [&](int n) {
+    if (n + 1 < total)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+
+  // Q^T (B operand): lane (row r16, kg) holds dims 32 ks + 8 kg .. +7 of its row
+  u32x4 qf[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ks++) qf[ks] = ldw(q + (size_t)min(row, S - 1) * QS + HD * h + 32 * ks + 8 * kg);
+  f32x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  issue(0);
+  issue(1);
+  int n = 0;
+  for (int b = 0; b < nblk; b++) {
+    const int kb0 = FKB * b, kb1 = min(nkey, kb0 + FKB), nchb = (kb1 - kb0 + FK - 1) / FK;
+    f32x4 sc[32];
+    // ---- scores of the block: chunk c holds tiles 4c .. 4c + 3
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      if (c < nchb) {
+        arrive(n);
+        issue(n + 2);
+        const uint8_t* kb = s_kv[n % FNB];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int t = 4 * c + j, key0 = kb0 + 16 * t;
+          if (key0 <= wrow1) {
+            u32x4 kf[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+              kf[ks] = *reinterpret_cast<const u32x4*>(kb + akv_off(16 * j + r16, 4 * ks + kg));
+            f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) a = mfma_16x16x32(kf[ks], qf[ks], a);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              const int key = key0 + 4 * kg + e;
+              sc[t][e] = (key < kb1 && key <= row) ? a[e] * scale : -INFINITY;
+            }
+          } else {
+            sc[t] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+          }
+        }
+        n++;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) sc[4 * c + j] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      }
+    }
+    // ---- softmax with the running maximum: query row = lane column r16
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 32; t++) mx = fmaxf(fmaxf(mx, fmaxf(sc[t][0], sc[t][1])), fmaxf(sc[t][2], sc[t][3]));
+    mx = lane_group_max(mx);
+    const float mn = fmaxf(m_run, mx), base = mn == -INFINITY ? 0.f : mn;
+    const float al = m_run == -INFINITY ? 0.f : expf(m_run - base);
+    u32x2 pb[32];
+    float sum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 32; t++) {
+      float e4[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        e4[e] = exp_fast(sc[t][e] - base);  // exp(-inf) = 0 past the keys
+        sum += e4[e];
+      }
+      pb[t] = u32x2{pack_bf2(e4[0], e4[1]), pack_bf2(e4[2], e4[3])};
+    }
+    sum = lane_group_sum(sum);
+    l_run = sum + al * l_run;
+    m_run = mn;
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) o[dt] *= al;
+    // ---- O^T += V^T P^T: chunk c holds key steps 2c, 2c + 1 (tiles 4c .. 4c + 3)
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      if (c < nchb) {
+        arrive(n);
+        issue(n + 2);
+        const uint32_t vb = kv0 + (uint32_t)(n % FNB) * (FK * 256);
+#pragma unroll
+        for (int j2 = 0; j2 < 2; j2++) {
+          const int t0 = 4 * c + 2 * j2;
+          if (kb0 + 16 * t0 <= wrow1) {
+            const u32x4 pf = u32x4{pb[t0].x, pb[t0].y, pb[t0 + 1].x, pb[t0 + 1].y};
+            const int ra = 32 * j2 + 4 * kg + (r16 >> 2);
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+              const int dq = 16 * dt + 4 * (r16 & 3);
+              const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_v4s*)(uintptr_t)(vb + akv_off(ra, dq >> 3) + 2 * (dq & 7)));
+              const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_v4s*)(uintptr_t)(vb + akv_off(ra + 16, dq >> 3) + 2 * (dq & 7)));
+              const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+              o[dt] = mfma_16x16x32(u32x4{l2.x, l2.y, h2.x, h2.y}, pf, o[dt]);
+            }
+          }
+        }
+        n++;
+      }
+    }
+  }
+  if (row < S) {
+    const float inv = 1.0f / l_run;
+    uint16_t* op = out + (size_t)row * QS + HD * h + 4 * kg;
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++)
+      *reinterpret_cast<u32x2*>(op + 16 * dt) =
+          u32x2{pack_bf2(o[dt][0] * inv, o[dt][1] * inv), pack_bf2(o[dt][2] * inv, o[dt][3] * inv)};
+  }
+}
+
 // ------------------------------------------------------------------ LM head
 constexpr int LMB = 1184;  // partial-argmax blocks (the length of the reference's block_max_* buffers)
 
@@ -826,7 +1028,12 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     g.qkn = QknArgs{bf(w.q_norm_weight), bf(w.k_norm_weight), bf(cos_table), bf(sin_table), qp, kcl, vcl, max_seq_len};
     gemm<EPI_QKN, TM_QKV, TN_QKV, GST, GKS, QKV_WM, QKV_WN>(g, (QS + 2 * KVS) / TN_QKV, stream);
     chk();
-    attn_prefill<<<NQ * ((S + AQ - 1) / AQ), 256, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
+    // long prompts: the flash form (64 rows of both heads a workgroup); short ones: 32 rows of
+    // one head a workgroup, which fills more CUs (256 workgroups at S = 512)
+    if (S > FLASH_MIN_S)
+      attn_prefill_fa<4><<<NKV * ((S + 63) / 64), 512, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
+    else
+      attn_prefill<<<NQ * ((S + AQ - 1) / AQ), 256, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
     chk();
     GemmArgs go{};
     go.a = att; go.lda = QS; go.m = S; go.k = QS; go.nseg = 1;
