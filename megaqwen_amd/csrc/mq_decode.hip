@@ -505,6 +505,49 @@ __device__ __forceinline__ float reduce_row8(const Buf& wsb, uint32_t* ws, uint3
   return ((f(0) + f(1)) + (f(2) + f(3))) + ((f(4) + f(5)) + (f(6) + f(7)));
 }
 
+// Polls N tagged words (word w[i] + lane) of the XCD's exchange region until all carry `tag`.
+template <int N>
+__device__ __forceinline__ void poll_words(const Buf& wsb, uint32_t* ws, const uint32_t (&w)[N], uint32_t tag,
+                                           uint32_t (&u)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; i++) u[i] = ldl1(wsb, w[i]);
+  uint32_t spins = 0;
+  for (;;) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < N; i++) ok &= (u[i] >> 16) == tag;
+    if (ok || watchdog(wsb, ws, ++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int i = 0; i < N; i++)
+      if ((u[i] >> 16) != tag) u[i] = ldl1(wsb, w[i]);
+  }
+}
+
+// HF Qwen3's q_norm / k_norm over one head (modeling_qwen3.py:252-253), then RoPE
+// (apply_rotary_pos_emb, :147-170), each op rounded to bf16: lane holds dims lane and
+// lane + 64 (tagged words u0, u1); nw0 selects the q_norm (0) or k_norm (64) weight words.
+__device__ __forceinline__ void qk_norm_rope(uint32_t u0, uint32_t u1, const uint32_t* s_qkn, int nw0,
+                                             const float* s_cos, const float* s_sin, int lane, float& ra,
+                                             float& rb) {
+  const uint32_t na = s_qkn[nw0 + (lane >> 1)], nb = s_qkn[nw0 + 32 + (lane >> 1)];
+  const float wa = (lane & 1) ? bfhi(na) : bflo(na), wb = (lane & 1) ? bfhi(nb) : bflo(nb);
+  const float x0 = bflo(u0), x1 = bflo(u1);
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float rstd = 1.0f / sqrtf(ss * (1.0f / HD) + EPS);
+  float fa = x0 * rstd, fb = x1 * rstd;
+  rbf2(fa, fb);
+  fa *= wa;
+  fb *= wb;
+  rbf2(fa, fb);
+  float p0 = fa * s_cos[lane], p1 = fb * s_sin[lane], p2 = fb * s_cos[lane + 64], p3 = fa * s_sin[lane + 64];
+  rbf2(p0, p1);
+  rbf2(p2, p3);
+  ra = p0 - p1;
+  rb = p2 + p3;
+  rbf2(ra, rb);
+}
+
 // ---------------------------------------------------------------- the kernel
 // SPLIT = false is the instance for contexts of at most KV_CAP positions (one
 // attention workgroup per XCD, one LDS pass): the chunk-merge and multi-pass code
@@ -903,63 +946,26 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         MQ_STAMP(layer * 40 + 14);
         if (att) {
           // ---------------- QK-norm, RoPE, K/V row p, attention
-          // wave 0: q heads 2g and 2g+1; wave 1: k and v; lane holds dims lane, lane + 64
-          uint32_t u[4];
-          const uint32_t wq = lb + LX_QKV + 2 * HD * c;
-#pragma unroll
-          for (int q = 0; q < 4; q++) u[q] = ldl1(wsb, wq + 64 * q + lane);
-          {
-            uint32_t spins = 0;
-            while (((u[0] >> 16) != tag) | ((u[1] >> 16) != tag) | ((u[2] >> 16) != tag) | ((u[3] >> 16) != tag)) {
-              if (watchdog(wsb, ws, ++spins)) break;
-              __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-              for (int q = 0; q < 4; q++)
-                if ((u[q] >> 16) != tag) u[q] = ldl1(wsb, wq + 64 * q + lane);
-            }
-          }
-          MQ_STAMP(layer * 40 + 15);
-          // HF: q_norm/k_norm over 128 (modeling_qwen3.py:252-253), then apply_rotary_pos_emb (:147-170)
-          // Both waves run both segments without a branch, so that the two dependency chains
-          // interleave; wave 1's second segment (v) keeps its raw values.
+          // poll wave 0: q head 2g; poll wave 1: k and v; the reduce wave: q head 2g + 1
+          // (lane holds dims lane, lane + 64)
           float fr[2][2];
-          {
-            const int nw0 = c == 1 ? 64 : 0;
-            const uint32_t na = s_qkn[nw0 + (lane >> 1)], nb = s_qkn[nw0 + 32 + (lane >> 1)];
-            const float wa = (lane & 1) ? bfhi(na) : bflo(na), wb = (lane & 1) ? bfhi(nb) : bflo(nb);
-            const float ca = s_cos[lane], sa = s_sin[lane], cb = s_cos[lane + 64], sb = s_sin[lane + 64];
-            float x[2][2], ss[2];
-#pragma unroll
-            for (int sg = 0; sg < 2; sg++) {
-              x[sg][0] = bflo(u[2 * sg]);
-              x[sg][1] = bflo(u[2 * sg + 1]);
-              ss[sg] = x[sg][0] * x[sg][0] + x[sg][1] * x[sg][1];
-            }
-            wave_sum_n(ss);
-#pragma unroll
-            for (int sg = 0; sg < 2; sg++) {
-              const float rstd = 1.0f / sqrtf(ss[sg] * (1.0f / HD) + EPS);
-              float fa = x[sg][0] * rstd, fb = x[sg][1] * rstd;
-              rbf2(fa, fb);
-              fa *= wa;
-              fb *= wb;
-              rbf2(fa, fb);
-              float p0 = fa * ca, p1 = fb * sa, p2 = fb * cb, p3 = fa * sb;
-              rbf2(p0, p1);
-              rbf2(p2, p3);
-              float ra = p0 - p1, rb = p2 + p3;
-              rbf2(ra, rb);
-              const bool raw = c == 1 && sg == 1;
-              fr[sg][0] = raw ? x[sg][0] : ra;
-              fr[sg][1] = raw ? x[sg][1] : rb;
-            }
-          }
           if (c == 0) {
-#pragma unroll
-            for (int sg = 0; sg < 2; sg++) {
-              s_q[sg * HD + lane] = (uint16_t)f2bf(fr[sg][0]);
-              s_q[sg * HD + 64 + lane] = (uint16_t)f2bf(fr[sg][1]);
-            }
+            const uint32_t w[2] = {lb + LX_QKV + lane, lb + LX_QKV + 64 + lane};
+            uint32_t u[2];
+            poll_words(wsb, ws, w, tag, u);
+            MQ_STAMP(layer * 40 + 15);
+            float ra, rb;
+            qk_norm_rope(u[0], u[1], s_qkn, 0, s_cos, s_sin, lane, ra, rb);
+            s_q[lane] = (uint16_t)f2bf(ra);
+            s_q[64 + lane] = (uint16_t)f2bf(rb);
+          } else {
+            const uint32_t w[4] = {lb + LX_QKV + 2 * HD + lane, lb + LX_QKV + 2 * HD + 64 + lane,
+                                   lb + LX_QKV + 3 * HD + lane, lb + LX_QKV + 3 * HD + 64 + lane};
+            uint32_t u[4];
+            poll_words(wsb, ws, w, tag, u);
+            qk_norm_rope(u[0], u[1], s_qkn, 64, s_cos, s_sin, lane, fr[0][0], fr[0][1]);
+            fr[1][0] = bflo(u[2]);
+            fr[1][1] = bflo(u[3]);
           }
           MQ_STAMP(layer * 40 + 25);
           for (int ps = 0; ps < npass; ps++) {
@@ -1132,6 +1138,16 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         MQ_STAMP(layer * 40 + 28);
         const float hrow = s_hrow[lane];
         if (att) {
+          {
+            // q head 2g + 1: QK-norm and RoPE (the poll waves take q head 2g, k and v)
+            const uint32_t w[2] = {lb + LX_QKV + HD + lane, lb + LX_QKV + HD + 64 + lane};
+            uint32_t u[2];
+            poll_words(wsb, ws, w, tag, u);
+            float ra, rb;
+            qk_norm_rope(u[0], u[1], s_qkn, 0, s_cos, s_sin, lane, ra, rb);
+            s_q[HD + lane] = (uint16_t)f2bf(ra);
+            s_q[HD + 64 + lane] = (uint16_t)f2bf(rb);
+          }
           for (int ps = 0; ps < npass; ps++) {
             const int ncp = pass_rows(ps);
             BAR();  // B1
