@@ -14,8 +14,10 @@
 // The 32 workgroups of an XCD form two groups of 16 that take turns on the critical
 // path of a layer:
 //   group A (members 0..15): input RMSNorm, q/k/v rows 32a .. 32a+31 of the group's
-//     [q0; q1; k; v], the attention (members a < nsplit each attend over one chunk of
-//     the context), o_proj partial sums of rows 64a .. 64a+63 over the group's 256
+//     [q0; q1; k; v], the attention (contexts of at most 256 positions: every member
+//     attends over the whole context, so the output needs no hand-out; longer ones:
+//     members a < nsplit each attend over one chunk), o_proj partial sums of rows
+//     64a .. 64a+63 over the group's 256
 //     columns, and the cross-XCD reduction of those rows into h1;
 //   group B (members 16..31, b = j - 16): post-attention RMSNorm, gate and up rows of
 //     units 384g + 24b .. +23, down_proj partial sums of rows 64b .. 64b+63 over the
@@ -123,7 +125,7 @@ constexpr uint32_t LOCAL_WORDS = 32768;
 constexpr uint32_t LX_H = 0;        // [1024] residual stream after the layer (from B)
 constexpr uint32_t LX_H1 = 1024;    // [1024] residual stream after attention (from A)
 constexpr uint32_t LX_QKV = 2048;   // [512]  raw q0, q1, k, v rows of the XCD's KV group
-constexpr uint32_t LX_ATT = 2560;   // [256]  attention output of the group's two query heads
+constexpr uint32_t LX_ATT = 2560;   // [256]  attention output of the two query heads (split, one chunk)
 constexpr uint32_t LX_M = 2816;     // [384]  SiLU(gate) * up of the XCD's MLP units
 // cue words (a 16-bit tag each): group A member 0 writes LX_CUE_A after its o_proj
 // partials, group B member 0 writes LX_CUE_B after its down_proj partials. The other group
@@ -628,8 +630,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   const int n_ctx = p + 1;
   const int nsplit = SPLIT ? plan_nsplit(n_ctx) : 1;
   const int CH = SPLIT ? plan_chunk(n_ctx) : n_ctx;
-  const bool att = ga && m < nsplit;
-  const int c0 = m * CH;
+  // contexts of at most KV_CAP positions: every group-A workgroup attends over the whole
+  // context (the same result in each), so none needs the attention output handed out;
+  // longer contexts: chunk m on member m < nsplit
+  const bool att = ga && (SPLIT ? m < nsplit : true);
+  const int c0 = SPLIT ? m * CH : 0;  // the unsplit instance: every A workgroup from position 0
   const int nc = att ? min(n_ctx, c0 + CH) - c0 : 0;
   const int npass = SPLIT ? (nc + KV_CAP - 1) / KV_CAP : 1;
   const int nc0 = min(nc, KV_CAP);
@@ -1193,10 +1198,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     BAR();  // P0
     // Every launch writes or clears every exchange word it could ever poll, so that the
     // content a poll can find before the awaited write is at most one launch old, whose
-    // tags differ from the polled ones: a split launch clears the attention-output words
-    // (read by unsplit launches only), and an A workgroup without a chunk partial to store
-    // clears its chunk's record (read by split launches with more chunks).
-    if (SPLIT && ga && m == 0) st4_plain(ws + lb + LX_ATT + 4 * lane, u32x4{0u, 0u, 0u, 0u});
+    // tags differ from the polled ones: a launch that does not write the attention-output
+    // words clears them (only split launches with one chunk write and read them), and an A
+    // workgroup without a chunk partial to store clears its chunk's record (read by split
+    // launches with more chunks).
+    if (ga && m == 0 && !(SPLIT && nsplit == 1)) st4_plain(ws + lb + LX_ATT + 4 * lane, u32x4{0u, 0u, 0u, 0u});
     if (ga && (!SPLIT || !att))
       for (int i = lane; i < 2 * 2 * (int)APART / 4; i += 64)
         st4_plain(ws + lb + LX_PART + 2 * 2 * APART * m + 4 * i, u32x4{0u, 0u, 0u, 0u});
@@ -1215,8 +1221,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           for (int ps = 0; ps < npass; ps++) {
             const int ncp = pass_rows(ps);
             BAR();  // B1
-            if (own_p && ps == npass - 1) {
-              // K/V-cache append at slot p (bf16 [L][8][max_seq][128]): lane -> dims 2 lane, 2 lane + 1
+            if (own_p && (SPLIT || m == 0) && ps == npass - 1) {
+              // K/V-cache append (one workgroup per XCD) at slot p (bf16 [L][8][max_seq][128]): lane -> dims 2 lane, 2 lane + 1
               const size_t slot = ((size_t)(layer * NKV + g) * P.max_seq_len + p) * HD;
               const uint32_t k2 = *reinterpret_cast<const uint32_t*>(s_kv + kv_off(prow, lane >> 2) + 4 * (lane & 3));
               const uint32_t v2 =
@@ -1261,9 +1267,12 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           }
           const int hh = lane >> 5, dim = 4 * (lane & 31);
           if (nsplit == 1) {
-            st4_plain(ws + lb + LX_ATT + hh * HD + dim,
-                      u32x4{tagged(tag, rbf(s_ao[hh][dim])), tagged(tag, rbf(s_ao[hh][dim + 1])),
-                            tagged(tag, rbf(s_ao[hh][dim + 2])), tagged(tag, rbf(s_ao[hh][dim + 3]))});
+            // split instance, one chunk: the other group-A workgroups gather it (in the
+            // unsplit instance every group-A workgroup has attended itself)
+            if (SPLIT)
+              st4_plain(ws + lb + LX_ATT + hh * HD + dim,
+                        u32x4{tagged(tag, rbf(s_ao[hh][dim])), tagged(tag, rbf(s_ao[hh][dim + 1])),
+                              tagged(tag, rbf(s_ao[hh][dim + 2])), tagged(tag, rbf(s_ao[hh][dim + 3]))});
           } else {
             // chunk partial (m, l, unnormalised acc) as (fp32, tag) pairs; every A workgroup of
             // the XCD merges them

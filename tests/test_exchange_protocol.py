@@ -41,15 +41,15 @@ def tag32(epoch, layer_plus_one):
 
 
 # Region -> (tag kind, who writes it). "every": every launch writes it at every layer;
-# "unsplit"/"split": only launches of that instance write it at every layer, the others
-# clear it (tag 0) at their start; "chunks": chunk j is written at every layer by split
+# "split1": only split launches with one attention chunk write it at every layer (the other
+# group-A workgroups read it there), every other launch clears it (tag 0) at its start; "chunks": chunk j is written at every layer by split
 # launches with j < nsplit, and cleared at the start of every launch that does not write it.
 # LX_H and LX_CUE_B are written by group B (h and its cue), LX_H1, LX_QKV, LX_ATT,
 # LX_PART and LX_CUE_A by group A, LX_M by group B; the cross-XCD arrays by both.
 REGIONS = {
     "LX_H": ("16", "every"), "LX_H1": ("16", "every"), "LX_QKV": ("16", "every"), "LX_M": ("16", "every"),
     "LX_CUE_A": ("16", "every"), "LX_CUE_B": ("16", "every"),
-    "LX_ATT": ("16", "unsplit"),
+    "LX_ATT": ("16", "split1"),
     "X_OPART": ("32", "every"), "X_DPART": ("32", "every"),
     "LX_PART": ("32", "chunks"),
 }
@@ -122,7 +122,7 @@ def _alias_distance_if_not_cleared(region, l_read, l_prev):
 
 
 def test_clears_are_needed_for_the_regions_only_some_launches_write():
-    """Without the clears, LX_ATT (written by unsplit launches only) would alias after
+    """Without the clears, LX_ATT (written by one-chunk split launches only) would alias after
     55296 launches that skip it, and LX_PART after 2^27: the model shows why a launch that
     does not write those regions clears them."""
     assert _alias_distance_if_not_cleared("LX_ATT", 0, 27) == 55296
