@@ -316,23 +316,27 @@ __device__ __forceinline__ void attn_scores(const uint8_t* s_kv, const uint16_t*
     acc[0] = mfma_16x16x32(ka[0][s4], qb[s4], acc[0]);
     acc[1] = mfma_16x16x32(ka[1][s4], qb[s4], acc[1]);
   }
-  // lane (column r16 = head, rows 4kg + e)
+  // lane (column r16 = head, rows 4kg + e): one 16-byte write of its four scores per block
 #pragma unroll
-  for (int bi = 0; bi < 2; bi++)
+  for (int bi = 0; bi < 2; bi++) {
+    const int r = 16 * (v + 8 * bi) + 4 * kg;
+    f32x4 val;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      const int r = 16 * (v + 8 * bi) + 4 * kg + e;
-      const float val = r < nc ? acc[bi][e] * scale : -INFINITY;
-      if (r16 < 2) s_sc[r16][r] = val;
-      mx = fmaxf(mx, val);
+      val[e] = r + e < nc ? acc[bi][e] * scale : -INFINITY;
+      mx = fmaxf(mx, val[e]);
     }
-  // per-head maximum over the lanes of column 0 (head 0) and column 1 (head 1)
-  const float m0 = fmaxf(fmaxf(readlane(mx, 0), readlane(mx, 16)), fmaxf(readlane(mx, 32), readlane(mx, 48)));
-  const float m1 = fmaxf(fmaxf(readlane(mx, 1), readlane(mx, 17)), fmaxf(readlane(mx, 33), readlane(mx, 49)));
-  if (lane == 0) {
-    s_mx[v][0] = m0;
-    s_mx[v][1] = m1;
+    if (r16 < 2) *reinterpret_cast<f32x4*>(&s_sc[r16][r]) = val;
   }
+  // per-head maximum over the lanes of column 0 (head 0) and column 1 (head 1): lane groups
+  // kg meet through permlane swaps; lanes 0 and 1 hold the two heads' maxima
+  {
+    const auto a2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = fmaxf(__uint_as_float(a2[0]), __uint_as_float(a2[1]));
+    const auto b2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = fmaxf(__uint_as_float(b2[0]), __uint_as_float(b2[1]));
+  }
+  if (lane < 2) s_mx[v][lane] = mx;
 }
 
 // Softmax numerators of this wave's 32 rows (blocks v and v + 8) for both heads:
@@ -351,12 +355,14 @@ __device__ __forceinline__ void attn_softmax(const float (*s_sc)[KV_CAP], uint16
   const int h = lane >> 5, r = 16 * (v + 8 * ((lane >> 4) & 1)) + (lane & 15);
   const float e = r < nc ? expf(s_sc[h][r] - (h ? M1 : M0)) : 0.f;
   s_p[h * KV_CAP + r] = (uint16_t)f2bf(e);
-  const float t = row16_sum(e);
-  const float l0 = readlane(t, 0) + readlane(t, 16), l1 = readlane(t, 32) + readlane(t, 48);
-  if (lane == 0) {
-    s_l[v][0] = l0;
-    s_l[v][1] = l1;
+  // rows 0 + 1 (head 0) and 2 + 3 (head 1) of the 16-lane sums, as readlane pairs would add
+  // them; lanes 0 and 32 hold the two heads' sums
+  float t = row16_sum(e);
+  {
+    const auto b2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(t), __float_as_uint(t), false, false);
+    t = __uint_as_float(b2[0]) + __uint_as_float(b2[1]);
   }
+  if ((lane & 31) == 0) s_l[v][lane >> 5] = t;
 }
 
 // acc[h][d] = sum_r bf16(p_h[r]) * v_r[d] for this wave's 16 dims d = 16v + (lane & 15)
@@ -378,10 +384,12 @@ __device__ __forceinline__ void attn_pv(const uint8_t* s_kv, const uint16_t* s_p
   // always lie in the LDS copy and hold finite values)
   const int nb = (nc + 31) >> 5;
   f32x4 acc2[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  for (int t0 = 0; t0 < nb; t0 += 2) {
-    u32x4 pa[2], vb[2];
+  // four blocks a trip (all their LDS reads issued together), block t0 + bi into
+  // accumulator bi % 2 as in a two-block loop; blocks past nb have p = 0
+  for (int t0 = 0; t0 < nb; t0 += 4) {
+    u32x4 pa[4], vb[4];
 #pragma unroll
-    for (int bi = 0; bi < 2; bi++) {
+    for (int bi = 0; bi < 4; bi++) {
       const int rr = 32 * (t0 + bi) + 8 * kg;
       const u32x4 pt = *reinterpret_cast<const u32x4*>(s_p + (r16 & 1) * KV_CAP + rr);
       pa[bi] = r16 < 2 ? pt : u32x4{0u, 0u, 0u, 0u};
@@ -395,6 +403,8 @@ __device__ __forceinline__ void attn_pv(const uint8_t* s_kv, const uint16_t* s_p
     }
     acc2[0] = mfma_16x16x32(pa[0], vb[0], acc2[0]);
     acc2[1] = mfma_16x16x32(pa[1], vb[1], acc2[1]);
+    acc2[0] = mfma_16x16x32(pa[2], vb[2], acc2[0]);
+    acc2[1] = mfma_16x16x32(pa[3], vb[3], acc2[1]);
   }
   const f32x4 acc = acc2[0] + acc2[1];
   L0 = 0.f;
@@ -565,7 +575,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ float s_cos[HD], s_sin[HD];
   __shared__ __align__(16) uint16_t s_q[2 * HD];      // normed, rotated q of the two heads
   __shared__ __align__(16) uint16_t s_p[2 * KV_CAP];  // bf16 softmax numerators
-  __shared__ float s_sc[2][KV_CAP];                    // attention scores
+  __shared__ __align__(16) float s_sc[2][KV_CAP];      // attention scores
   __shared__ float s_ao[2][HD];                        // attention output (or unnormalised partial)
   __shared__ float s_ao1[2][HD];                       // a later LDS pass's unnormalised partial
   __shared__ float s_mx[8][2], s_l[8][2];              // per-wave score maxima and softmax sums
