@@ -748,6 +748,16 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
               kv_dma(P, layer, g, c0 + KV_CAP * ps, pass_rows(ps), p, lds_kv, s, lane);
               wait_vmem();
             }
+            if (s == 0 && own_p && ps == npass - 1) {
+              // the new v row (the raw bf16 values; no loads of this wave are in flight)
+              const uint32_t w[2] = {lb + LX_QKV + 3 * HD + lane, lb + LX_QKV + 3 * HD + 64 + lane};
+              uint32_t u[2];
+              poll_words(wsb, ws, w, tag_of(epoch, layer), u);
+              uint8_t* vbase = s_kv + KV_CAP * 256;
+              *reinterpret_cast<uint16_t*>(vbase + kv_off(prow, lane >> 3) + 2 * (lane & 7)) = (uint16_t)(u[0] & 0xffffu);
+              *reinterpret_cast<uint16_t*>(vbase + kv_off(prow, 8 + (lane >> 3)) + 2 * (lane & 7)) =
+                  (uint16_t)(u[1] & 0xffffu);
+            }
             const int ncp = pass_rows(ps);
             BAR();  // B1: q, the new k/v row and the K/V rows are in LDS
             MQ_STAMP(layer * 40 + 2);
@@ -961,9 +971,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         MQ_STAMP(layer * 40 + 14);
         if (att) {
           // ---------------- QK-norm, RoPE, K/V row p, attention
-          // poll wave 0: q head 2g; poll wave 1: k and v; the reduce wave: q head 2g + 1
+          // poll wave 0: q head 2g; poll wave 1: k; the reduce wave: q head 2g + 1; stream
+          // wave 0: v
           // (lane holds dims lane, lane + 64)
-          float fr[2][2];
+          float fr[1][2];
           if (c == 0) {
             const uint32_t w[2] = {lb + LX_QKV + lane, lb + LX_QKV + 64 + lane};
             uint32_t u[2];
@@ -974,27 +985,21 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             s_q[lane] = (uint16_t)f2bf(ra);
             s_q[64 + lane] = (uint16_t)f2bf(rb);
           } else {
-            const uint32_t w[4] = {lb + LX_QKV + 2 * HD + lane, lb + LX_QKV + 2 * HD + 64 + lane,
-                                   lb + LX_QKV + 3 * HD + lane, lb + LX_QKV + 3 * HD + 64 + lane};
-            uint32_t u[4];
+            const uint32_t w[2] = {lb + LX_QKV + 2 * HD + lane, lb + LX_QKV + 2 * HD + 64 + lane};
+            uint32_t u[2];
             poll_words(wsb, ws, w, tag, u);
             qk_norm_rope(u[0], u[1], s_qkn, 64, s_cos, s_sin, lane, fr[0][0], fr[0][1]);
-            fr[1][0] = bflo(u[2]);
-            fr[1][1] = bflo(u[3]);
           }
           MQ_STAMP(layer * 40 + 25);
           for (int ps = 0; ps < npass; ps++) {
             if (c == 1 && own_p && ps == npass - 1) {
-              // the new k and v rows into the LDS copy of the pass that holds position p (the
-              // store wave appends them to the cache); the passes' copies exclude that row
+              // the new k row into the LDS copy of the pass that holds position p (stream wave
+              // 0 writes the v row; the store wave appends both to the cache); the passes'
+              // copies exclude that row
               const int o0 = kv_off(prow, lane >> 3) + 2 * (lane & 7);
               const int o1 = kv_off(prow, 8 + (lane >> 3)) + 2 * (lane & 7);
-#pragma unroll
-              for (int sg = 0; sg < 2; sg++) {
-                uint8_t* base = s_kv + sg * (KV_CAP * 256);
-                *reinterpret_cast<uint16_t*>(base + o0) = (uint16_t)f2bf(fr[sg][0]);
-                *reinterpret_cast<uint16_t*>(base + o1) = (uint16_t)f2bf(fr[sg][1]);
-              }
+              *reinterpret_cast<uint16_t*>(s_kv + o0) = (uint16_t)f2bf(fr[0][0]);
+              *reinterpret_cast<uint16_t*>(s_kv + o1) = (uint16_t)f2bf(fr[0][1]);
             }
             const int ncp = pass_rows(ps);
             BAR();  // B1
