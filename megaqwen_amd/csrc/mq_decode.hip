@@ -234,6 +234,11 @@ __device__ __forceinline__ uint32_t ldl1(const Buf& b, uint32_t word) {
 // K/V rows of a chunk live in LDS as [row][16 chunks of 8 dims], chunk c of row r
 // stored in slot c ^ (r & 15) so that 16 rows read at one chunk hit distinct banks.
 __device__ __forceinline__ uint32_t kv_off(int row, int chunk) { return row * 256 + 16 * (chunk ^ (row & 15)); }
+// V rows use their own swizzle, chunk c of row r in slot c ^ vsw(r): P.V's transpose reads
+// take 16 rows (8 kg + i of a 32-row block, i < 4) by one 32-byte chunk pair each, and vsw
+// (bits 1..3 = r % 4 and bit 3 of r) spreads those 16 rows evenly over the 8 pair slots.
+__device__ __forceinline__ int vsw(int row) { return 2 * ((row & 3) | (((row >> 3) & 1) << 2)); }
+__device__ __forceinline__ uint32_t vkv_off(int row, int chunk) { return row * 256 + 16 * (chunk ^ vsw(row)); }
 
 // Stream wave s copies K and V rows [0, nc) of the chunk starting at position c0
 // (except position p, which the layer itself produces) into LDS.
@@ -247,9 +252,8 @@ __device__ __forceinline__ void kv_dma(const DecodeParams& P, int layer, int g, 
   for (int q = s; q < nq; q += NSW) {
     const int row = 4 * q + rin;
     if (row < nc && c0 + row != p) {
-      const int chunk = slot ^ (row & 15);
-      dma16(kb + row * HD + 8 * chunk, lds + q * 1024);
-      dma16(vb + row * HD + 8 * chunk, lds + KV_CAP * 256 + q * 1024);
+      dma16(kb + row * HD + 8 * (slot ^ (row & 15)), lds + q * 1024);
+      dma16(vb + row * HD + 8 * (slot ^ vsw(row)), lds + KV_CAP * 256 + q * 1024);
     }
   }
 }
@@ -395,9 +399,9 @@ __device__ __forceinline__ void attn_pv(const uint8_t* s_kv, const uint16_t* s_p
       pa[bi] = r16 < 2 ? pt : u32x4{0u, 0u, 0u, 0u};
       const int ra = rr + (r16 >> 2), rb = ra + 4;
       const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_v4s*)(uintptr_t)(vb0 + kv_off(ra, dq >> 3) + 2 * (dq & 7)));
+          (lds_v4s*)(uintptr_t)(vb0 + vkv_off(ra, dq >> 3) + 2 * (dq & 7)));
       const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_v4s*)(uintptr_t)(vb0 + kv_off(rb, dq >> 3) + 2 * (dq & 7)));
+          (lds_v4s*)(uintptr_t)(vb0 + vkv_off(rb, dq >> 3) + 2 * (dq & 7)));
       const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
       vb[bi] = u32x4{l2.x, l2.y, h2.x, h2.y};
     }
@@ -754,8 +758,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
               uint32_t u[2];
               poll_words(wsb, ws, w, tag_of(epoch, layer), u);
               uint8_t* vbase = s_kv + KV_CAP * 256;
-              *reinterpret_cast<uint16_t*>(vbase + kv_off(prow, lane >> 3) + 2 * (lane & 7)) = (uint16_t)(u[0] & 0xffffu);
-              *reinterpret_cast<uint16_t*>(vbase + kv_off(prow, 8 + (lane >> 3)) + 2 * (lane & 7)) =
+              *reinterpret_cast<uint16_t*>(vbase + vkv_off(prow, lane >> 3) + 2 * (lane & 7)) = (uint16_t)(u[0] & 0xffffu);
+              *reinterpret_cast<uint16_t*>(vbase + vkv_off(prow, 8 + (lane >> 3)) + 2 * (lane & 7)) =
                   (uint16_t)(u[1] & 0xffffu);
             }
             const int ncp = pass_rows(ps);
@@ -1241,7 +1245,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
               const size_t slot = ((size_t)(layer * NKV + g) * P.max_seq_len + p) * HD;
               const uint32_t k2 = *reinterpret_cast<const uint32_t*>(s_kv + kv_off(prow, lane >> 2) + 4 * (lane & 3));
               const uint32_t v2 =
-                  *reinterpret_cast<const uint32_t*>(s_kv + KV_CAP * 256 + kv_off(prow, lane >> 2) + 4 * (lane & 3));
+                  *reinterpret_cast<const uint32_t*>(s_kv + KV_CAP * 256 + vkv_off(prow, lane >> 2) + 4 * (lane & 3));
               st1_plain(reinterpret_cast<uint32_t*>(P.k_cache + slot) + lane, k2);
               st1_plain(reinterpret_cast<uint32_t*>(P.v_cache + slot) + lane, v2);
             }
