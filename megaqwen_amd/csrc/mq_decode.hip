@@ -241,8 +241,9 @@ __device__ __forceinline__ int vsw(int row) { return 2 * ((row & 3) | (((row >> 
 __device__ __forceinline__ uint32_t vkv_off(int row, int chunk) { return row * 256 + 16 * (chunk ^ vsw(row)); }
 
 // Stream wave s copies K and V rows [0, nc) of the chunk starting at position c0
-// (except position p, which the layer itself produces) into LDS.
-__device__ __forceinline__ void kv_dma(const DecodeParams& P, int layer, int g, int c0, int nc, int p, uint32_t lds,
+// (except position p, which the layer itself produces) into LDS; nt picks the
+// non-temporal cache policy.
+__device__ __forceinline__ void kv_dma(bool nt, const DecodeParams& P, int layer, int g, int c0, int nc, int p, uint32_t lds,
                                        int s, int lane) {
   const size_t base = ((size_t)(layer * NKV + g) * P.max_seq_len + c0) * HD;
   const uint16_t* kb = P.k_cache + base;
@@ -252,8 +253,13 @@ __device__ __forceinline__ void kv_dma(const DecodeParams& P, int layer, int g, 
   for (int q = s; q < nq; q += NSW) {
     const int row = 4 * q + rin;
     if (row < nc && c0 + row != p) {
-      dma16(kb + row * HD + 8 * (slot ^ (row & 15)), lds + q * 1024);
-      dma16(vb + row * HD + 8 * (slot ^ vsw(row)), lds + KV_CAP * 256 + q * 1024);
+      if (nt) {
+        dma16_nt(kb + row * HD + 8 * (slot ^ (row & 15)), lds + q * 1024);
+        dma16_nt(vb + row * HD + 8 * (slot ^ vsw(row)), lds + KV_CAP * 256 + q * 1024);
+      } else {
+        dma16(kb + row * HD + 8 * (slot ^ (row & 15)), lds + q * 1024);
+        dma16(vb + row * HD + 8 * (slot ^ vsw(row)), lds + KV_CAP * 256 + q * 1024);
+      }
     }
   }
 }
@@ -652,6 +658,9 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   const int nc = att ? min(n_ctx, c0 + CH) - c0 : 0;
   const int npass = SPLIT ? (nc + KV_CAP - 1) / KV_CAP : 1;
   const int nc0 = min(nc, KV_CAP);
+  // K/V rows by non-temporal copies where that measured faster: the unsplit instance and
+  // chunks of several passes (one-pass chunks of 257..4096-position contexts lose 1-9 us)
+  const bool kv_nt = !SPLIT || npass > 1;
   const bool own_p = att && p >= c0 && p < c0 + nc;  // p is always in the last pass
   const int prow = p - c0 - KV_CAP * (npass - 1);     // its LDS row there
   const uint32_t lds_kv = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)s_kv;
@@ -722,7 +731,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       load_a(0);
       load_o(0);
       put_norms();
-      if (att) kv_dma(P, 0, g, c0, nc0, p, lds_kv, s, lane);
+      if (att) kv_dma(kv_nt, P, 0, g, c0, nc0, p, lds_kv, s, lane);
       BAR();  // P0
       for (int layer = 0; layer < L; layer++) {
         // ---------------- q/k/v rows 32m + 8s .. +7 of the group's [q0; q1; k; v]
@@ -749,7 +758,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           for (int ps = 0; ps < npass; ps++) {
             if (ps > 0) {
               // rows KV_CAP * ps .. of the chunk replace the previous pass's rows
-              kv_dma(P, layer, g, c0 + KV_CAP * ps, pass_rows(ps), p, lds_kv, s, lane);
+              kv_dma(kv_nt, P, layer, g, c0 + KV_CAP * ps, pass_rows(ps), p, lds_kv, s, lane);
               wait_vmem();
             }
             if (s == 0 && own_p && ps == npass - 1) {
@@ -801,7 +810,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           load_a(layer + 1);
           load_o(layer + 1);
           put_norms();
-          if (att) kv_dma(P, layer + 1, g, c0, nc0, p, lds_kv, s, lane);
+          if (att) kv_dma(kv_nt, P, layer + 1, g, c0, nc0, p, lds_kv, s, lane);
           MQ_STAMP(layer * 40 + 10);
         }
       }
