@@ -731,8 +731,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       load_a(0);
       load_o(0);
       put_norms();
-      if (att) kv_dma(kv_nt, P, 0, g, c0, nc0, p, lds_kv, s, lane);
       BAR();  // P0
+      if (att) kv_dma(kv_nt, P, 0, g, c0, nc0, p, lds_kv, s, lane);
       for (int layer = 0; layer < L; layer++) {
         // ---------------- q/k/v rows 32m + 8s .. +7 of the group's [q0; q1; k; v]
         BAR();  // A1: normed h in s_x0
@@ -913,6 +913,14 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   } else if (wave < NSW + NPW) {
     // ==================================================================== poll waves
     const int c = wave - NSW, pt = tid - NSW * 64;  // pt: poll thread 0..127
+    // group A's layer-0 residual stream (the embedding row, or the hidden input), loaded
+    // before the prologue so that its latency overlaps the pointer table's and the norms'
+    u32x2 emb[4];
+    if (ga) {
+      const uint16_t* src = (P.mode & MODE_INPUT_HIDDEN) ? P.hidden_in : P.embed + (size_t)token * H;
+#pragma unroll
+      for (int k = 0; k < 4; k++) emb[k] = ldw2(src + 4 * (lane + 64 * k));
+    }
     for (int i = pt; i < 2 * HD; i += NPW * 64) {
       if (i < HD) s_cos[i] = bf2f(ldraw16(P.cos_tab + (size_t)p * HD + i));
       else s_sin[i - HD] = bf2f(ldraw16(P.sin_tab + (size_t)p * HD + i - HD));
@@ -957,11 +965,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         // ---------------- gather h (each poll wave its half, with the sum of squares), RMSNorm
         float ss;
         if (layer == 0) {
-          const uint16_t* src = (P.mode & MODE_INPUT_HIDDEN) ? P.hidden_in : P.embed + (size_t)token * H;
           ss = 0.f;
 #pragma unroll
           for (int k = 0; k < 4; k++) {
-            const u32x2 v = ldw2(src + 4 * (lane + 64 * k));
+            const u32x2 v = emb[k];
             // widen the raw bf16 values to the tagged layout so every layer reads hv alike
             const u32x4 t = u32x4{v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16};
             if (k == 2 * c) hv0 = t;
