@@ -25,8 +25,8 @@
 // While one group works, the other streams its next layer's weights into registers
 // (and the attention workgroups their next K/V rows into LDS): a CU's loads and its
 // exchange polls complete in order, so a group only ever polls with no weight load
-// in flight. Group B holds its burst until group A has published the next layer's
-// q/k/v, which moves it off the hand-overs that precede the attention.
+// in flight. Each group issues its burst as soon as its reduce wave has stored its
+// rows, so that the burst has landed before the other group's cross-XCD reduction.
 //
 // Every workgroup runs four roles, one per wave kind:
 //   * stream waves 0-3 hold the group's weight slice in registers and compute the
@@ -44,8 +44,10 @@
 // Exchanges use "tagged words": a bf16 value in the low half of a 32-bit word
 // and a 16-bit tag (launch epoch x 32 + layer) in the high half, or an fp32
 // value with a 32-bit tag in a 64-bit word. A consumer issues all its loads at
-// once and re-polls only stale words, so an exchange costs one memory round
-// trip. Across XCDs both sides use device-scope (sc1) accesses; inside an XCD
+// once, keeps two such poll rounds in flight (half a round trip apart) and keeps
+// each word from the first round that returns it with the expected tag, so an
+// exchange costs about one memory round trip after the producer's store. Across
+// XCDs both sides use device-scope (sc1) accesses; inside an XCD
 // producers use plain stores and consumers non-temporal loads, served by the
 // XCD's shared L2. A watchdog bounds every poll and turns a lost producer into an
 // error code instead of a hang.
@@ -75,6 +77,14 @@
 #endif
 #ifndef MQ_STAMP_DUMP
 #define MQ_STAMP_DUMP() ((void)0)
+#endif
+// MQ_STAMP_AFTER(slot, v) stamps once the value v is available (a load has returned).
+#ifndef MQ_STAMP_AFTER
+#define MQ_STAMP_AFTER(i, v) ((void)0)
+#endif
+// MQ_LANDED(slot) stamps once the wave's outstanding loads have landed (a tracing build only)
+#ifndef MQ_LANDED
+#define MQ_LANDED(i) ((void)0)
 #endif
 
 namespace mq {
@@ -144,6 +154,11 @@ constexpr size_t WS_BYTES = ((WS_WORDS * 4 + 4 + 65535) / 65536) * 65536;
 static_assert(LX_PART + 2 * NGA * 2 * APART <= LOCAL_WORDS, "per-XCD region overflow");
 
 constexpr uint32_t POLL_LIMIT = 1u << 21;  // ~1 s of polling before the watchdog fires
+// Exchange polls keep two rounds of loads in flight, the second issued this many s_sleep
+// units (64 clocks each) after the first; a poll round then returns about every half round
+// trip instead of every round trip, which shortens the time from a producer's store to the
+// consumer seeing it.
+constexpr int POLL_STAGGER = 4;
 constexpr uint32_t ERR_POLL = 1u;
 constexpr uint32_t ERR_XCD = 2u;  // a workgroup ran on an XCD numbered 8 or above
 constexpr uint32_t ERR_STEP = 4u;  // a device-resident step found an invalid token, position or count
@@ -229,6 +244,43 @@ __device__ __forceinline__ u32x4 repoll_l4(const Buf& b, uint32_t* ws, uint32_t 
 }
 __device__ __forceinline__ uint32_t ldl1(const Buf& b, uint32_t word) {
   return __builtin_amdgcn_raw_buffer_load_b32(b.r, word * 4u, 0, NT_LD);
+}
+// One 16-byte chunk of tagged words with two poll rounds in flight (as in reduce_row8).
+__device__ __forceinline__ u32x4 poll2_l4(const Buf& b, uint32_t* ws, uint32_t word, uint32_t tag) {
+  u32x4 r[2], v = u32x4{0u, 0u, 0u, 0u};
+  bool have = false;
+  r[0] = ldl4(b, word);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_sleep(POLL_STAGGER);
+  r[1] = ldl4(b, word);
+  asm volatile("" ::: "memory");
+  auto merge = [&](const u32x4& x) {
+    if (!have && tags_ok(x, tag)) {
+      v = x;
+      have = true;
+    }
+    return __all(have);
+  };
+#define MQ_MSTEP(k)                   \
+  if (merge(r[(k) % 2])) return v;    \
+  r[(k) % 2] = ldl4(b, word);         \
+  asm volatile("" ::: "memory");
+  MQ_MSTEP(0) MQ_MSTEP(1) MQ_MSTEP(2) MQ_MSTEP(3) MQ_MSTEP(4) MQ_MSTEP(5)
+  MQ_MSTEP(6) MQ_MSTEP(7) MQ_MSTEP(8) MQ_MSTEP(9) MQ_MSTEP(10) MQ_MSTEP(11)
+#undef MQ_MSTEP
+  merge(r[0]);
+  merge(r[1]);
+  uint32_t spins = 0;
+  while (!have) {
+    if (watchdog(b, ws, ++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+    const u32x4 x = ldl4(b, word);
+    if (tags_ok(x, tag)) {
+      v = x;
+      have = true;
+    }
+  }
+  return v;
 }
 
 // K/V rows of a chunk live in LDS as [row][16 chunks of 8 dims], chunk c of row r
@@ -468,16 +520,65 @@ __device__ __forceinline__ void wait_cue(const Buf& b, uint32_t* ws, uint32_t wo
 // order (half 0 first), so both waves' norms agree bit for bit. `target` is the number
 // of half sums the LDS counter holds once this exchange is complete.
 __device__ __forceinline__ float gather_half(const Buf& b, uint32_t* ws, uint32_t base, uint32_t tag, int c, int lane,
-                                             u32x4& v0, u32x4& v1, float* s_ssx, uint32_t* s_ssn, uint32_t target) {
+                                             u32x4& v0, u32x4& v1, float* s_ssx, uint32_t* s_ssn, uint32_t target,
+                                             int sk = 0) {
   const uint32_t w0 = base + 4 * (lane + 128 * c), w1 = w0 + 4 * 64;
-  u32x4 a = ldl4(b, w0), e = ldl4(b, w1);
-  uint32_t spins = 0;
-  while (!(tags_ok(a, tag) & tags_ok(e, tag))) {
-    if (watchdog(b, ws, ++spins)) break;
-    __builtin_amdgcn_s_sleep(1);
-    if (!tags_ok(a, tag)) a = ldl4(b, w0);
-    if (!tags_ok(e, tag)) e = ldl4(b, w1);
+  // two poll rounds in flight (as in reduce_row8): round k % 2 is checked while the other
+  // is outstanding, then re-issued; a chunk is kept once a round returns it with the tag
+  u32x4 a = u32x4{0u, 0u, 0u, 0u}, e = a;
+  bool ha = false, he = false;
+  u32x4 ra[2], re[2];
+  ra[0] = ldl4(b, w0);
+  re[0] = ldl4(b, w1);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_sleep(POLL_STAGGER);
+  ra[1] = ldl4(b, w0);
+  re[1] = ldl4(b, w1);
+  asm volatile("" ::: "memory");
+  MQ_STAMP_AFTER(sk, ra[0].x + re[0].x);
+  auto merge = [&](const u32x4& x0, const u32x4& x1) {
+    if (!ha && tags_ok(x0, tag)) {
+      a = x0;
+      ha = true;
+    }
+    if (!he && tags_ok(x1, tag)) {
+      e = x1;
+      he = true;
+    }
+    return __all(ha & he);
+  };
+#define MQ_GSTEP(k)                                  \
+  if (merge(ra[(k) % 2], re[(k) % 2])) goto gathered; \
+  ra[(k) % 2] = ldl4(b, w0);                         \
+  re[(k) % 2] = ldl4(b, w1);                         \
+  asm volatile("" ::: "memory");
+  MQ_GSTEP(0) MQ_GSTEP(1) MQ_GSTEP(2) MQ_GSTEP(3) MQ_GSTEP(4) MQ_GSTEP(5)
+  MQ_GSTEP(6) MQ_GSTEP(7) MQ_GSTEP(8) MQ_GSTEP(9) MQ_GSTEP(10) MQ_GSTEP(11)
+#undef MQ_GSTEP
+  merge(ra[0], re[0]);
+  merge(ra[1], re[1]);
+  {
+    uint32_t spins = 0;
+    while (!(ha & he)) {
+      if (watchdog(b, ws, ++spins)) break;
+      __builtin_amdgcn_s_sleep(1);
+      if (!ha) {
+        const u32x4 v = ldl4(b, w0);
+        if (tags_ok(v, tag)) {
+          a = v;
+          ha = true;
+        }
+      }
+      if (!he) {
+        const u32x4 v = ldl4(b, w1);
+        if (tags_ok(v, tag)) {
+          e = v;
+          he = true;
+        }
+      }
+    }
   }
+gathered:
   v0 = a;
   v1 = e;
   float fa[4], fe[4];
@@ -510,27 +611,136 @@ __device__ __forceinline__ float reduce_row8(const Buf& wsb, uint32_t* ws, uint3
   auto ok = [&](const u32x2& v) { return v.y == tag64; };
   uint32_t spins = 0;
   u32x2 q[NXCD];
+  // Two poll rounds in flight: the older round is checked while the other is still
+  // outstanding, then re-issued; a pair is kept once a round returns it with the expected
+  // tag. The rounds are unrolled (no loop-carried loads, so the compiler's waits stay exact),
+  // the compiler barriers keep each round's loads where they are issued, and the exit tests
+  // are wave-uniform; past the unrolled rounds the single-round loop takes over.
+  constexpr int NR = 2;
+  u32x2 r[NR][NXCD];
+  bool have[NXCD];
 #pragma unroll
-  for (int x = 0; x < NXCD; x++) q[x] = wsb.ld2((wd + 2 * ROWS * x) * 4u);
-  // re-poll the stale XCDs' pairs together (one round trip per iteration)
-  for (;;) {
+  for (int x = 0; x < NXCD; x++) {
+    have[x] = false;
+    q[x] = u32x2{0u, 0u};
+  }
+#pragma unroll
+  for (int k = 0; k < NR; k++) {
+    if (k) __builtin_amdgcn_s_sleep(POLL_STAGGER);
+#pragma unroll
+    for (int x = 0; x < NXCD; x++) r[k][x] = wsb.ld2((wd + 2 * ROWS * x) * 4u);
+    asm volatile("" ::: "memory");
+  }
+  auto merge = [&](const u32x2 (&v)[NXCD]) {
     bool all = true;
 #pragma unroll
-    for (int x = 0; x < NXCD; x++) all &= ok(q[x]);
-    if (all || watchdog(wsb, ws, ++spins)) break;
-    __builtin_amdgcn_s_sleep(1);
+    for (int x = 0; x < NXCD; x++) {
+      if (!have[x] && ok(v[x])) {
+        q[x] = v[x];
+        have[x] = true;
+      }
+      all &= have[x];
+    }
+    return __all(all);
+  };
+  auto reissue = [&](u32x2 (&v)[NXCD]) {
 #pragma unroll
-    for (int x = 0; x < NXCD; x++)
-      if (!ok(q[x])) q[x] = wsb.ld2((wd + 2 * ROWS * x) * 4u);
+    for (int x = 0; x < NXCD; x++) v[x] = wsb.ld2((wd + 2 * ROWS * x) * 4u);
+    asm volatile("" ::: "memory");
+  };
+  // the oldest round is r[k % NR] at step k
+#define MQ_RSTEP(k)                          \
+  if (merge(r[(k) % NR])) goto reduced;      \
+  reissue(r[(k) % NR]);
+  MQ_RSTEP(0) MQ_RSTEP(1) MQ_RSTEP(2) MQ_RSTEP(3) MQ_RSTEP(4) MQ_RSTEP(5)
+  MQ_RSTEP(6) MQ_RSTEP(7) MQ_RSTEP(8) MQ_RSTEP(9) MQ_RSTEP(10) MQ_RSTEP(11)
+#undef MQ_RSTEP
+  {
+    // the pairs not yet kept, one round at a time
+#pragma unroll
+    for (int k = 0; k < NR; k++) merge(r[k]);
+    for (;;) {
+      bool all = true;
+#pragma unroll
+      for (int x = 0; x < NXCD; x++) all &= have[x];
+      if (all || watchdog(wsb, ws, ++spins)) break;
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int x = 0; x < NXCD; x++)
+        if (!have[x]) {
+          const u32x2 v = wsb.ld2((wd + 2 * ROWS * x) * 4u);
+          if (ok(v)) {
+            q[x] = v;
+            have[x] = true;
+          }
+        }
+    }
   }
+reduced:
   auto f = [&](int x) { return __uint_as_float(q[x].x); };
   return ((f(0) + f(1)) + (f(2) + f(3))) + ((f(4) + f(5)) + (f(6) + f(7)));
 }
 
 // Polls N tagged words (word w[i] + lane) of the XCD's exchange region until all carry `tag`.
-template <int N>
+template <bool PIPE, int N>
 __device__ __forceinline__ void poll_words(const Buf& wsb, uint32_t* ws, const uint32_t (&w)[N], uint32_t tag,
                                            uint32_t (&u)[N]) {
+  if (PIPE) {
+  // two poll rounds in flight (as in reduce_row8)
+  uint32_t r[2][N];
+  bool have[N];
+#pragma unroll
+  for (int i = 0; i < N; i++) {
+    have[i] = false;
+    u[i] = 0u;
+    r[0][i] = ldl1(wsb, w[i]);
+  }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_sleep(POLL_STAGGER);
+#pragma unroll
+  for (int i = 0; i < N; i++) r[1][i] = ldl1(wsb, w[i]);
+  asm volatile("" ::: "memory");
+  auto merge = [&](const uint32_t (&v)[N]) {
+    bool all = true;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+      if (!have[i] && (v[i] >> 16) == tag) {
+        u[i] = v[i];
+        have[i] = true;
+      }
+      all &= have[i];
+    }
+    return __all(all);
+  };
+#define MQ_WSTEP(k)                              \
+  if (merge(r[(k) % 2])) return;                 \
+  _Pragma("unroll") for (int i = 0; i < N; i++) r[(k) % 2][i] = ldl1(wsb, w[i]); \
+  asm volatile("" ::: "memory");
+  MQ_WSTEP(0) MQ_WSTEP(1) MQ_WSTEP(2) MQ_WSTEP(3) MQ_WSTEP(4) MQ_WSTEP(5)
+  MQ_WSTEP(6) MQ_WSTEP(7) MQ_WSTEP(8) MQ_WSTEP(9) MQ_WSTEP(10) MQ_WSTEP(11)
+#undef MQ_WSTEP
+  merge(r[0]);
+  merge(r[1]);
+  uint32_t spins = 0;
+  for (;;) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < N; i++) ok &= have[i];
+    if (ok || watchdog(wsb, ws, ++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int i = 0; i < N; i++)
+      if (!have[i]) {
+        const uint32_t v = ldl1(wsb, w[i]);
+        if ((v >> 16) == tag) {
+          u[i] = v;
+          have[i] = true;
+        }
+      }
+  }
+  return;
+  }
+  {
 #pragma unroll
   for (int i = 0; i < N; i++) u[i] = ldl1(wsb, w[i]);
   uint32_t spins = 0;
@@ -543,6 +753,7 @@ __device__ __forceinline__ void poll_words(const Buf& wsb, uint32_t* ws, const u
 #pragma unroll
     for (int i = 0; i < N; i++)
       if ((u[i] >> 16) != tag) u[i] = ldl1(wsb, w[i]);
+  }
   }
 }
 
@@ -765,7 +976,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
               // the new v row (the raw bf16 values; no loads of this wave are in flight)
               const uint32_t w[2] = {lb + LX_QKV + 3 * HD + lane, lb + LX_QKV + 3 * HD + 64 + lane};
               uint32_t u[2];
-              poll_words(wsb, ws, w, tag_of(epoch, layer), u);
+              poll_words<!SPLIT>(wsb, ws, w, tag_of(epoch, layer), u);
               uint8_t* vbase = s_kv + KV_CAP * 256;
               *reinterpret_cast<uint16_t*>(vbase + vkv_off(prow, lane >> 3) + 2 * (lane & 7)) = (uint16_t)(u[0] & 0xffffu);
               *reinterpret_cast<uint16_t*>(vbase + vkv_off(prow, 8 + (lane >> 3)) + 2 * (lane & 7)) =
@@ -811,7 +1022,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           load_o(layer + 1);
           put_norms();
           if (att) kv_dma(kv_nt, P, layer + 1, g, c0, nc0, p, lds_kv, s, lane);
-          MQ_STAMP(layer * 40 + 10);
+          MQ_LANDED(layer * 40 + 10);
         }
       }
     } else {
@@ -892,20 +1103,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         if (layer + 1 < L) {
           // hold the burst until group A has published the next layer's q/k/v rows (its
           // member 0's first word), so that it runs during A's attention
-          {
-            const uint32_t want = tag_of(epoch, layer + 1);
-            uint32_t v = ldl1(wsb, lb + LX_QKV), spins = 0;
-            while ((v >> 16) != want) {
-              if (watchdog(wsb, ws, ++spins)) break;
-              __builtin_amdgcn_s_sleep(4);
-              v = ldl1(wsb, lb + LX_QKV);
-            }
-          }
           R.wpost = ldw2(wp(layer + 1, W_POST) + 4 * st);
           load_gu(layer + 1);
           load_d(layer + 1);
           put_norms();
-          MQ_STAMP(layer * 40 + 11);
+          MQ_LANDED(layer * 40 + 11);
         }
       }
     }
@@ -981,7 +1183,9 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         } else {
           ngat++;
           wait_cue(wsb, ws, lb + LX_CUE_B, tag_of(epoch, layer - 1));
-          ss = gather_half(wsb, ws, lb + LX_H, tag_of(epoch, layer - 1), c, lane, hv0, hv1, s_ssx, &s_ssn, 2u * ngat);
+          MQ_STAMP(layer * 40 + 39);
+          ss = gather_half(wsb, ws, lb + LX_H, tag_of(epoch, layer - 1), c, lane, hv0, hv1, s_ssx, &s_ssn, 2u * ngat,
+                           layer * 40 + 18);
         }
         MQ_STAMP(layer * 40 + 13);
         wait_norms(layer);
@@ -998,7 +1202,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           if (c == 0) {
             const uint32_t w[2] = {lb + LX_QKV + lane, lb + LX_QKV + 64 + lane};
             uint32_t u[2];
-            poll_words(wsb, ws, w, tag, u);
+            poll_words<!SPLIT>(wsb, ws, w, tag, u);
             MQ_STAMP(layer * 40 + 15);
             float ra, rb;
             qk_norm_rope(u[0], u[1], s_qkn, 0, s_cos, s_sin, lane, ra, rb);
@@ -1007,7 +1211,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           } else {
             const uint32_t w[2] = {lb + LX_QKV + 2 * HD + lane, lb + LX_QKV + 2 * HD + 64 + lane};
             uint32_t u[2];
-            poll_words(wsb, ws, w, tag, u);
+            poll_words<!SPLIT>(wsb, ws, w, tag, u);
             qk_norm_rope(u[0], u[1], s_qkn, 64, s_cos, s_sin, lane, fr[0][0], fr[0][1]);
           }
           MQ_STAMP(layer * 40 + 25);
@@ -1117,7 +1321,9 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         // ---------------- gather h1; post-attention RMSNorm
         ngat++;
         wait_cue(wsb, ws, lb + LX_CUE_A, tag);
-        const float ss1 = gather_half(wsb, ws, lb + LX_H1, tag, c, lane, hv0, hv1, s_ssx, &s_ssn, 2u * ngat);
+        MQ_STAMP(layer * 40 + 39);
+        const float ss1 = gather_half(wsb, ws, lb + LX_H1, tag, c, lane, hv0, hv1, s_ssx, &s_ssn, 2u * ngat,
+                                      layer * 40 + 18);
         MQ_STAMP(layer * 40 + 21);
         wait_norms(layer);
         norm_out(hv0, hv1, ss1, s_wn);
@@ -1128,8 +1334,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         {
           const int q = pt;
           if (q < XUNITS / 4) {
-            u32x4 v = ldl4(wsb, lb + LX_M + 4 * q);
-            v = repoll_l4(wsb, ws, lb + LX_M + 4 * q, tag, v);
+            const u32x4 v = poll2_l4(wsb, ws, lb + LX_M + 4 * q, tag);
             reinterpret_cast<u32x2*>(s_x1)[q] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
           }
         }
@@ -1182,7 +1387,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             // q head 2g + 1: QK-norm and RoPE (the poll waves take q head 2g, k and v)
             const uint32_t w[2] = {lb + LX_QKV + HD + lane, lb + LX_QKV + HD + 64 + lane};
             uint32_t u[2];
-            poll_words(wsb, ws, w, tag, u);
+            poll_words<!SPLIT>(wsb, ws, w, tag, u);
             float ra, rb;
             qk_norm_rope(u[0], u[1], s_qkn, 0, s_cos, s_sin, lane, ra, rb);
             s_q[HD + lane] = (uint16_t)f2bf(ra);

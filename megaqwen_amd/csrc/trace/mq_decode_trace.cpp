@@ -23,6 +23,16 @@ __device__ unsigned long long* g_trace;
       g_str[(i)] = (uint32_t)c_;                                                      \
     }                                                                                 \
   } while (0)
+#define MQ_STAMP_AFTER(i, v)                  \
+  do {                                        \
+    asm volatile("" ::"v"(v) : "memory");     \
+    MQ_STAMP(i);                              \
+  } while (0)
+#define MQ_LANDED(i)                          \
+  do {                                        \
+    __builtin_amdgcn_s_waitcnt(0x0f70);       \
+    MQ_STAMP(i);                              \
+  } while (0)
 #define MQ_STAMP_DUMP()                                                \
   do {                                                                 \
     for (int i_ = threadIdx.x; i_ < 32 * 40 + 8; i_ += blockDim.x)     \
@@ -190,6 +200,67 @@ int main(int argc, char** argv) {
     prev = end[i];
   }
   printf("\nLayer period (XCD's last h store to the next): %.2f us; hop stages add up to %.2f us.\n", per, hop);
+  // the residual-stream gathers in detail: cue seen, first poll returned, gathered, re-polls
+  for (int grp = 0; grp < 2; grp++) {
+    const int j0 = grp ? 16 : 0, j1 = grp ? 32 : 16;
+    double cue = 0, first = 0, done = 0, cnt = 0;
+    for (int l = 3; l <= 26; l++)
+      for (int g = 0; g < 8; g++) {
+        const int64_t t0 = T0(l, g);
+        for (int j = j0; j < j1; j++) {
+          const int w = 8 * j + g;
+          cue += (double)(int32_t)(T(w, l, 39) - t0) * 0.01;
+          first += (double)(int32_t)(T(w, l, 18) - t0) * 0.01;
+          done += (double)(int32_t)(T(w, l, grp ? 21 : 13) - t0) * 0.01;
+          cnt++;
+        }
+      }
+    printf("%s gather (workgroup means, from the XCD's last h store): cue seen %.2f us, first poll round back "
+           "%.2f us, gathered %.2f us\n",
+           grp ? "group-B h1" : "group-A h", cue / cnt, first / cnt, done / cnt);
+  }
+  // cross-XCD reductions: for each reducer (member m of XCD g), its eight producers (member
+  // m of every XCD) store their partials; latency from the last producer's store to the
+  // reducer's store, and the spread of the producers' stores
+  for (int grp = 0; grp < 2; grp++) {
+    const int kp = grp ? 38 : 36, kd = grp ? 32 : 30, j0 = grp ? 16 : 0;
+    double lat = 0, spread = 0, lat_own = 0, cnt = 0;
+    for (int l = 3; l <= 26; l++)
+      for (int m = 0; m < 16; m++) {
+        int64_t pmax = INT64_MIN, pmin = INT64_MAX;
+        for (int x = 0; x < 8; x++) {
+          pmax = std::max(pmax, T(8 * (j0 + m) + x, l, kp));
+          pmin = std::min(pmin, T(8 * (j0 + m) + x, l, kp));
+        }
+        spread += (double)(int32_t)(pmax - pmin) * 0.01;
+        for (int g = 0; g < 8; g++) {
+          lat += (double)(int32_t)(T(8 * (j0 + m) + g, l, kd) - pmax) * 0.01;
+          lat_own += (double)(int32_t)(T(8 * (j0 + m) + g, l, kd) - T(8 * (j0 + m) + g, l, kp)) * 0.01;
+          cnt++;
+        }
+      }
+    printf("%s cross-XCD reduction: reducer done %.2f us after the last of its 8 producers' stores "
+           "(%.2f us after its own XCD's producer); producers' spread %.2f us\n",
+           grp ? "down_proj" : "o_proj", lat / cnt, lat_own / cnt, spread / (cnt / 8));
+  }
+  // weight bursts: when stream wave 0's loads have all landed (this build waits for them)
+  {
+    double a = 0, b = 0, ca = 0, cb = 0;
+    for (int l = 3; l <= 25; l++)
+      for (int g = 0; g < 8; g++)
+        for (int j = 0; j < 32; j++) {
+          const int w = 8 * j + g;
+          if (j < 16) {
+            a += (double)(int32_t)(T(w, l, 10) - T0(l, g)) * 0.01;
+            ca++;
+          } else {
+            b += (double)(int32_t)(T(w, l, 11) - T0(l + 1, g)) * 0.01;
+            cb++;
+          }
+        }
+    printf("bursts landed (stream wave 0, workgroup means): group A's next-layer weights and K/V at %.2f us of the "
+           "layer; group B's at %.2f us of the next layer\n", a / ca, b / cb);
+  }
   // final norm and LM head
   double fin = 0, lm = 0;
   int64_t first = INT64_MAX, lastf2 = INT64_MIN;

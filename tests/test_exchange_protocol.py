@@ -58,9 +58,7 @@ FROM_PREVIOUS_LAYER = ("LX_H", "LX_CUE_B")
 
 
 def expected_tag(region, epoch, layer, L):
-    """Tag a consumer polls for at `layer` (layer == L: the final-norm gather). Group B's
-    stream waves also poll LX_QKV word 0 for layer l + 1 before streaming: that is the read
-    of layer l + 1 below, made earlier, against the same stale content."""
+    """Tag a consumer polls for at `layer` (layer == L: the final-norm gather)."""
     kind = REGIONS[region][0]
     if region in FROM_PREVIOUS_LAYER:
         return tag16(epoch, layer - 1)
