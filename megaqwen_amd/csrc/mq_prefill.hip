@@ -931,22 +931,56 @@ __global__ void __launch_bounds__(256) argmax_final(const float* bmv, const int*
 using namespace mq;
 using namespace mq::pf;
 
-// GEMM shapes (measured on MI355X at S = 512 with the weights cold, as each layer's are):
-// eight-wave workgroups (sixteen for gate/up) with 128-row tiles and a ring of 64-wide
-// k-steps (more waves hide more latency: four-wave tiles were 15-25% slower);
-// o_proj and down_proj split k four ways into fp32 partials, so that each of their 256
-// workgroups streams (128 + 64) rows instead of (32 + 64) rows over a quarter of k
-constexpr int GST = 4, GKS = 1, GWM = 4, GWN = 2;
-// gate/up (128 x 128 tiles, 192 workgroups): sixteen waves and a three-step ring
-constexpr int GU_ST = 3, GU_WM = 4, GU_WN = 4;
-constexpr int TM_G = 128, TN_GU = 128, TN_RES = 64, RES_SPLIT = 4;
-// q/k/v with the QK-norm/RoPE/K-V-append epilogue: 64 x 128 tiles (one head each), 2 x 4 waves
-constexpr int TM_QKV = 64, TN_QKV = HD, QKV_WM = 2, QKV_WN = 4;
+// GEMM shapes by prompt length (measured on MI355X, weights cold as each layer's are).
+// Every shape computes each output with the same MFMA chain over k in the same order, and
+// o_proj / down_proj always split k four ways, so the choice does not change any result.
+// Longer prompts take larger tiles: a launch streams M N K 2 (1 / TM + 1 / TN) operand
+// bytes from L2 into the CUs, and at S = 8192 the 256 x 256 tiles (sixteen waves, a
+// two-step ring) run gate/up at 840-910 TFLOP/s against 650 for 128 x 128 ones. Short
+// prompts keep smaller tiles so that the grid still fills the 256 CUs:
+//   q/k/v (whole-head tiles, QK-norm/RoPE/K-V-append epilogue): 64 x 128 on 2 x 4 waves;
+//     from S = 1024 128 x 128 on 4 x 2; from 2048 256 x 128 on 4 x 2 with a three-step ring;
+//   gate/up: 128 x 128 on 4 x 4 waves; from S = 1024 128 x 256; from 2048 256 x 256;
+//   o_proj, down_proj (k split four ways into fp32 partials): 128 x 64 on 4 x 2 waves;
+//     from S = 1024 128 x 256 on 2 x 4; from 4096 256 x 256 on 4 x 4.
+constexpr int RES_SPLIT = 4;
 
 // one launch of gemm_nt over a [m, sum of the segments' widths] output, k split `split` ways
 template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
 void gemm(const GemmArgs& g, int ntiles, hipStream_t stream, int split = 1) {
   gemm_nt<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, (g.m + TM - 1) / TM, split), 64 * WM * WN, 0, stream>>>(g);
+}
+static void gemm_qkv(GemmArgs g, hipStream_t stream) {
+  g.seg[0].ntiles = QS / HD;
+  g.seg[1].ntiles = g.seg[2].ntiles = KVS / HD;
+  const int nt = (QS + 2 * KVS) / HD;
+  if (g.m >= 2048) gemm<EPI_QKN, 256, HD, 3, 1, 4, 2>(g, nt, stream);
+  else if (g.m >= 1024) gemm<EPI_QKN, 128, HD, 4, 1, 4, 2>(g, nt, stream);
+  else gemm<EPI_QKN, 64, HD, 4, 1, 2, 4>(g, nt, stream);
+}
+static void gemm_gate_up(GemmArgs g, hipStream_t stream) {
+  if (g.m >= 2048) {
+    g.seg[0].ntiles = I / 128;
+    gemm<EPI_SILU, 256, 256, 2, 1, 4, 4>(g, I / 128, stream);
+  } else if (g.m >= 1024) {
+    g.seg[0].ntiles = I / 128;
+    gemm<EPI_SILU, 128, 256, 3, 1, 4, 4>(g, I / 128, stream);
+  } else {
+    g.seg[0].ntiles = I / 64;
+    gemm<EPI_SILU, 128, 128, 3, 1, 4, 4>(g, I / 64, stream);
+  }
+}
+static void gemm_residual(GemmArgs g, hipStream_t stream) {
+  if (g.m >= 4096) {
+    g.seg[0].ntiles = H / 256;
+    gemm<EPI_PART, 256, 256, 2, 1, 4, 4>(g, H / 256, stream, RES_SPLIT);
+  } else if (g.m >= 1024) {
+    g.seg[0].ntiles = H / 256;
+    gemm<EPI_PART, 128, 256, 3, 1, 2, 4>(g, H / 256, stream, RES_SPLIT);
+  } else {
+    g.seg[0].ntiles = H / 64;
+    gemm<EPI_PART, 128, 64, 4, 1, 4, 2>(g, H / 64, stream, RES_SPLIT);
+  }
 }
 
 extern "C" int launch_prefill_float(const int* input_token_ids, int* output_token_id, int seq_len,
@@ -1022,11 +1056,11 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     uint16_t* vcl = bfm(v_cache) + l * kv_layer;
     GemmArgs g{};
     g.a = nrm; g.lda = H; g.m = S; g.k = H; g.nseg = 3;
-    g.seg[0] = GemmSeg{bf(w.q_proj_weight), nullptr, nullptr, QS / TN_QKV, QS};
-    g.seg[1] = GemmSeg{bf(w.k_proj_weight), nullptr, nullptr, KVS / TN_QKV, KVS};
-    g.seg[2] = GemmSeg{bf(w.v_proj_weight), nullptr, nullptr, KVS / TN_QKV, KVS};
+    g.seg[0] = GemmSeg{bf(w.q_proj_weight), nullptr, nullptr, 0, QS};
+    g.seg[1] = GemmSeg{bf(w.k_proj_weight), nullptr, nullptr, 0, KVS};
+    g.seg[2] = GemmSeg{bf(w.v_proj_weight), nullptr, nullptr, 0, KVS};
     g.qkn = QknArgs{bf(w.q_norm_weight), bf(w.k_norm_weight), bf(cos_table), bf(sin_table), qp, kcl, vcl, max_seq_len};
-    gemm<EPI_QKN, TM_QKV, TN_QKV, GST, GKS, QKV_WM, QKV_WN>(g, (QS + 2 * KVS) / TN_QKV, stream);
+    gemm_qkv(g, stream);
     chk();
     // long prompts: the flash form (64 rows of both heads a workgroup); short ones: 32 rows of
     // one head a workgroup, which fills more CUs (256 workgroups at S = 512)
@@ -1037,22 +1071,22 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     chk();
     GemmArgs go{};
     go.a = att; go.lda = QS; go.m = S; go.k = QS; go.nseg = 1;
-    go.seg[0] = GemmSeg{bf(w.o_proj_weight), nullptr, nullptr, H / TN_RES, H};
+    go.seg[0] = GemmSeg{bf(w.o_proj_weight), nullptr, nullptr, 0, H};
     go.part = parts;
-    gemm<EPI_PART, TM_G, TN_RES, GST, GKS, GWM, GWN>(go, H / TN_RES, stream, RES_SPLIT);
+    gemm_residual(go, stream);
     chk();
     resid_norm_rows<RES_SPLIT><<<S, 64, 0, stream>>>(parts, h, bf(w.post_attn_layernorm_weight), mln, S);
     chk();
     GemmArgs gu{};
     gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
-    gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, I / (TN_GU / 2), I};
-    gemm<EPI_SILU, TM_G, TN_GU, GU_ST, GKS, GU_WM, GU_WN>(gu, I / (TN_GU / 2), stream);
+    gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, 0, I};
+    gemm_gate_up(gu, stream);
     chk();
     GemmArgs gd{};
     gd.a = mid; gd.lda = I; gd.m = S; gd.k = I; gd.nseg = 1;
-    gd.seg[0] = GemmSeg{bf(w.down_proj_weight), nullptr, nullptr, H / TN_RES, H};
+    gd.seg[0] = GemmSeg{bf(w.down_proj_weight), nullptr, nullptr, 0, H};
     gd.part = parts;
-    gemm<EPI_PART, TM_G, TN_RES, GST, GKS, GWM, GWN>(gd, H / TN_RES, stream, RES_SPLIT);
+    gemm_residual(gd, stream);
     chk();
     // the next layer's input RMSNorm (none after the last: the final norm is the LM head's)
     resid_norm_rows<RES_SPLIT><<<S, 64, 0, stream>>>(parts, h, l + 1 < num_layers ? bf(layer_weights[l + 1].input_layernorm_weight) : nullptr,

@@ -106,6 +106,35 @@ def test_prefill_two_attention_blocks(state_dict, embed_gpu):
     assert rel_l2(hg, h) < 5e-3
 
 
+@pytest.mark.parametrize("S", [1100, 2100, 4200])
+def test_prefill_long_tile_shapes_vs_oracle(state_dict, embed_gpu, S):
+    """Prompts that take the larger GEMM tiles (q/k/v 128- and 256-row tiles, gate/up
+    128 x 256 and 256 x 256, o_proj/down_proj 128 x 256 and 256 x 256) and the flash-form
+    attention: the layer's K/V slots and attention output element-wise against the oracle,
+    the layer output as a vector."""
+    print(f"prefill S={S}", flush=True)
+    dec, orc = small_pair(state_dict, embed_gpu, 1, S + 16)
+    ids = prompt_ids(S, seed=7 + S)
+    dec.prefill_step(ids)
+    trace = {}
+    kc, vc = np.zeros_like(orc.k_cache[0]), np.zeros_like(orc.v_cache[0])
+    h = O.decoder_layer(orc.layers[0], orc.embed[ids], np.arange(S), orc.cos, orc.sin, kc, vc, trace=trace)
+    kg, vg = f32(dec.get_k_cache()), f32(dec.get_v_cache())
+    ok, dmax, frac = ulp_close(kg[0, :, :S], kc[:, :S], max_ulps=1, max_frac=0.3, floor=2.0 ** -5)
+    print(f"k: max {dmax:.3g} frac {frac:.3f}")
+    assert ok
+    ok, dmax, frac = ulp_close(vg[0, :, :S], vc[:, :S], max_ulps=1, max_frac=0.05)
+    print(f"v: max {dmax:.3g} frac {frac:.3f}")
+    assert ok
+    att, oatt = f32(dec.attn_out_[:S]), trace["attn"]
+    ok, dmax, frac = ulp_close(att, oatt, max_ulps=2, max_frac=0.1)
+    print(f"attention: max {dmax:.3g} frac {frac:.3f} rel L2 {rel_l2(att, oatt):.3g}")
+    assert ok
+    hg = f32(dec.hidden_float_[:S])
+    print(f"1-layer output rel L2 {rel_l2(hg, h):.3g}")
+    assert rel_l2(hg, h) < 5e-3
+
+
 def test_prefill_matches_token_by_token_decode(state_dict, embed_gpu):
     """Prefill's K/V cache and next token agree with feeding the same prompt to the
     decode kernel one token at a time (two independent kernels, one model)."""
