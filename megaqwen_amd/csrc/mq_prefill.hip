@@ -5,7 +5,7 @@
 // slots 0..S-1 of every layer are written, and the greedy next token is taken
 // from the last row. After embed_rows and the first layer's rmsnorm_rows, per layer:
 //   gemm_nt (q, k, v in one launch; its epilogue applies QK-norm and RoPE and appends K/V)
-//   -> attn_prefill or, past 1024 tokens, attn_prefill_fa (causal, MFMA)
+//   -> attn_prefill or, past 1024 tokens, attn_prefill_fa, past 5120 attn_prefill_fa2 (causal, MFMA)
 //   -> gemm_nt (o_proj, k split four ways)
 //   -> resid_norm_rows (partials + residual, post-attention RMSNorm)
 //   -> gemm_nt (gate and up, SiLU(gate) * up epilogue) -> gemm_nt (down_proj, k split)
@@ -426,6 +426,12 @@ __device__ __forceinline__ uint32_t akv_off(int row, int chunk) { return row * 2
 // the arguments of the softmax (x <= 0), the accuracy class of the vectorised exp that
 // torch's CPU flash-attention kernel uses (exp_u20); exp(-inf) = 0.
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+// x, opaque to the compiler: a product passed through it is rounded on its own and never
+// contracted with a later add into one fused multiply-add
+__device__ __forceinline__ float unfused(float x) {
+  asm("" : "+v"(x));
+  return x;
+}
 
 // Rows k0 .. k0 + ACK - 1 of a K or V cache head (rows past klast repeat row klast) into
 // the chunk buffer at LDS address `lds`: instruction q moves rows 4q .. 4q + 3, lane ->
@@ -613,8 +619,6 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
       o[16] = (uint16_t)f2bf(oacc[rb][1][e] * inv);
     }
 }
-#undef AWAIT
-#undef ABAR
 
 // ------------------------------------------------------------------ causal attention, flash form
 // Workgroup (KV group g, query block): query rows r0 .. r0 + 16 RT - 1 of both query heads of
@@ -816,6 +820,270 @@ __global__ void __launch_bounds__(128 * RT) attn_prefill_fa(const uint16_t* q, c
           u32x2{pack_bf2(o[dt][0] * inv, o[dt][1] * inv), pack_bf2(o[dt][2] * inv, o[dt][3] * inv)};
   }
 }
+
+// ------------------------------------------------------------------ causal attention, two passes
+// Workgroup (KV group g, query block): query rows r0 .. r0 + 127 of both query heads of the
+// group, eight waves of 16 rows each, every wave holding both heads' rows, so that each K
+// or V fragment read from LDS feeds two MFMAs. Keys run in blocks of 512 (torch's CPU flash
+// blocks) with a running maximum; a block's softmax needs its row maxima before any
+// exponential, so each block is swept twice over its 64-key chunks: pass 1 computes the
+// scores and keeps only the row maxima, pass 2 recomputes them, takes the bf16
+// probabilities (held in registers as the B operand of O^T = V^T P^T, as in
+// attn_prefill_fa) and runs that chunk's P.V at once. The sums, the P.V chains and the
+// rescaling happen in the same order as in attn_prefill_fa, so both give the same bits.
+//
+// LDS: the block's 512 K rows (128 KB, resident for both passes) and a two-chunk V ring
+// (32 KB). During pass 2 the next block's K chunk c - 1 is copied into the slot that
+// chunk c - 1 has just left, and V runs one chunk ahead, so pass 1 of the next block finds
+// its K rows in place.
+constexpr int F2W = 8, F2Q = 16 * F2W, F2KB = 512, F2K = 64, F2NC = F2KB / F2K;
+// prompts longer than this take the two-pass form (at most 8 S / 128 workgroups, so shorter
+// prompts run faster on attn_prefill_fa's 8 S / 64; the two give the same bits)
+constexpr int FLASH2_MIN_S = 5120;
+// V rows live in LDS with their own chunk swizzle, chunk c of row r in slot c ^ vsw_pf(r):
+// a P.V transpose read takes, per half wave, rows 4 kg + i (kg < 2, i < 4, plus a multiple
+// of 16) at chunks 2 dt and 2 dt + 1, and vsw_pf = 2 (r % 8) puts those 16 (row, chunk)
+// pairs in 16 distinct slots, so the read is free of bank conflicts
+__device__ __forceinline__ int vsw_pf(int row) { return 2 * (row & 7); }
+__device__ __forceinline__ uint32_t vkv_off_pf(int row, int chunk) { return row * 256 + 16 * (chunk ^ vsw_pf(row)); }
+
+__global__ void __launch_bounds__(64 * F2W) attn_prefill_fa2(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                                                              uint16_t* out, int S, int max_seq, float scale) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  __shared__ __align__(16) uint8_t s_k[F2NC][F2K * 256];
+  __shared__ __align__(16) uint8_t s_v[2][F2K * 256];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // XCD-aware order: workgroup id runs on XCD id % 8, made the KV group; the longest query
+  // blocks (the most keys) are dispatched first
+  const int id = blockIdx.x, g = id & 7, nqb = gridDim.x >> 3;
+  const int r0 = (nqb - 1 - (id >> 3)) * F2Q;
+  const int r16 = lane & 15, kg = lane >> 4;
+  const int row = r0 + 16 * wv + r16;  // this lane's query row
+  const int wrow0 = r0 + 16 * wv, wrow1 = wrow0 + 15;  // the wave's query rows
+  const int nkey = min(S, r0 + F2Q);
+  const int nblk = (nkey + F2KB - 1) / F2KB;
+  const uint16_t* K = kc + (size_t)g * max_seq * HD;
+  const uint16_t* V = vc + (size_t)g * max_seq * HD;
+  const uint32_t lk = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_k[0][0];
+  const uint32_t lv = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_v[0][0];
+
+  // rows base .. base + 63 of a K or V head (rows past klast repeat row klast) into the
+  // chunk buffer at `lds`: instruction i moves rows 4 qq .. 4 qq + 3, qq = wv + 8 i (lane ->
+  // row 4 qq + lane / 16, slot lane % 16, which holds the row's 16-byte chunk slot ^ row % 16)
+  // (K rows in slots chunk ^ row % 16, V rows in slots chunk ^ vsw_pf(row); rows 4 qq + r and
+  // 4 qq + 32 + r share both, so one source chunk offset serves both instructions)
+  const int drow0 = 4 * wv + (lane >> 4);
+  const int dchk_k = 8 * ((lane & 15) ^ (drow0 & 15)), dchk_v = 8 * ((lane & 15) ^ vsw_pf(drow0));
+  const uint32_t dl0 = __builtin_amdgcn_readfirstlane(1024u * wv), dl1 = dl0 + 1024u * F2W;
+  auto dma_chunk = [&](const uint16_t* src, int base, int klast, uint32_t lds) {
+    const int dchk = src == K ? dchk_k : dchk_v;
+    dma16(src + (size_t)min(base + drow0, klast) * HD + dchk, lds + dl0);
+    dma16(src + (size_t)min(base + drow0 + 32, klast) * HD + dchk, lds + dl1);
+  };
+  auto klast_of = [&](int b) { return min(nkey, F2KB * b + F2KB) - 1; };
+
+  // Q^T (B operand) of both heads: lane (row r16, kg) holds dims 32 ks + 8 kg .. +7 of its row
+  u32x4 qf[2][4];
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+      qf[hh][ks] = ldw(q + (size_t)min(row, S - 1) * QS + HD * (2 * g + hh) + 32 * ks + 8 * kg);
+  f32x4 o[2][8];
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) o[hh][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+
+  // block 0's K rows and V chunk 0
+  for (int c = 0; c < F2NC; c++) dma_chunk(K, F2K * c, klast_of(0), lk + (uint32_t)c * (F2K * 256));
+  dma_chunk(V, 0, klast_of(0), lv);
+  // (a compiler-visible wait: the q loads are then known complete on every path, so no
+  // wait for them, which would also wait for the DMAs in flight, lands inside the loops)
+  wait_vmem();
+  ABAR();
+
+  // LDS byte offsets of this lane's fragment reads: K (A operand) row 16 j + r16, 16-byte
+  // chunk 4 ks + kg -> 4096 j + koff[ks]; V^T (transpose reads) rows 32 j2 + 4 kg + r16 / 4
+  // (+ 16), dims 16 dt + 4 (r16 % 4) .. +3 -> 8192 j2 + voff[dt] (+ 4096)
+  uint32_t koff[4], voff[8];
+#pragma unroll
+  for (int ks = 0; ks < 4; ks++) koff[ks] = lk + akv_off(r16, 4 * ks + kg);
+#pragma unroll
+  for (int dt = 0; dt < 8; dt++) {
+    const int dq = 16 * dt + 4 * (r16 & 3);
+    voff[dt] = vkv_off_pf(4 * kg + (r16 >> 2), dq >> 3) + 2 * (dq & 7);
+  }
+
+  // raw scores (q . k, unscaled) of key tile j (16 keys; lane: query row r16, keys
+  // 16 j + 4 kg + e) of K chunk slot c, both heads
+  auto raw_scores = [&](uint32_t kbase, int j, f32x4 (&a)[2]) {
+    u32x4 kf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+      kf[ks] = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(kbase + 4096u * j + koff[ks]);
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      a[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) a[hh] = mfma_16x16x32(kf[ks], qf[hh][ks], a[hh]);
+    }
+  };
+
+  for (int b = 0; b < nblk; b++) {
+    const int kb0 = F2KB * b, kb1 = min(nkey, kb0 + F2KB), nchb = (kb1 - kb0 + F2K - 1) / F2K;
+    const bool more = b + 1 < nblk;
+    // ---- pass 1: the block's row maxima, over the unscaled scores (scale > 0 and rounding
+    // is monotonic, so max(a * scale) = max(a) * scale, both rounded)
+    float mx[2] = {-INFINITY, -INFINITY};
+    for (int c = 0; c < nchb; c++) {
+      const uint32_t kbase = (uint32_t)c * (F2K * 256);
+      const int ck0 = kb0 + F2K * c;  // the chunk's first key
+      if (ck0 + F2K - 1 < kb1 && ck0 + F2K - 1 <= wrow0) {
+        // no score of the chunk is masked
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          f32x4 a[2];
+          raw_scores(kbase, j, a);
+#pragma unroll
+          for (int hh = 0; hh < 2; hh++)
+            mx[hh] = fmaxf(fmaxf(mx[hh], fmaxf(a[hh][0], a[hh][1])), fmaxf(a[hh][2], a[hh][3]));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int key0 = ck0 + 16 * j;
+          if (key0 <= wrow1) {
+            f32x4 a[2];
+            raw_scores(kbase, j, a);
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                const int key = key0 + 4 * kg + e;
+                mx[hh] = fmaxf(mx[hh], (key < kb1 && key <= row) ? a[hh][e] : -INFINITY);
+              }
+          }
+        }
+      }
+    }
+    float base[2], al[2], sum[2] = {0.f, 0.f};
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      const float mn = fmaxf(m_run[hh], lane_group_max(mx[hh]) * scale);
+      base[hh] = mn == -INFINITY ? 0.f : mn;
+      al[hh] = m_run[hh] == -INFINITY ? 0.f : expf(m_run[hh] - base[hh]);
+      m_run[hh] = mn;
+#pragma unroll
+      for (int dt = 0; dt < 8; dt++) o[hh][dt] *= al[hh];
+    }
+    // ---- pass 2: probabilities and P.V, chunk by chunk
+    for (int c = 0; c < F2NC; c++) {
+      // V chunk c has landed (the later DMAs of this wave: the next block's K chunk c - 2,
+      // issued after it); every wave is done with chunk c - 1
+      if (c >= 2 && more) AWAIT(2);
+      else if (c >= 1) AWAIT(0);
+      ABAR();
+      // V runs one chunk ahead (the next block's chunk 0 after chunk 7); the next block's K
+      // chunk c - 1 goes into the slot chunk c - 1 has left
+      if (c + 1 < F2NC) {
+        if (more || c + 1 < nchb) dma_chunk(V, kb0 + F2K * (c + 1), kb1 - 1, lv + (uint32_t)((c + 1) & 1) * (F2K * 256));
+      } else if (more) {
+        dma_chunk(V, kb0 + F2KB, klast_of(b + 1), lv);
+      }
+      if (c >= 1 && more)
+        dma_chunk(K, kb0 + F2KB + F2K * (c - 1), klast_of(b + 1), lk + (uint32_t)(c - 1) * (F2K * 256));
+      if (c >= nchb) continue;
+      const uint32_t kbase = (uint32_t)c * (F2K * 256);
+      const int ck0 = kb0 + F2K * c;
+      u32x2 pb[2][4];
+      if (ck0 + F2K - 1 < kb1 && ck0 + F2K - 1 <= wrow0) {
+        // no score of the chunk is masked
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          f32x4 a[2];
+          raw_scores(kbase, j, a);
+#pragma unroll
+          for (int hh = 0; hh < 2; hh++) {
+            float e4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              e4[e] = exp_fast(unfused(a[hh][e] * scale) - base[hh]);
+              sum[hh] += e4[e];
+            }
+            pb[hh][j] = u32x2{pack_bf2(e4[0], e4[1]), pack_bf2(e4[2], e4[3])};
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int key0 = ck0 + 16 * j;
+          if (key0 <= wrow1) {
+            f32x4 a[2];
+            raw_scores(kbase, j, a);
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+              float e4[4];
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                // the score a * scale, or -inf where masked (exp(-inf) = 0)
+                const int key = key0 + 4 * kg + e;
+                const float sv = (key < kb1 && key <= row) ? unfused(a[hh][e] * scale) : -INFINITY;
+                e4[e] = exp_fast(sv - base[hh]);
+                sum[hh] += e4[e];
+              }
+              pb[hh][j] = u32x2{pack_bf2(e4[0], e4[1]), pack_bf2(e4[2], e4[3])};
+            }
+          } else {
+            pb[0][j] = pb[1][j] = u32x2{0u, 0u};
+          }
+        }
+      }
+      const uint32_t vb = lv + (uint32_t)(c & 1) * (F2K * 256);
+#pragma unroll
+      for (int j2 = 0; j2 < 2; j2++) {
+        if (ck0 + 32 * j2 <= wrow1) {
+          const u32x4 pf0 = u32x4{pb[0][2 * j2].x, pb[0][2 * j2].y, pb[0][2 * j2 + 1].x, pb[0][2 * j2 + 1].y};
+          const u32x4 pf1 = u32x4{pb[1][2 * j2].x, pb[1][2 * j2].y, pb[1][2 * j2 + 1].x, pb[1][2 * j2 + 1].y};
+#pragma unroll
+          for (int dt = 0; dt < 8; dt++) {
+            const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(vb + 8192 * j2 + voff[dt]));
+            const v4s hi =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(vb + 8192 * j2 + 4096 + voff[dt]));
+            const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+            const u32x4 vf = u32x4{l2.x, l2.y, h2.x, h2.y};
+            o[0][dt] = mfma_16x16x32(vf, pf0, o[0][dt]);
+            o[1][dt] = mfma_16x16x32(vf, pf1, o[1][dt]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) l_run[hh] = lane_group_sum(sum[hh]) + al[hh] * l_run[hh];
+    // the next block's K chunk 7 (every wave is done with slot 7), then all of its K rows
+    // and its V chunk 0 in place
+    ABAR();
+    if (more) dma_chunk(K, kb0 + F2KB + F2K * (F2NC - 1), klast_of(b + 1), lk + (uint32_t)(F2NC - 1) * (F2K * 256));
+    AWAIT(0);
+    ABAR();
+  }
+  if (row < S) {
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      const float inv = 1.0f / l_run[hh];
+      uint16_t* op = out + (size_t)row * QS + HD * (2 * g + hh) + 4 * kg;
+#pragma unroll
+      for (int dt = 0; dt < 8; dt++)
+        *reinterpret_cast<u32x2*>(op + 16 * dt) =
+            u32x2{pack_bf2(o[hh][dt][0] * inv, o[hh][dt][1] * inv), pack_bf2(o[hh][dt][2] * inv, o[hh][dt][3] * inv)};
+    }
+  }
+}
+
+#undef AWAIT
+#undef ABAR
 
 // ------------------------------------------------------------------ LM head
 constexpr int LMB = 1184;  // partial-argmax blocks (the length of the reference's block_max_* buffers)
@@ -1062,9 +1330,13 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     g.qkn = QknArgs{bf(w.q_norm_weight), bf(w.k_norm_weight), bf(cos_table), bf(sin_table), qp, kcl, vcl, max_seq_len};
     gemm_qkv(g, stream);
     chk();
-    // long prompts: the flash form (64 rows of both heads a workgroup); short ones: 32 rows of
-    // one head a workgroup, which fills more CUs (256 workgroups at S = 512)
-    if (S > FLASH_MIN_S)
+    // long prompts: the two-pass flash form (128 rows of both heads a workgroup), then the
+    // one-pass flash form (64 rows); short ones: 32 rows of one head a workgroup, which fills
+    // more CUs (256 workgroups at S = 512)
+    if (S > FLASH2_MIN_S)
+      attn_prefill_fa2<<<NKV * ((S + F2Q - 1) / F2Q), 64 * F2W, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len,
+                                                                             attn_scale);
+    else if (S > FLASH_MIN_S)
       attn_prefill_fa<4><<<NKV * ((S + 63) / 64), 512, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
     else
       attn_prefill<<<NQ * ((S + AQ - 1) / AQ), 256, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
