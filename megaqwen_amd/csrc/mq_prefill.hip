@@ -55,7 +55,12 @@ namespace pf {
 // that follows) so that their grid still fills the 256 CUs.
 constexpr int TK = 64;
 
-enum : int { EPI_STORE = 0, EPI_SILU = 1, EPI_PART = 2, EPI_QKN = 3 };
+enum : int { EPI_STORE = 0, EPI_SILU = 1, EPI_PART = 2, EPI_QKN = 3, EPI_RESADD = 4 };
+// EPI_RESADD: the product's k range is summed as four consecutive quarters, each its own
+// MFMA chain from zero, added in quarter order (((q0 + q1) + q2) + q3) -- the same sums as a
+// four-way k split whose fp32 partials resid_norm_rows adds in split order -- and the
+// epilogue applies the residual add out = bf16(out + bf16(sum)) in place
+constexpr int RES_QUARTERS = 4;
 
 struct GemmSeg {
   const uint16_t* w;   // weight rows [n, k]; EPI_SILU: gate_proj rows
@@ -163,6 +168,9 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
   for (int i = 0; i < RB; i++)
 #pragma unroll
     for (int j = 0; j < CB; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // EPI_RESADD: the sum of the quarters done so far
+  f32x4 tot[EPI == EPI_RESADD ? RB : 1][EPI == EPI_RESADD ? CB : 1];
+  const int kq = KT / RES_QUARTERS;  // k-steps (of TK * KS) per quarter
 #pragma unroll
   for (int kt = 0; kt < NST - 1; kt++) issue(kt);
   for (int kt = 0; kt < KT; kt++) {
@@ -187,6 +195,20 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
 #pragma unroll
           for (int j = 0; j < CB; j++) acc[i][j] = mfma_16x16x32(af, bf[j], acc[i][j]);
         }
+      }
+    }
+    if constexpr (EPI == EPI_RESADD) {
+      if ((kt + 1) % kq == 0) {
+        // a quarter ends: fold it into the running sum (the first one is the sum) and
+        // start the next quarter's chain from zero
+        const bool first = kt + 1 == kq;
+#pragma unroll
+        for (int i = 0; i < RB; i++)
+#pragma unroll
+          for (int j = 0; j < CB; j++) {
+            tot[i][j] = first ? acc[i][j] : tot[i][j] + acc[i][j];
+            acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
       }
     }
   }
@@ -257,6 +279,16 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
     for (int e = 0; e < 4; e++) {
       const int row = m0 + 16 * (RB * wm + i) + rq + e;
       if (row >= G.m) continue;
+      if (EPI == EPI_RESADD) {
+        // h = bf16(h + bf16(o)) (modeling_qwen3.py:316,322)
+        uint16_t* hrow = S.out + (size_t)row * S.ldo + TN * nt;
+#pragma unroll
+        for (int j = 0; j < CB; j++) {
+          const int cc = 16 * jb[j] + col;
+          hrow[cc] = (uint16_t)f2bf(bf2f(hrow[cc]) + rbf(tot[i][j][e]));
+        }
+        continue;
+      }
       if (EPI == EPI_PART) {
         static_assert(PART_HALF % TN == 0, "a tile lies in one column half");
         const int c0 = TN * nt;
@@ -1238,6 +1270,16 @@ static void gemm_gate_up(GemmArgs g, hipStream_t stream) {
     gemm<EPI_SILU, 128, 128, 3, 1, 4, 4>(g, I / 64, stream);
   }
 }
+// Long prompts: o_proj / down_proj with the residual add in the epilogue (the four k quarters
+// summed in order inside the workgroup: the same bits as the split-four partials and
+// resid_norm_rows), on 256 x 128 tiles; out = h, updated in place
+constexpr int RESADD_MIN_S = 7168;
+static void gemm_residual_add(GemmArgs g, uint16_t* h, hipStream_t stream) {
+  g.seg[0].out = h;
+  g.seg[0].ldo = H;
+  g.seg[0].ntiles = H / 128;
+  gemm<EPI_RESADD, 256, 128, 3, 1, 4, 2>(g, H / 128, stream);
+}
 static void gemm_residual(GemmArgs g, hipStream_t stream) {
   if (g.m >= 4096) {
     g.seg[0].ntiles = H / 256;
@@ -1344,10 +1386,16 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     GemmArgs go{};
     go.a = att; go.lda = QS; go.m = S; go.k = QS; go.nseg = 1;
     go.seg[0] = GemmSeg{bf(w.o_proj_weight), nullptr, nullptr, 0, H};
-    go.part = parts;
-    gemm_residual(go, stream);
-    chk();
-    resid_norm_rows<RES_SPLIT><<<S, 64, 0, stream>>>(parts, h, bf(w.post_attn_layernorm_weight), mln, S);
+    if (S >= RESADD_MIN_S) {
+      gemm_residual_add(go, h, stream);
+      chk();
+      rmsnorm_rows<<<S, 64, 0, stream>>>(h, bf(w.post_attn_layernorm_weight), mln, S);
+    } else {
+      go.part = parts;
+      gemm_residual(go, stream);
+      chk();
+      resid_norm_rows<RES_SPLIT><<<S, 64, 0, stream>>>(parts, h, bf(w.post_attn_layernorm_weight), mln, S);
+    }
     chk();
     GemmArgs gu{};
     gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
@@ -1357,12 +1405,18 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     GemmArgs gd{};
     gd.a = mid; gd.lda = I; gd.m = S; gd.k = I; gd.nseg = 1;
     gd.seg[0] = GemmSeg{bf(w.down_proj_weight), nullptr, nullptr, 0, H};
-    gd.part = parts;
-    gemm_residual(gd, stream);
-    chk();
-    // the next layer's input RMSNorm (none after the last: the final norm is the LM head's)
-    resid_norm_rows<RES_SPLIT><<<S, 64, 0, stream>>>(parts, h, l + 1 < num_layers ? bf(layer_weights[l + 1].input_layernorm_weight) : nullptr,
-                                          nrm, S);
+    // then the next layer's input RMSNorm (none after the last: the final norm is the LM head's)
+    if (S >= RESADD_MIN_S) {
+      gemm_residual_add(gd, h, stream);
+      chk();
+      if (l + 1 < num_layers) rmsnorm_rows<<<S, 64, 0, stream>>>(h, bf(layer_weights[l + 1].input_layernorm_weight), nrm, S);
+    } else {
+      gd.part = parts;
+      gemm_residual(gd, stream);
+      chk();
+      resid_norm_rows<RES_SPLIT><<<S, 64, 0, stream>>>(
+          parts, h, l + 1 < num_layers ? bf(layer_weights[l + 1].input_layernorm_weight) : nullptr, nrm, S);
+    }
     chk();
   }
   lm_partial<<<LMB, 256, 0, stream>>>(h + (size_t)(S - 1) * H, bf(final_norm_weight), bf(lm_head_weight),

@@ -106,7 +106,7 @@ def test_prefill_two_attention_blocks(state_dict, embed_gpu):
     assert rel_l2(hg, h) < 5e-3
 
 
-@pytest.mark.parametrize("S", [1100, 2100, 4200, 5400])
+@pytest.mark.parametrize("S", [1100, 2100, 4200, 5400, 7200])
 def test_prefill_long_tile_shapes_vs_oracle(state_dict, embed_gpu, S):
     """Prompts that take the larger GEMM tiles (q/k/v 128- and 256-row tiles, gate/up
     128 x 256 and 256 x 256, o_proj/down_proj 128 x 256 and 256 x 256) and the flash-form
