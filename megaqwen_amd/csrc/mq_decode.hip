@@ -159,6 +159,13 @@ constexpr uint32_t POLL_LIMIT = 1u << 21;  // ~1 s of polling before the watchdo
 // trip instead of every round trip, which shortens the time from a producer's store to the
 // consumer seeing it.
 constexpr int POLL_STAGGER = 4;
+// From this many context positions on (in the unsplit instance) group B's reduce waves
+// also sum the o_proj partials into h1, so that group A streams its next weights and K/V
+// rows right after its o_proj partials: its burst, which grows with the K/V rows, then lands
+// before the layer ends instead of holding up its own gather of h (CU loads complete in
+// order). Shorter contexts keep the reduction in group A, whose short burst would otherwise
+// overlap that cross-XCD reduction (measured crossover: 160-180 positions).
+constexpr int B_H1_MIN_CTX = 176;
 constexpr uint32_t ERR_POLL = 1u;
 constexpr uint32_t ERR_XCD = 2u;  // a workgroup ran on an XCD numbered 8 or above
 constexpr uint32_t ERR_STEP = 4u;  // a device-resident step found an invalid token, position or count
@@ -873,6 +880,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   // chunks of several passes (one-pass chunks of 257..4096-position contexts lose 1-9 us)
   const bool kv_nt = !SPLIT || npass > 1;
   const bool own_p = att && p >= c0 && p < c0 + nc;  // p is always in the last pass
+  // which group's reduce waves sum the o_proj partials (uniform across the grid)
+  const bool b_h1 = !SPLIT && n_ctx >= B_H1_MIN_CTX;
   const int prow = p - c0 - KV_CAP * (npass - 1);     // its LDS row there
   const uint32_t lds_kv = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)s_kv;
   auto pass_rows = [&](int ps) { return ps == npass - 1 ? nc - KV_CAP * ps : KV_CAP; };
@@ -1015,7 +1024,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         }
         // group A's quiet window: once this workgroup's reduce wave has stored its h1 rows,
         // group B carries the layer, and this workgroup streams its next layer's weights
-        wait_count(&s_red, (uint32_t)layer + 1u);
+        if (!b_h1) wait_count(&s_red, (uint32_t)layer + 1u);
         if (layer + 1 < L) {
           load_norms(layer + 1);
           load_a(layer + 1);
@@ -1375,6 +1384,13 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     BAR();  // P00
     BAR();  // P0
     const int row = ROWS * m + lane;
+    // group B with b_h1: this workgroup's 64 rows of the residual stream h (the embedding or
+    // hidden-input rows, then each layer's own down_proj reduction)
+    float hcur = 0.f;
+    if (!ga && b_h1) {
+      const uint16_t* src = (P.mode & MODE_INPUT_HIDDEN) ? P.hidden_in : P.embed + (size_t)token * H;
+      hcur = bf2f(ldraw16(src + row));
+    }
     for (int layer = 0; layer < L; layer++) {
       const uint32_t tag = tag_of(epoch, layer);
       const uint32_t tag64 = epoch * 32u + (uint32_t)layer + 1u;
@@ -1407,20 +1423,32 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         }
         BAR();  // C1
         MQ_STAMP(layer * 40 + 29);
-        // h1 = bf16(h + bf16(o)) (modeling_qwen3.py:297-298)
-        const float h1v = rbf(hrow + rbf(reduce_row8(wsb, ws, X_OPART + 2 * (m * NXCD * ROWS + lane), tag64)));
-        st1_plain(ws + lb + LX_H1 + row, tagged(tag, h1v));
-        // the stream waves' next weight loads go behind this store
-        if (lane == 0) signal_store(&s_red);
-        MQ_STAMP(layer * 40 + 30);
+        if (!b_h1) {
+          // h1 = bf16(h + bf16(o)) (modeling_qwen3.py:297-298)
+          const float h1v = rbf(hrow + rbf(reduce_row8(wsb, ws, X_OPART + 2 * (m * NXCD * ROWS + lane), tag64)));
+          st1_plain(ws + lb + LX_H1 + row, tagged(tag, h1v));
+          // the stream waves' next weight loads go behind this store
+          if (lane == 0) signal_store(&s_red);
+          MQ_STAMP(layer * 40 + 30);
+        }
       } else {
-        BAR();  // D1: h1 rows in s_hrow
-        const float h1row = s_hrow[lane];
+        float h1row;
+        if (b_h1) {
+          // h1 = bf16(h + bf16(o)) of the same 64 rows, from the o_proj partials
+          h1row = rbf(hcur + rbf(reduce_row8(wsb, ws, X_OPART + 2 * (m * NXCD * ROWS + lane), tag64)));
+          st1_plain(ws + lb + LX_H1 + row, tagged(tag, h1row));
+          MQ_STAMP(layer * 40 + 33);
+          BAR();  // D1
+        } else {
+          BAR();  // D1: h1 rows in s_hrow
+          h1row = s_hrow[lane];
+        }
         BAR();  // E1
         MQ_STAMP(layer * 40 + 31);
         // h' = bf16(h1 + bf16(down)) (modeling_qwen3.py:303-304)
         const float hn = rbf(h1row + rbf(reduce_row8(wsb, ws, X_DPART + 2 * (m * NXCD * ROWS + lane), tag64)));
         st1_plain(ws + lb + LX_H + row, tagged(tag, hn));
+        hcur = hn;
         if (lane == 0) signal_store(&s_red);
         MQ_STAMP(layer * 40 + 32);
       }

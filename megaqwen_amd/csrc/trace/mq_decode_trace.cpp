@@ -143,6 +143,8 @@ int main(int argc, char** argv) {
     const char* what;
   };
   const int A0 = 0, A1 = 16, B0 = 16, B1 = 32;
+  // the unsplit instance from B_H1_MIN_CTX positions: group B's reduce waves sum o_proj into h1
+  const bool b_h1 = pos + 1 <= mq::KV_CAP && pos + 1 >= mq::B_H1_MIN_CTX;
   const Stage st[] = {
       {"h gathered (group A poll waves)", 13, A0, A1, "hop: XCD-local all-gather of h, sum of squares"},
       {"A1: input RMSNorm done", 14, A0, A1, "compute: RMSNorm, barrier"},
@@ -159,7 +161,8 @@ int main(int argc, char** argv) {
       {"C1", 20, A0, A1, "barrier"},
       {"o_proj dot products handed over", 5, A0, A1, "compute: 64 rows x 256 per workgroup"},
       {"o_proj partials stored", 36, A0, A1, "store wave (sc1)"},
-      {"h1 rows stored (reduce waves)", 30, A0, A1, "hop: cross-XCD reduction of 8 partials"},
+      {"h1 rows stored (reduce waves)", b_h1 ? 33 : 30, b_h1 ? B0 : A0, b_h1 ? B1 : A1,
+       "hop: cross-XCD reduction of 8 partials"},
       {"h1 gathered (group B poll waves)", 21, B0, B1, "hop: XCD-local all-gather of h1"},
       {"D1: post-attention RMSNorm done", 22, B0, B1, "compute: RMSNorm, barrier"},
       {"gate/up dot products handed over", 7, B0, B1, "compute: 48 rows x 1024 per workgroup"},
@@ -223,7 +226,7 @@ int main(int argc, char** argv) {
   // m of every XCD) store their partials; latency from the last producer's store to the
   // reducer's store, and the spread of the producers' stores
   for (int grp = 0; grp < 2; grp++) {
-    const int kp = grp ? 38 : 36, kd = grp ? 32 : 30, j0 = grp ? 16 : 0;
+    const int kp = grp ? 38 : 36, kd = grp ? 32 : (b_h1 ? 33 : 30), j0 = grp ? 16 : 0, jd = grp || b_h1 ? 16 : 0;
     double lat = 0, spread = 0, lat_own = 0, cnt = 0;
     for (int l = 3; l <= 26; l++)
       for (int m = 0; m < 16; m++) {
@@ -234,8 +237,8 @@ int main(int argc, char** argv) {
         }
         spread += (double)(int32_t)(pmax - pmin) * 0.01;
         for (int g = 0; g < 8; g++) {
-          lat += (double)(int32_t)(T(8 * (j0 + m) + g, l, kd) - pmax) * 0.01;
-          lat_own += (double)(int32_t)(T(8 * (j0 + m) + g, l, kd) - T(8 * (j0 + m) + g, l, kp)) * 0.01;
+          lat += (double)(int32_t)(T(8 * (jd + m) + g, l, kd) - pmax) * 0.01;
+          lat_own += (double)(int32_t)(T(8 * (jd + m) + g, l, kd) - T(8 * (j0 + m) + g, l, kp)) * 0.01;
           cnt++;
         }
       }

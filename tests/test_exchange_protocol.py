@@ -44,8 +44,10 @@ def tag32(epoch, layer_plus_one):
 # "split1": only split launches with one attention chunk write it at every layer (the other
 # group-A workgroups read it there), every other launch clears it (tag 0) at its start; "chunks": chunk j is written at every layer by split
 # launches with j < nsplit, and cleared at the start of every launch that does not write it.
-# LX_H and LX_CUE_B are written by group B (h and its cue), LX_H1, LX_QKV, LX_ATT,
-# LX_PART and LX_CUE_A by group A, LX_M by group B; the cross-XCD arrays by both.
+# LX_H and LX_CUE_B are written by group B (h and its cue), LX_QKV, LX_ATT, LX_PART and
+# LX_CUE_A by group A, LX_M by group B; LX_H1 by the reduce waves of group A, or of group B
+# in unsplit launches of 176 or more positions (the same rows, member m's 64, either way);
+# the cross-XCD arrays by both.
 REGIONS = {
     "LX_H": ("16", "every"), "LX_H1": ("16", "every"), "LX_QKV": ("16", "every"), "LX_M": ("16", "every"),
     "LX_CUE_A": ("16", "every"), "LX_CUE_B": ("16", "every"),
