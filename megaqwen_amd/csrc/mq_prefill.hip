@@ -29,6 +29,12 @@
 #include "megaqwen_amd.h"
 #include "mq_common.h"
 
+// Instrumentation hook of a tracing build: MQ_PF_STAMP(slot) marks a point of a kernel's
+// timeline; it compiles to nothing unless a tracing harness defines it first.
+#ifndef MQ_PF_STAMP
+#define MQ_PF_STAMP(i) ((void)0)
+#endif
+
 namespace mq {
 
 int current_workspace(uint32_t** ws);  // mq_decode.hip: this device's library workspace
@@ -220,56 +226,112 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
     // QK-norm (per head over 128, weights q_norm/k_norm) and RoPE (modeling_qwen3.py:247-257,
     // rotate_half form, three bf16 ops) of the tile's rows, which are tokens m0.. of head
     // nt of segment si (q, k or v); per token the reference's ldg_qk_norm_rope_cache
-    // (fused_decode_ldg.cu:166-276) for a whole prompt
-    static_assert(TN == HD && TM * (HD + 1) * 4 <= NST * KS * SCH * 16, "a tile is one head and fits the ring");
-    float* tile = reinterpret_cast<float*>(&sbuf[0][0][0]);  // [TM][HD + 1] bf16-rounded outputs
+    // (fused_decode_ldg.cu:166-276) for a whole prompt. The bf16-rounded outputs go through
+    // LDS ([TM][QP] fp32: the pitch puts the 64 lanes of a fragment store in 64 banks and keeps
+    // rows 16-byte aligned); then eight lanes take a row, lane p of them dims 8 p .. 8 p + 7
+    // and their rotation partners 64 + 8 p .. + 7, with 16-byte loads and stores.
+    constexpr int QP = HD + 4, RPI = 8 * NW;  // tile pitch (floats); rows per pass of the workgroup
+    static_assert(TN == HD && TM * QP * 4 <= NST * KS * SCH * 16 && TM % RPI == 0, "a tile is one head and fits the ring");
+    float* tile = reinterpret_cast<float*>(&sbuf[0][0][0]);
     __syncthreads();  // every wave is past its last read of the ring
 #pragma unroll
     for (int i = 0; i < RB; i++)
 #pragma unroll
       for (int e = 0; e < 4; e++)
 #pragma unroll
-        for (int j = 0; j < CB; j++) tile[(16 * (RB * wm + i) + rq + e) * (HD + 1) + 16 * jb[j] + col] = rbf(acc[i][j][e]);
+        for (int j = 0; j < CB; j++) tile[(16 * (RB * wm + i) + rq + e) * QP + 16 * jb[j] + col] = rbf(acc[i][j][e]);
     __syncthreads();
     const QknArgs& Q = G.qkn;
-    const int h = nt;
-    constexpr int RPW = TM / NW;  // rows per wave: wave wv takes rows wv + NW i
+    const int h = nt, pd = 8 * (lane & 7), rr = lane >> 3;
+    constexpr int NPASS = TM / RPI;
+    auto bf8 = [](const u32x4 v, float (&f)[8]) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        f[2 * e] = bf2f(v[e] & 0xffffu);
+        f[2 * e + 1] = bf2f(v[e] >> 16);
+      }
+    };
     if (si == 2) {
-      for (int i = 0; i < RPW; i++) {
-        const int r = wv + NW * i, t = m0 + r;  // token (cache slot); wave-uniform
-        if (t >= G.m) break;
+      // v rows: a copy (exact: the tile holds bf16 values)
+#pragma unroll
+      for (int it = 0; it < NPASS; it++) {
+        const int r = RPI * it + 8 * wv + rr, t = m0 + r;
+        if (t >= G.m) continue;
+        const float* x = tile + r * QP;
         uint16_t* dst = Q.vc + ((size_t)h * Q.max_seq + t) * HD;
-        dst[lane] = (uint16_t)f2bf(tile[r * (HD + 1) + lane]);  // exact: x is a bf16 value
-        dst[64 + lane] = (uint16_t)f2bf(tile[r * (HD + 1) + 64 + lane]);
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(x + 64 * half + pd);
+          const f32x4 b = *reinterpret_cast<const f32x4*>(x + 64 * half + pd + 4);
+          *reinterpret_cast<u32x4*>(dst + 64 * half + pd) =
+              u32x4{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3]), pack_bf2(b[0], b[1]), pack_bf2(b[2], b[3])};
+        }
       }
       return;
     }
-    // every row's cos/sin and the norm weights first: one memory round trip, not one a row
+    // every pass's cos/sin and the norm weights first: one memory round trip
     const uint16_t* nwp = si == 0 ? Q.qn : Q.kn;
-    const float w1 = bf2f(nwp[lane]), w2 = bf2f(nwp[64 + lane]);
-    float cs[RPW][4];
+    float w1[8], w2[8];
+    bf8(ldw(nwp + pd), w1);
+    bf8(ldw(nwp + 64 + pd), w2);
+    u32x4 cs[NPASS][4];
 #pragma unroll
-    for (int i = 0; i < RPW; i++) {
-      const size_t t = (size_t)min(m0 + wv + NW * i, G.m - 1) * HD;  // rows past the prompt: never stored
-      cs[i][0] = bf2f(Q.cos_t[t + lane]);
-      cs[i][1] = bf2f(Q.cos_t[t + 64 + lane]);
-      cs[i][2] = bf2f(Q.sin_t[t + lane]);
-      cs[i][3] = bf2f(Q.sin_t[t + 64 + lane]);
+    for (int it = 0; it < NPASS; it++) {
+      const size_t t = (size_t)min(m0 + RPI * it + 8 * wv + rr, G.m - 1) * HD;  // rows past the prompt: never stored
+      cs[it][0] = ldw(Q.cos_t + t + pd);
+      cs[it][1] = ldw(Q.cos_t + t + 64 + pd);
+      cs[it][2] = ldw(Q.sin_t + t + pd);
+      cs[it][3] = ldw(Q.sin_t + t + 64 + pd);
     }
 #pragma unroll
-    for (int i = 0; i < RPW; i++) {
-      const int r = wv + NW * i, t = m0 + r;
-      if (t >= G.m) break;
-      const float x1 = tile[r * (HD + 1) + lane], x2 = tile[r * (HD + 1) + 64 + lane];
-      float ss[1] = {x1 * x1 + x2 * x2};
-      wave_sum_n(ss);
-      const float rstd = 1.0f / sqrtf(ss[0] * (1.0f / HD) + EPS);
-      const float n1 = rbf(w1 * rbf(x1 * rstd)), n2 = rbf(w2 * rbf(x2 * rstd));
-      const float o1 = rbf(rbf(n1 * cs[i][0]) - rbf(n2 * cs[i][2]));
-      const float o2 = rbf(rbf(n2 * cs[i][1]) + rbf(n1 * cs[i][3]));
+    for (int it = 0; it < NPASS; it++) {
+      const int r = RPI * it + 8 * wv + rr, t = m0 + r;
+      const float* x = tile + r * QP;
+      float x1[8], x2[8];
+#pragma unroll
+      for (int e = 0; e < 8; e += 4) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(x + pd + e);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(x + 64 + pd + e);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          x1[e + u] = a[u];
+          x2[e + u] = b[u];
+        }
+      }
+      // sum of squares over the head in a fixed tree: v_d = x_d^2 + x_(d+64)^2, eight
+      // consecutive d summed as ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7)) in the lane,
+      // then the eight lanes' sums as ((g0 + g1) + (g2 + g3)) + ((g4 + g5) + (g6 + g7)) by
+      // xor 1, xor 2 and the half-row mirror (every lane of the row ends with the same sum)
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = x1[e] * x1[e] + x2[e] * x2[e];
+      float ss = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+      ss += dpp<0xB1>(ss);
+      ss += dpp<0x4E>(ss);
+      ss += dpp<0x141>(ss);
+      const float rstd = 1.0f / sqrtf(ss * (1.0f / HD) + EPS);
+      float c1[8], c2[8], s1[8], s2[8];
+      bf8(cs[it][0], c1);
+      bf8(cs[it][1], c2);
+      bf8(cs[it][2], s1);
+      bf8(cs[it][3], s2);
+      uint32_t o1[4], o2[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float r1[2], r2[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          const float n1 = rbf(w1[e + u] * rbf(x1[e + u] * rstd)), n2 = rbf(w2[e + u] * rbf(x2[e + u] * rstd));
+          r1[u] = rbf(rbf(n1 * c1[e + u]) - rbf(n2 * s1[e + u]));
+          r2[u] = rbf(rbf(n2 * c2[e + u]) + rbf(n1 * s2[e + u]));
+        }
+        o1[e / 2] = pack_bf2(r1[0], r1[1]);
+        o2[e / 2] = pack_bf2(r2[0], r2[1]);
+      }
+      if (t >= G.m) continue;
       uint16_t* dst = si == 0 ? Q.q_out + (size_t)t * QS + HD * h : Q.kc + ((size_t)h * Q.max_seq + t) * HD;
-      dst[lane] = (uint16_t)f2bf(o1);
-      dst[64 + lane] = (uint16_t)f2bf(o2);
+      *reinterpret_cast<u32x4*>(dst + pd) = u32x4{o1[0], o1[1], o1[2], o1[3]};
+      *reinterpret_cast<u32x4*>(dst + 64 + pd) = u32x4{o2[0], o2[1], o2[2], o2[3]};
     }
     return;
   }
@@ -438,15 +500,21 @@ __global__ void __launch_bounds__(64) resid_norm_rows(PartSet ps, uint16_t* h, c
 // scores (MFMA) -> LDS; per-row max, exp and sum with the running maximum -> bf16
 // probabilities in LDS; P.V on MFMA with the accumulator rescaled by exp(m_old - m_new).
 //
-// K and V rows reach LDS by 1 KB DMA instructions (four whole rows each), 64 keys at a
-// time through two buffers, one chunk in flight while the previous one is used: loading
-// MFMA operands straight from global memory would touch 16 rows per instruction, which
-// streams at a third of the rate. A row's eight-dim chunk c sits in slot c ^ (row & 15),
-// so the 16 rows of a score fragment read hit distinct banks; P.V reads V with transpose
-// reads (ds_read_b64_tr_b16), so V needs no transposed copy.
+// Eight waves. Scores: wave w takes keys 16 (w % 4) .. +15 of every other 64-key chunk
+// (parity w / 4) and loads those K rows straight into registers as the MFMA operand, all
+// four chunks' loads issued back to back before the first product (a short prompt's
+// attention is latency-bound: one round trip for the whole block instead of one per
+// chunk through an LDS ring); the scores go to LDS for the row-wise softmax (four rows a
+// wave). P.V: wave w owns dims 16 w .. 16 w + 15. V rows reach LDS by 1 KB DMA instructions
+// (four whole rows each): chunks 0..2 into three buffers at the block's start, chunks 3..6
+// into the score rows' space once the softmax has read it, chunk 7 into buffer 0 once chunk
+// 0 is consumed, so the whole block's V is in flight at once. A row's eight-dim chunk c sits
+// in slot c ^ (row & 15), so the 16 rows of a fragment read hit distinct banks; P.V reads V
+// with transpose reads (ds_read_b64_tr_b16), so V needs no transposed copy.
 constexpr int AQ = 32;
 constexpr int AKB = 512;
 constexpr int ACK = 64;  // keys per LDS chunk
+constexpr int AW = 8;    // waves a workgroup
 // LDS row pitches: a P row is padded by 16 bytes so that the 16 rows a quarter-wave
 // reads in one P.V fragment load fall in distinct bank groups (unpadded, 1 KB rows
 // share their banks), and a score row by one word, which spreads the score writes
@@ -470,8 +538,8 @@ __device__ __forceinline__ float unfused(float x) {
 // row 4q + lane / 16, slot lane % 16.
 __device__ __forceinline__ void kv_chunk(const uint16_t* src, int k0, int klast, uint32_t lds, int wv, int lane) {
 #pragma unroll
-  for (int i = 0; i < ACK / 16; i++) {
-    const int q = wv + 4 * i, row = 4 * q + (lane >> 4), chunk = (lane & 15) ^ (row & 15);
+  for (int i = 0; i < ACK / 4 / AW; i++) {
+    const int q = wv + AW * i, row = 4 * q + (lane >> 4), chunk = (lane & 15) ^ (row & 15);
     dma16(src + (size_t)min(k0 + row, klast) * HD + 8 * chunk, __builtin_amdgcn_readfirstlane(lds + 1024u * q));
   }
 }
@@ -480,13 +548,14 @@ __device__ __forceinline__ void kv_chunk(const uint16_t* src, int k0, int klast,
 #define AWAIT(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
 #define ABAR() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
-__global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
-                                                    uint16_t* out, int S, int max_seq, float scale) {
+__global__ void __launch_bounds__(64 * AW) attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                                                       uint16_t* out, int S, int max_seq, float scale) {
   typedef short v4s __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) v4s lds_v4s;
+  constexpr int RPW = AQ / AW;  // softmax rows per wave
   __shared__ float s_sc[AQ][SC_PITCH];
   __shared__ __align__(16) uint16_t s_p[AQ][P_PITCH];
-  __shared__ __align__(16) uint8_t s_kv[2][ACK * 256];
+  __shared__ __align__(16) uint8_t s_kv[3][ACK * 256];  // V chunk ring
   __shared__ float s_m[AQ], s_l[AQ], s_a[AQ];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   // XCD-aware order: workgroup id runs on XCD id % 8, which is made the KV group g, so the
@@ -499,6 +568,9 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
   const int nkey = min(S, r0 + AQ);
   const int r16 = lane & 15, kg = lane >> 4;
   const uint32_t kv0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_kv[0][0];
+  MQ_PF_STAMP(0);
+  // the scores: wave wv takes keys 16 (wv % 4) .. +15 of the chunks c with c % 2 == wv / 4
+  const int kw = wv & 3, kpar = wv >> 2;
 
   u32x4 qf[2][4];
 #pragma unroll
@@ -512,61 +584,70 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
     s_m[tid] = -INFINITY;
     s_l[tid] = 0.f;
   }
-  f32x4 oacc[2][2];
+  f32x4 oacc[2];
 #pragma unroll
-  for (int rb = 0; rb < 2; rb++)
-#pragma unroll
-    for (int db = 0; db < 2; db++) oacc[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int rb = 0; rb < 2; rb++) oacc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int kb0 = 0; kb0 < nkey; kb0 += AKB) {
     const int kb1 = min(nkey, kb0 + AKB), nk = kb1 - kb0, nk32 = (nk + 31) & ~31;
     const int nch = (nk + ACK - 1) / ACK;
-    // ---- scores: chunk c (keys kb0 + 64c ..), wave wv takes its 16 keys 16 wv .. of it
-    kv_chunk(K, kb0, kb1 - 1, kv0, wv, lane);
-    for (int c = 0; c < nch; c++) {
-      AWAIT(0);  // chunk c (the only one in flight)
-      ABAR();    // ... for every wave, which are also done with chunk c - 1's buffer
-      if (c + 1 < nch) kv_chunk(K, kb0 + ACK * (c + 1), kb1 - 1, kv0 + ((c + 1) & 1) * ACK * 256, wv, lane);
-      const uint8_t* kb = s_kv[c & 1];
-      const int row = 16 * wv + r16, key = kb0 + ACK * c + row;
-      u32x4 kf[4];
+    // the block's first three V chunks into the three buffers, in flight during the scores
+    // (issued before the K loads below, so they have landed once those have)
 #pragma unroll
-      for (int ks = 0; ks < 4; ks++) kf[ks] = *reinterpret_cast<const u32x4*>(kb + akv_off(row, 4 * ks + kg));
+    for (int v = 0; v < 3; v++)
+      if (v < nch) kv_chunk(V, kb0 + ACK * v, kb1 - 1, kv0 + v * ACK * 256, wv, lane);
+    // ---- scores: the K rows go straight into registers as the MFMA operand (lane: key row
+    // 16 kw + r16 of the chunk, dims 32 ks + 8 kg .. +7), all of the wave's chunks at once
+    // (unconditional, past the block's keys too: those rows repeat its last key and their
+    // scores are masked, and straight-line loads let the compiler keep them all in flight)
+    u32x4 kf[AKB / ACK / 2][4];
 #pragma unroll
-      for (int rb = 0; rb < 2; rb++) {
-        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < AKB / ACK / 2; i++) {
+      const int c = 2 * i + kpar;
+      const int krow = min(kb0 + ACK * c + 16 * kw + r16, kb1 - 1);
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) a = mfma_16x16x32(qf[rb][ks], kf[ks], a);
+      for (int ks = 0; ks < 4; ks++) kf[i][ks] = ldw(K + (size_t)krow * HD + 32 * ks + 8 * kg);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every K load issued before the first product
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int rl = 16 * rb + 4 * kg + e;
-          s_sc[rl][ACK * c + row] = (key <= r0 + rl && key < kb1) ? a[e] * scale : -INFINITY;
+    for (int i = 0; i < AKB / ACK / 2; i++) {
+      const int c = 2 * i + kpar;
+      {
+        const int row = 16 * kw + r16, key = kb0 + ACK * c + row;
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++) {
+          f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ks++) a = mfma_16x16x32(qf[rb][ks], kf[i][ks], a);
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int rl = 16 * rb + 4 * kg + e;
+            s_sc[rl][ACK * c + row] = (key <= r0 + rl && key < kb1) ? a[e] * scale : -INFINITY;
+          }
         }
       }
     }
-    ABAR();  // scores complete, K buffers free
-    // the block's first two V chunks, in flight during the softmax
+    ABAR();  // scores complete
+    MQ_PF_STAMP(1);
     const int ncv = nk32 / ACK + ((nk32 & (ACK - 1)) != 0);
-    kv_chunk(V, kb0, kb1 - 1, kv0, wv, lane);
-    if (ncv > 1) kv_chunk(V, kb0 + ACK, kb1 - 1, kv0 + ACK * 256, wv, lane);
-    // ---- softmax of rows 8 wv .. 8 wv + 7, all eight at once (the LDS reads of every row
-    // are issued together and the reductions interleaved); lane takes keys lane + 64 u
+    // ---- softmax of rows RPW wv .. RPW wv + RPW - 1, all at once (the LDS reads of every
+    // row are issued together and the reductions interleaved); lane takes keys lane + 64 u
     {
-      float x[8][AKB / 64], mx[8], sum[8];
+      float x[RPW][AKB / 64], mx[RPW], sum[RPW];
 #pragma unroll
-      for (int i = 0; i < 8; i++)
+      for (int i = 0; i < RPW; i++)
 #pragma unroll
-        for (int u = 0; u < AKB / 64; u++) x[i][u] = s_sc[8 * wv + i][lane + 64 * u];  // past nk: unused
+        for (int u = 0; u < AKB / 64; u++) x[i][u] = s_sc[RPW * wv + i][lane + 64 * u];  // past nk: unused
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
+      for (int i = 0; i < RPW; i++) {
         mx[i] = -INFINITY;
 #pragma unroll
         for (int u = 0; u < AKB / 64; u++) mx[i] = fmaxf(mx[i], lane + 64 * u < nk ? x[i][u] : -INFINITY);
       }
       wave_max_n(mx);
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const int rl = 8 * wv + i;
+      for (int i = 0; i < RPW; i++) {
+        const int rl = RPW * wv + i;
         const float mn = fmaxf(s_m[rl], mx[i]);
         const float base = mn == -INFINITY ? 0.f : mn;
         sum[i] = 0.f;
@@ -585,8 +666,8 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
       wave_sum_n(sum);
       if (lane == 0)
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const int rl = 8 * wv + i;
+        for (int i = 0; i < RPW; i++) {
+          const int rl = RPW * wv + i;
           const float mo = s_m[rl], mn = mx[i], base = mn == -INFINITY ? 0.f : mn;
           const float al = mo == -INFINITY ? 0.f : expf(mo - base);
           s_m[rl] = mn;
@@ -594,50 +675,57 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
           s_a[rl] = al;
         }
     }
-    ABAR();  // s_p, s_a
-    // ---- P.V: wave wv owns dims 32 wv .. 32 wv + 31 (two 16-dim blocks)
+    ABAR();  // s_p, s_a; every wave is done with s_sc
+    MQ_PF_STAMP(2);
+    // V chunks 3..6 into the score rows' LDS, now dead (chunk 7 follows into buffer 0 once
+    // chunk 0 is consumed): the whole block's V rows in flight at once
+    const uint32_t scb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_sc[0][0];
+    auto vslot = [&](int c) { return c < 3 ? kv0 + c * ACK * 256 : c < 7 ? scb + (c - 3) * ACK * 256 : kv0; };
+#pragma unroll
+    for (int c = 3; c < 7; c++)
+      if (c < ncv) kv_chunk(V, kb0 + ACK * c, kb1 - 1, vslot(c), wv, lane);
+    // ---- P.V: wave wv owns dims 16 wv .. 16 wv + 15
 #pragma unroll
     for (int rb = 0; rb < 2; rb++)
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float al = s_a[16 * rb + 4 * kg + e];
-        oacc[rb][0][e] *= al;
-        oacc[rb][1][e] *= al;
-      }
+      for (int e = 0; e < 4; e++) oacc[rb][e] *= s_a[16 * rb + 4 * kg + e];
+    static_assert(AKB / ACK == 8 && ACK / 4 / AW == 2, "the V schedule below assumes 8 chunks, 2 DMAs a wave each");
     for (int c = 0; c < ncv; c++) {
-      // chunk c landed (for c = 0, chunk 1 may still be in flight)
-      if (c == 0 && ncv > 1)
-        AWAIT(ACK / 16);
-      else
-        AWAIT(0);
+      // chunk c landed: chunks 0..2 before the K loads did; for c >= 3 every later chunk of
+      // the block has been issued after it (chunk 7 at c = 1), two DMAs a wave each
+      if (c >= 3) {
+        switch (ncv - 1 - c) {
+          case 4: AWAIT(8); break;
+          case 3: AWAIT(6); break;
+          case 2: AWAIT(4); break;
+          case 1: AWAIT(2); break;
+          default: AWAIT(0); break;
+        }
+      }
       ABAR();  // ... for every wave, which are also done with chunk c - 1's buffer
-      if (c >= 1 && c + 1 < ncv) kv_chunk(V, kb0 + ACK * (c + 1), kb1 - 1, kv0 + ((c + 1) & 1) * ACK * 256, wv, lane);
-      const uint32_t vb = kv0 + (c & 1) * ACK * 256;
+      if (c == 1 && ncv > 7) kv_chunk(V, kb0 + ACK * 7, kb1 - 1, vslot(7), wv, lane);
+      const uint32_t vb = vslot(c);
       for (int kk = 0; kk < 2 && ACK * c + 32 * kk < nk32; kk++) {
         // B operand (8 keys of one dim per lane) from two transpose reads: within each
         // 16-lane group, lane j addresses key base + j / 4, dims 4 (j % 4) .. +3 of the
         // 16-dim block, and lane i receives that dim's 4 keys
         const int ra = 32 * kk + 8 * kg + (r16 >> 2);
-        u32x4 vf[2];
-#pragma unroll
-        for (int db = 0; db < 2; db++) {
-          const int dq = 32 * wv + 16 * db + 4 * (r16 & 3);
-          const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_v4s*)(uintptr_t)(vb + akv_off(ra, dq >> 3) + 2 * (dq & 7)));
-          const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_v4s*)(uintptr_t)(vb + akv_off(ra + 4, dq >> 3) + 2 * (dq & 7)));
-          const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-          vf[db] = u32x4{l2.x, l2.y, h2.x, h2.y};
-        }
+        const int dq = 16 * wv + 4 * (r16 & 3);
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4s*)(uintptr_t)(vb + akv_off(ra, dq >> 3) + 2 * (dq & 7)));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4s*)(uintptr_t)(vb + akv_off(ra + 4, dq >> 3) + 2 * (dq & 7)));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+        const u32x4 vf = u32x4{l2.x, l2.y, h2.x, h2.y};
 #pragma unroll
         for (int rb = 0; rb < 2; rb++) {
           const u32x4 pfr = *reinterpret_cast<const u32x4*>(&s_p[16 * rb + r16][ACK * c + 32 * kk + 8 * kg]);
-          oacc[rb][0] = mfma_16x16x32(pfr, vf[0], oacc[rb][0]);
-          oacc[rb][1] = mfma_16x16x32(pfr, vf[1], oacc[rb][1]);
+          oacc[rb] = mfma_16x16x32(pfr, vf, oacc[rb]);
         }
       }
     }
     ABAR();  // V buffers and s_p free for the next key block
+    MQ_PF_STAMP(3);
   }
 #pragma unroll
   for (int rb = 0; rb < 2; rb++)
@@ -646,9 +734,7 @@ __global__ void __launch_bounds__(256) attn_prefill(const uint16_t* q, const uin
       const int rl = 16 * rb + 4 * kg + e, row = r0 + rl;
       if (row >= S) continue;
       const float inv = 1.0f / s_l[rl];
-      uint16_t* o = out + (size_t)row * QS + HD * h + 32 * wv + r16;
-      o[0] = (uint16_t)f2bf(oacc[rb][0][e] * inv);
-      o[16] = (uint16_t)f2bf(oacc[rb][1][e] * inv);
+      out[(size_t)row * QS + HD * h + 16 * wv + r16] = (uint16_t)f2bf(oacc[rb][e] * inv);
     }
 }
 
@@ -1381,7 +1467,7 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     else if (S > FLASH_MIN_S)
       attn_prefill_fa<4><<<NKV * ((S + 63) / 64), 512, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
     else
-      attn_prefill<<<NQ * ((S + AQ - 1) / AQ), 256, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
+      attn_prefill<<<NQ * ((S + AQ - 1) / AQ), 64 * AW, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
     chk();
     GemmArgs go{};
     go.a = att; go.lda = QS; go.m = S; go.k = QS; go.nseg = 1;
