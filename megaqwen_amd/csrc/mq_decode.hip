@@ -69,7 +69,9 @@
 
 // Instrumentation hooks: MQ_STAMP(slot) marks a point of a layer's timeline
 // (slot = layer * 40 + event; stream events 0..11, poll 12..27, reduce 28..32,
-// store 34..38; slots 32 * 40 .. +3 the final norm and LM head), MQ_STAMP_DUMP()
+// store 34..38; slots 32 * 40 .. +3 the final norm and LM head; a workgroup keeps its
+// own slots, so group A's attention reuses 21..23, which only group B writes otherwise),
+// MQ_STAMP_DUMP()
 // runs once at the end of the kernel. Both compile to nothing unless a tracing build
 // (csrc/trace/mq_decode_trace.cpp) defines them before including this file.
 #ifndef MQ_STAMP
@@ -1238,13 +1240,16 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             BAR();  // B1
             MQ_STAMP(layer * 40 + 16);
             attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
+            MQ_STAMP(layer * 40 + 21);  // (slots 21..23: group B's elsewhere)
             BAR();  // B2
             MQ_STAMP(layer * 40 + 26);
             float M0, M1, L0, L1;
             attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
+            MQ_STAMP(layer * 40 + 22);
             BAR();  // B3
             MQ_STAMP(layer * 40 + 27);
             attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+            MQ_STAMP(layer * 40 + 23);
             BAR();  // B4
           }
           MQ_STAMP(layer * 40 + 17);

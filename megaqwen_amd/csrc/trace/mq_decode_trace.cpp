@@ -203,6 +203,21 @@ int main(int argc, char** argv) {
     prev = end[i];
   }
   printf("\nLayer period (XCD's last h store to the next): %.2f us; hop stages add up to %.2f us.\n", per, hop);
+  if (nsplit == 1) {
+    // the attention's phases in the workgroups that run it (group A; slots 21..23 are
+    // group B's elsewhere): the latest of waves 0, 4, 6, 7 done with the phase's work, then
+    // the barrier that ends the phase
+    const int ks[7] = {16, 21, 26, 22, 27, 23, 17};
+    double d[6] = {0, 0, 0, 0, 0, 0}, cnt = 0;
+    for (int l = 3; l <= 26; l++)
+      for (int w = 0; w < 8 * 16; w++) {
+        for (int i = 0; i < 6; i++) d[i] += (double)(int32_t)(T(w, l, ks[i + 1]) - T(w, l, ks[i])) * 0.01;
+        cnt++;
+      }
+    printf("attention phases (workgroup means): scores %.2f us + barrier %.2f; softmax %.2f + barrier %.2f; "
+           "P.V %.2f + barrier %.2f\n",
+           d[0] / cnt, d[1] / cnt, d[2] / cnt, d[3] / cnt, d[4] / cnt, d[5] / cnt);
+  }
   // the residual-stream gathers in detail: cue seen, first poll returned, gathered, re-polls
   for (int grp = 0; grp < 2; grp++) {
     const int j0 = grp ? 16 : 0, j1 = grp ? 32 : 16;
