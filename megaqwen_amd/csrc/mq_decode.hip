@@ -69,7 +69,8 @@
 
 // Instrumentation hooks: MQ_STAMP(slot) marks a point of a layer's timeline
 // (slot = layer * 40 + event; stream events 0..11, poll 12..27, reduce 28..32,
-// store 34..38; slots 32 * 40 .. +3 the final norm and LM head; a workgroup keeps its
+// store 34..38; slots 32 * 40 .. +3 the final norm and LM head, + 4 the kernel's entry;
+// a workgroup keeps its
 // own slots, so group A's attention reuses 21..23, which only group B writes otherwise),
 // MQ_STAMP_DUMP()
 // runs once at the end of the kernel. Both compile to nothing unless a tracing build
@@ -840,6 +841,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   const Buf wsb(ws);
   // token, position, epoch: kernel arguments, or a device-resident step written by the
   // previous launch's last workgroup (visible at this launch's start)
+  MQ_STAMP(32 * 40 + 4);
   int token = P.token, p = P.position, step_count = 0;
   uint32_t epoch = P.epoch;
   if (P.mode & MODE_DEVICE_STEP) {

@@ -279,6 +279,32 @@ int main(int argc, char** argv) {
     printf("bursts landed (stream wave 0, workgroup means): group A's next-layer weights and K/V at %.2f us of the "
            "layer; group B's at %.2f us of the next layer\n", a / ca, b / cb);
   }
+  // the launch's start: entry (earliest and latest workgroup), the first layers' periods
+  {
+    int64_t e0 = INT64_MAX, e1 = INT64_MIN;
+    for (int w = 0; w < 256; w++) {
+      e0 = std::min(e0, T(w, 32, 4));
+      e1 = std::max(e1, T(w, 32, 4));
+    }
+    double l0 = 0, l1 = 0, l2 = 0, ll = 0;
+    for (int g = 0; g < 8; g++) {
+      l0 += (double)(int32_t)(T0(1, g) - e0) * 0.01 / 8;
+      l1 += (double)(int32_t)(T0(2, g) - T0(1, g)) * 0.01 / 8;
+      l2 += (double)(int32_t)(T0(3, g) - T0(2, g)) * 0.01 / 8;
+      ll += (double)(int32_t)(T0(28, g) - T0(27, g)) * 0.01 / 8;
+    }
+    printf("launch start: workgroups enter within %.2f us; first entry to layer 0's last h store %.2f us; "
+           "layers 1, 2 and 27 take %.2f, %.2f and %.2f us\n",
+           (double)(int32_t)(e1 - e0) * 0.01, l0, l1, l2, ll);
+    // layer 0's stages from the first entry (XCD means)
+    printf("layer 0 from the first entry (us):");
+    for (int i = 0; i < nst; i++) {
+      double e = 0;
+      for (int g = 0; g < 8; g++) e += (double)(int32_t)(last(g, 0, st[i].k, st[i].j0, st[i].j1) - e0) * 0.01 / 8;
+      printf(" [%d] %.2f", i + 1, e);
+    }
+    printf("\n");
+  }
   // final norm and LM head
   double fin = 0, lm = 0;
   int64_t first = INT64_MAX, lastf2 = INT64_MIN;
