@@ -953,10 +953,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       // ---- prologue: layer-0 norms, weights and K/V rows
       load_norms(0);
       load_a(0);
-      load_o(0);
       put_norms();
       BAR();  // P0
       if (att) kv_dma(kv_nt, P, 0, g, c0, nc0, p, lds_kv, s, lane);
+      load_o(0);  // (needed after the attention)
       for (int layer = 0; layer < L; layer++) {
         // ---------------- q/k/v rows 32m + 8s .. +7 of the group's [q0; q1; k; v]
         BAR();  // A1: normed h in s_x0
@@ -1070,11 +1070,14 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       };
       // ---- prologue: layer-0 post-attention norm and weights (streamed during group A's
       // first layer)
+      // the norm weights alone first: the layer-0 MLP weights (needed only once group A's
+      // attention is done) go out after the prologue barrier, so that the first q/k/v rows
+      // and norm weights of every workgroup meet less traffic
       R.wpost = ldw2(wp(0, W_POST) + 4 * st);
-      load_gu(0);
-      load_d(0);
       put_norms();
       BAR();  // P0
+      load_gu(0);
+      load_d(0);
       for (int layer = 0; layer < L; layer++) {
         // ---------------- gate/up rows of units 384g + 24m + 6s .. +5
         BAR();  // D1: normed h1 in s_x0
