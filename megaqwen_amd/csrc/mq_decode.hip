@@ -29,13 +29,14 @@
 // rows, so that the burst has landed before the other group's cross-XCD reduction.
 //
 // Every workgroup runs four roles, one per wave kind:
-//   * stream waves 0-3 hold the group's weight slice in registers and compute the
-//     dot products, handing them to the store wave through LDS;
+//   * stream waves 0-3 hold the group's weight slice in registers, compute the dot
+//     products and store them (a wave's rows regrouped through its own LDS slots);
 //   * poll waves 4-5 gather the XCD-local exchanges (h, q/k/v, attention output,
 //     h1, m), normalise, apply QK-norm and RoPE, and merge attention chunks;
 //   * reduce wave 6 sums the eight XCDs' partials of the workgroup's 64 residual
 //     rows and applies the residual add;
-//   * store wave 7 publishes the dot products and appends the new K/V row.
+//   * store wave 7 appends the new K/V row, stores the attention output and the
+//     stage cues, and clears the words a launch does not write.
 // A layer has five XCD-local all-gathers and two cross-XCD reductions and no grid
 // barrier. The kernel has two instances: SPLIT = false for contexts of at most 256
 // positions (one attention workgroup per XCD, no chunk merge compiled in) and
@@ -328,12 +329,16 @@ __device__ __forceinline__ void kv_dma(bool nt, const DecodeParams& P, int layer
 
 // ---- exchange stores: inline assembly, so that the compiler's vmcnt bookkeeping for
 // the stream waves' register loads ignores them (each makes a later wait at most one
-// instruction longer). Only the store and reduce waves store inside the layer loop, and
-// each of them stores after its last poll of the stage, so no poll queues behind a
+// instruction longer). The stream waves store their dot products (q/k/v rows, o_proj and
+// down_proj partials, m) as soon as they have them, before their next weight burst; the
+// reduce waves store after their last poll of the stage, so no poll queues behind a
 // store's write acknowledgement. `dev` stores (sc1) write through to memory for readers
 // on other XCDs; plain stores stay in this XCD's L2.
 __device__ __forceinline__ void st2_dev(uint32_t* p, u32x2 v) {
   asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st2_plain(uint32_t* p, u32x2 v) {
+  asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
 }
 __device__ __forceinline__ void st1_plain(uint32_t* p, uint32_t v) {
   asm volatile("global_store_dword %0, %1, off" ::"v"(p), "v"(v) : "memory");
@@ -967,10 +972,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
 #pragma unroll
           for (int k = 0; k < 8; k++) r[k] = dot_chunk(R.a[2 * k], x0, dot_chunk(R.a[2 * k + 1], x1, 0.f));
           wave_sum_t(r);  // lane 16q holds rows 2q, 2q + 1
-          if ((lane & 15) == 0) {
-            s_res[8 * s + 2 * (lane >> 4)] = r[0];
-            s_res[8 * s + 2 * (lane >> 4) + 1] = r[1];
-          }
+          // the wave publishes its own 8 rows (tagged, bf16), no hand-off to the store wave
+          if ((lane & 15) == 0)
+            st2_plain(ws + lb + LX_QKV + QROWS * m + 8 * s + 2 * (lane >> 4),
+                      u32x2{tagged(tag_of(epoch, layer), rbf(r[0])), tagged(tag_of(epoch, layer), rbf(r[1]))});
           if (lane == 0) signal_store(&s_cnt);
           AFTER(r[0] + r[1]);
           MQ_STAMP(layer * 40 + 1);
@@ -1022,6 +1027,12 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
 #pragma unroll
             for (int i = 0; i < 4; i++) s_res[16 * s + 2 * (i + 4 * (q & 1)) + (q >> 1)] = r[i];
           }
+          // the wave's 16 partials back in row order (its own slots of s_res), stored by the
+          // wave itself as one 128-byte run of (value, tag) pairs
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (lane < 16)
+            st2_dev(ws + X_OPART + 2 * ((m * NXCD + g) * ROWS + 16 * s + lane),
+                    u32x2{__float_as_uint(s_res[16 * s + lane]), epoch * 32u + (uint32_t)layer + 1u});
           if (lane == 0) signal_store(&s_cnt);
           AFTER(r[0] + r[1] + r[2] + r[3]);
           MQ_STAMP(layer * 40 + 5);
@@ -1092,6 +1103,14 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
 #pragma unroll
             for (int k = 0; k < 3; k++) s_res[12 * s + 3 * (lane >> 4) + k] = r[k];
           }
+          // HF Qwen3MLP (modeling_qwen3.py:81-83): m = bf16(bf16(silu(gate)) * up) of the
+          // wave's 6 units (gate rows 0..5, up rows 6..11 of its s_res slots), stored by the wave
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (lane < 6) {
+            const float gt = rbf(s_res[12 * s + lane]), up = rbf(s_res[12 * s + 6 + lane]);
+            st1_plain(ws + lb + LX_M + UNITS * m + 6 * s + lane,
+                      tagged(tag_of(epoch, layer), rbf(rbf(gt / (1.0f + expf(-gt))) * up)));
+          }
           if (lane == 0) signal_store(&s_cnt);
           AFTER(r[0] + r[1] + r[2]);
           MQ_STAMP(layer * 40 + 7);
@@ -1109,6 +1128,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
 #pragma unroll
             for (int k = 0; k < 4; k++) s_res[16 * s + 4 * (lane >> 4) + k] = r[k];
           }
+          // the wave's 16 partials, stored by the wave as one 128-byte run of (value, tag) pairs
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (lane < 16)
+            st2_dev(ws + X_DPART + 2 * ((m * NXCD + g) * ROWS + 16 * s + lane),
+                    u32x2{__float_as_uint(s_res[16 * s + lane]), epoch * 32u + (uint32_t)layer + 1u});
           if (lane == 0) signal_store(&s_cnt);
           AFTER(r[0] + r[1] + r[2] + r[3]);
           MQ_STAMP(layer * 40 + 9);
@@ -1491,8 +1515,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       if (ga) {
         BAR();  // A1
         target += NSW;
-        wait_count(&s_cnt, target);
-        if (lane < QROWS) st1_plain(ws + lb + LX_QKV + QROWS * m + lane, tagged(tag, rbf(s_res[lane])));
+        wait_count(&s_cnt, target);  // (the stream waves store the q/k/v rows themselves)
         MQ_STAMP(layer * 40 + 34);
         if (att) {
           float Mr0 = 0.f, Mr1 = 0.f, Lr0 = 0.f, Lr1 = 0.f;  // running max / sum over the passes
@@ -1567,26 +1590,19 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         // o_proj partials of rows 64m .. 64m+63 over this XCD's two heads
         BAR();  // C1
         target += NSW;
-        wait_count(&s_cnt, target);
-        st2_dev(ws + X_OPART + 2 * ((m * NXCD + g) * ROWS + lane), u32x2{__float_as_uint(s_res[lane]), tag64});
+        wait_count(&s_cnt, target);  // (the stream waves store the partials themselves)
         if (m == 0 && lane == 0) st1_plain(ws + lb + LX_CUE_A, tag);
         MQ_STAMP(layer * 40 + 36);
       } else {
         // HF Qwen3MLP (modeling_qwen3.py:81-83): m = bf16(bf16(silu(gate)) * up)
         BAR();  // D1
         target += NSW;
-        wait_count(&s_cnt, target);
-        if (lane < UNITS) {
-          const int sw = lane / 6, u = lane - 6 * sw;  // stream wave sw holds gate / up rows 6 sw + u
-          const float gt = rbf(s_res[12 * sw + u]), up = rbf(s_res[12 * sw + 6 + u]);
-          st1_plain(ws + lb + LX_M + UNITS * m + lane, tagged(tag, rbf(rbf(gt / (1.0f + expf(-gt))) * up)));
-        }
+        wait_count(&s_cnt, target);  // (the stream waves store m themselves)
         MQ_STAMP(layer * 40 + 37);
         // down_proj partials of rows 64m .. 64m+63 over this XCD's 384 units
         BAR();  // E1
         target += NSW;
-        wait_count(&s_cnt, target);
-        st2_dev(ws + X_DPART + 2 * ((m * NXCD + g) * ROWS + lane), u32x2{__float_as_uint(s_res[lane]), tag64});
+        wait_count(&s_cnt, target);  // (the stream waves store the partials themselves)
         if (m == 0 && lane == 0) st1_plain(ws + lb + LX_CUE_B, tag);
         MQ_STAMP(layer * 40 + 38);
       }

@@ -133,16 +133,19 @@ def test_clears_are_needed_for_the_regions_only_some_launches_write():
 
 # ---------------------------------------------------------------- word coverage
 
-def _qkv_words():  # store wave of A workgroup a, lanes < 32
-    return {QROWS * a + lane for a in range(NGA) for lane in range(QROWS)}
+def _qkv_words():
+    """Stream wave s of A workgroup a: lanes 16 q (q < 4) hold rows 2 q, 2 q + 1 of the wave's
+    8 and store them as one pair at word 32 a + 8 s + 2 q."""
+    return {QROWS * a + 8 * s + 2 * q + e for a in range(NGA) for s in range(4) for q in range(4) for e in range(2)}
 
 
 def _rows_words():  # LX_H (B) / LX_H1 (A): reduce wave of member m, lane -> row 64 m + lane
     return {ROWS * m + lane for m in range(NGA) for lane in range(64)}
 
 
-def _m_words():  # store wave of B workgroup b, lanes < 24
-    return {UNITS * b + lane for b in range(NGB) for lane in range(UNITS)}
+def _m_words():
+    """Stream wave s of B workgroup b: lanes < 6 store the wave's 6 units at word 24 b + 6 s + lane."""
+    return {UNITS * b + 6 * s + lane for b in range(NGB) for s in range(4) for lane in range(6)}
 
 
 def _att_words():  # store wave: lane -> 4 words at hh * 128 + 4 (lane & 31)
@@ -195,10 +198,11 @@ def test_every_polled_word_is_written_at_every_layer():
 
 
 def test_cross_xcd_partials_cover_every_row():
-    """X_OPART / X_DPART ([member][xcd][row] pairs): the store wave of workgroup (g, m)
-    stores lane < 64 at [m][g][lane] (one contiguous 512-byte run); the reduce wave of
-    (g', m) polls [m][x][lane] for every XCD x, lane < 64, one 8-byte pair per load."""
-    written = {(m, g, r) for g in range(NXCD) for m in range(NGA) for r in range(ROWS)}
+    """X_OPART / X_DPART ([member][xcd][row] pairs): stream wave s of workgroup (g, m) stores
+    lane < 16 at [m][g][16 s + lane] (one contiguous 128-byte run per wave); the reduce wave
+    of (g', m) polls [m][x][lane] for every XCD x, lane < 64, one 8-byte pair per load."""
+    written = {(m, g, 16 * s + lane) for g in range(NXCD) for m in range(NGA) for s in range(4) for lane in range(16)}
+    assert len(written) == NXCD * NGA * ROWS
     polled = {(m, x, lane) for m in range(NGA) for x in range(NXCD) for lane in range(64)}
     assert polled == written
     # word offsets: producer 2 ((m 8 + g) 64 + lane), consumer 2 (m 8 64 + lane) + 2 64 x
