@@ -154,8 +154,9 @@ int launch_prefill_float(const int* input_token_ids, int* output_token_id, int s
  * the full model like launch_ldg_decode, taking token/position/epoch from `step`,
  * appending the greedy token to out_ids[count] and advancing `step`. No host read is
  * needed between steps. split_instance: 0 runs the kernel instance for contexts of at
- * most 256 positions (a step past that fails with a negative token), 1 the instance for
- * every length (see mq_decode_plan). Re-initialise `step` before replaying a graph. */
+ * most 256 positions (a step past that fails with a negative token), 1 and 2 the
+ * instances for every length (2 pipelines a chunk's LDS passes: the faster one past 4096
+ * positions, see mq_decode_plan). Re-initialise `step` before replaying a graph. */
 int mq_decode_step_init(MqDecodeStep* step, int token, int position, int capacity, hipStream_t stream);
 int mq_decode_step_device(MqDecodeStep* step, int* out_ids, int out_capacity, int split_instance,
                           const void* embed_weight, const LDGLayerWeights* layer_weights,
@@ -164,7 +165,8 @@ int mq_decode_step_device(MqDecodeStep* step, int* out_ids, int out_capacity, in
                           void* g_normalized, int num_layers, int max_seq_len, float attn_scale, hipStream_t stream);
 
 /* The decode kernel's work split for the query at `position` (host-side, no GPU needed):
- * *instance = 0 (one attention workgroup per XCD, contexts of at most 256 positions) or 1;
+ * *instance = 0 (one attention workgroup per XCD, contexts of at most 256 positions), 1,
+ * or 2 (a chunk's LDS passes pipelined, where a chunk takes more than one pass);
  * the attention is split into *nsplit chunks of at most *chunk positions, each attended
  * in at most *npass LDS passes. The MI355X counterpart of the reference's decode-kernel
  * variant choice (chat.py:17-29). MQ_ERR_ARG past the 16384-position limit. */

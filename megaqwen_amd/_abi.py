@@ -17,6 +17,9 @@ MQ_ERR_ARG = -1
 MQ_ERR_HIP = -2
 MQ_ERR_DEVICE = -3
 MQ_ERR_ALLOC = -4
+# Longest context of the decode kernel (positions 0 .. MAX_CONTEXT - 1; mq_decode_plan
+# rejects the rest)
+MAX_CONTEXT = 16384
 
 LAYER_FIELDS = (
     "input_layernorm_weight",
@@ -108,8 +111,9 @@ def exported_symbols() -> list[str]:
 
 def decode_plan(position: int) -> dict:
     """The decode kernel's work split for the query at `position` (C ABI `mq_decode_plan`,
-    host only): kernel instance (0: contexts <= 256 positions, 1: any), number of attention
-    chunks, positions per chunk, LDS passes per chunk."""
+    host only): kernel instance (0: contexts <= 256 positions; 1: any; 2: any, a chunk's
+    LDS passes pipelined, chosen where a chunk takes more than one pass), number of
+    attention chunks, positions per chunk, LDS passes per chunk."""
     inst, ns, ch, npass = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     check(lib().mq_decode_plan(int(position), ctypes.byref(inst), ctypes.byref(ns), ctypes.byref(ch),
                                ctypes.byref(npass)), "mq_decode_plan")

@@ -15,7 +15,8 @@ Variants. The reference's variants are NVIDIA source rewrites (fast-math,
 128-block grids). The MI355X knob is the decode kernel instance
 (`mq_decode_plan`): "unsplit" attends with one workgroup per XCD and serves
 contexts of at most SHORT_CONTEXT_POSITIONS positions; "split" splits the
-attention over up to 16 workgroups per XCD and serves every length; "baseline"
+attention over up to 16 workgroups per XCD and serves every length (past 4096
+positions the variant of it that pipelines a chunk's LDS passes); "baseline"
 picks per step (the launcher's own choice, always the faster valid instance).
 The host-driven `decode_ldg` path always picks per step; the variant selects the
 instance of the device-resident generation loop, whose launches cannot switch

@@ -38,9 +38,11 @@
 //   * store wave 7 appends the new K/V row, stores the attention output and the
 //     stage cues, and clears the words a launch does not write.
 // A layer has five XCD-local all-gathers and two cross-XCD reductions and no grid
-// barrier. The kernel has two instances: SPLIT = false for contexts of at most 256
-// positions (one attention workgroup per XCD, no chunk merge compiled in) and
-// SPLIT = true for the rest (up to 16 chunks of up to four 256-position LDS passes).
+// barrier. The kernel has three instances: SPLIT = false for contexts of at most 256
+// positions (one attention workgroup per XCD, no chunk merge compiled in), SPLIT = true
+// for the rest (up to 16 chunks of up to four 256-position LDS passes), and its PIPE
+// variant, which overlaps the later passes' K/V copies with the previous pass (used
+// where a chunk takes more than one pass: past 4096 positions).
 //
 // Exchanges use "tagged words": a bf16 value in the low half of a 32-bit word
 // and a 16-bit tag (launch epoch x 32 + layer) in the high half, or an fp32
@@ -127,6 +129,12 @@ constexpr bool plan_is_sound() {
   return true;
 }
 static_assert(plan_is_sound(), "attention chunks must fit MAX_PASS LDS passes and cover the context");
+// Kernel instance for the query at `position`: 0 (one attention workgroup per XCD, one
+// pass) below KV_CAP, 2 (passes pipelined) where a chunk takes more than one LDS pass,
+// else 1.
+__host__ __device__ constexpr int plan_instance(int position) {
+  return position < KV_CAP ? 0 : plan_chunk(position + 1) > KV_CAP ? 2 : 1;
+}
 
 // Workspace layout, in 32-bit words.
 constexpr uint32_t WS_RESERVED = 0;  // (words 0..31 unused)
@@ -304,8 +312,9 @@ __device__ __forceinline__ int vsw(int row) { return 2 * ((row & 3) | (((row >> 
 __device__ __forceinline__ uint32_t vkv_off(int row, int chunk) { return row * 256 + 16 * (chunk ^ vsw(row)); }
 
 // Stream wave s copies K and V rows [0, nc) of the chunk starting at position c0
-// (except position p, which the layer itself produces) into LDS; nt picks the
-// non-temporal cache policy.
+// (except position p, which the layer itself produces) into LDS (WHAT: 1 the K rows,
+// 2 the V rows, 3 both); nt picks the non-temporal cache policy.
+template <int WHAT = 3>
 __device__ __forceinline__ void kv_dma(bool nt, const DecodeParams& P, int layer, int g, int c0, int nc, int p, uint32_t lds,
                                        int s, int lane) {
   const size_t base = ((size_t)(layer * NKV + g) * P.max_seq_len + c0) * HD;
@@ -317,11 +326,11 @@ __device__ __forceinline__ void kv_dma(bool nt, const DecodeParams& P, int layer
     const int row = 4 * q + rin;
     if (row < nc && c0 + row != p) {
       if (nt) {
-        dma16_nt(kb + row * HD + 8 * (slot ^ (row & 15)), lds + q * 1024);
-        dma16_nt(vb + row * HD + 8 * (slot ^ vsw(row)), lds + KV_CAP * 256 + q * 1024);
+        if constexpr ((WHAT & 1) != 0) dma16_nt(kb + row * HD + 8 * (slot ^ (row & 15)), lds + q * 1024);
+        if constexpr ((WHAT & 2) != 0) dma16_nt(vb + row * HD + 8 * (slot ^ vsw(row)), lds + KV_CAP * 256 + q * 1024);
       } else {
-        dma16(kb + row * HD + 8 * (slot ^ (row & 15)), lds + q * 1024);
-        dma16(vb + row * HD + 8 * (slot ^ vsw(row)), lds + KV_CAP * 256 + q * 1024);
+        if constexpr ((WHAT & 1) != 0) dma16(kb + row * HD + 8 * (slot ^ (row & 15)), lds + q * 1024);
+        if constexpr ((WHAT & 2) != 0) dma16(vb + row * HD + 8 * (slot ^ vsw(row)), lds + KV_CAP * 256 + q * 1024);
       }
     }
   }
@@ -799,9 +808,13 @@ __device__ __forceinline__ void qk_norm_rope(uint32_t u0, uint32_t u1, const uin
 // ---------------------------------------------------------------- the kernel
 // SPLIT = false is the instance for contexts of at most KV_CAP positions (one
 // attention workgroup per XCD, one LDS pass): the chunk-merge and multi-pass code
-// is compiled out of it. SPLIT = true handles every context length.
-template <bool SPLIT>
+// is compiled out of it. SPLIT = true handles every context length; PIPE (with SPLIT)
+// overlaps a chunk's later LDS passes' K/V copies with the previous pass's work, the
+// instance for chunks of more than one pass (compiled apart, so that the one-pass
+// instance keeps its own register allocation).
+template <bool SPLIT, bool PIPE = false>
 __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
+  static_assert(SPLIT || !PIPE, "the pipelined passes belong to the split instance");
   __shared__ __align__(16) uint8_t s_kv[2 * KV_CAP * HD * 2];  // K rows, then V rows of the chunk
   __shared__ __align__(16) uint32_t s_x0[H / 2];               // normed h (A) or h1 (B) (bf16 pairs)
   __shared__ __align__(16) uint32_t s_x1[XUNITS / 2];          // attention output (A) or m (B) of the XCD
@@ -984,33 +997,79 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           // this wave's K/V copy of the layer has landed (issued in the previous layer's
           // quiet window; all of the wave's vector-memory operations are awaited)
           wait_vmem();
-          for (int ps = 0; ps < npass; ps++) {
-            if (ps > 0) {
-              // rows KV_CAP * ps .. of the chunk replace the previous pass's rows
-              kv_dma(kv_nt, P, layer, g, c0 + KV_CAP * ps, pass_rows(ps), p, lds_kv, s, lane);
-              wait_vmem();
+          // Later passes of a chunk (contexts past 256 positions a chunk). PIPE: a pass's K
+          // rows are copied while the previous pass runs its P.V (the previous K rows are
+          // consumed at B2), its V rows while it runs its own scores and softmax (the previous
+          // V rows are consumed at B4); each copy is issued after the wave's last wait, so
+          // every wait is for all of the wave's copies in flight. Otherwise a pass's K and V
+          // rows are copied, and awaited, after the previous pass.
+          if constexpr (PIPE) {
+            const bool piped = npass > 1;
+            for (int ps = 0; ps < npass; ps++) {
+              if (ps > 0) {
+                wait_vmem();  // the pass's K rows
+                kv_dma<2>(kv_nt, P, layer, g, c0 + KV_CAP * ps, pass_rows(ps), p, lds_kv, s, lane);
+              }
+              // the new v row (the raw bf16 values), polled when no copy of this wave is in
+              // flight: before B1, or before B3 when the passes are pipelined
+              auto v_row = [&]() {
+                const uint32_t w[2] = {lb + LX_QKV + 3 * HD + lane, lb + LX_QKV + 3 * HD + 64 + lane};
+                uint32_t u[2];
+                poll_words<!SPLIT>(wsb, ws, w, tag_of(epoch, layer), u);
+                uint8_t* vbase = s_kv + KV_CAP * 256;
+                *reinterpret_cast<uint16_t*>(vbase + vkv_off(prow, lane >> 3) + 2 * (lane & 7)) = (uint16_t)(u[0] & 0xffffu);
+                *reinterpret_cast<uint16_t*>(vbase + vkv_off(prow, 8 + (lane >> 3)) + 2 * (lane & 7)) =
+                    (uint16_t)(u[1] & 0xffffu);
+              };
+              const bool vrow = s == 0 && own_p && ps == npass - 1;
+              if (vrow && !piped) v_row();
+              const int ncp = pass_rows(ps);
+              BAR();  // B1: q, the new k row (unless pipelined: and v row) and the pass's K rows are in LDS
+              MQ_STAMP(layer * 40 + 2);
+              attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
+              BAR();  // B2: the pass's K rows consumed
+              float M0, M1, L0, L1;
+              attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
+              if (piped) {
+                wait_vmem();  // the pass's V rows
+                if (vrow) v_row();
+                if (ps + 1 < npass)
+                  kv_dma<1>(kv_nt, P, layer, g, c0 + KV_CAP * (ps + 1), pass_rows(ps + 1), p, lds_kv, s, lane);
+              }
+              BAR();  // B3: the pass's V rows and the new v row are in LDS
+              attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+              BAR();  // B4: the pass's V rows consumed
+              MQ_STAMP(layer * 40 + 3);
             }
-            if (s == 0 && own_p && ps == npass - 1) {
-              // the new v row (the raw bf16 values; no loads of this wave are in flight)
-              const uint32_t w[2] = {lb + LX_QKV + 3 * HD + lane, lb + LX_QKV + 3 * HD + 64 + lane};
-              uint32_t u[2];
-              poll_words<!SPLIT>(wsb, ws, w, tag_of(epoch, layer), u);
-              uint8_t* vbase = s_kv + KV_CAP * 256;
-              *reinterpret_cast<uint16_t*>(vbase + vkv_off(prow, lane >> 3) + 2 * (lane & 7)) = (uint16_t)(u[0] & 0xffffu);
-              *reinterpret_cast<uint16_t*>(vbase + vkv_off(prow, 8 + (lane >> 3)) + 2 * (lane & 7)) =
-                  (uint16_t)(u[1] & 0xffffu);
+          } else {
+            for (int ps = 0; ps < npass; ps++) {
+              if (ps > 0) {
+                // rows KV_CAP * ps .. of the chunk replace the previous pass's rows
+                kv_dma(kv_nt, P, layer, g, c0 + KV_CAP * ps, pass_rows(ps), p, lds_kv, s, lane);
+                wait_vmem();
+              }
+              if (s == 0 && own_p && ps == npass - 1) {
+                // the new v row (the raw bf16 values; no loads of this wave are in flight)
+                const uint32_t w[2] = {lb + LX_QKV + 3 * HD + lane, lb + LX_QKV + 3 * HD + 64 + lane};
+                uint32_t u[2];
+                poll_words<!SPLIT>(wsb, ws, w, tag_of(epoch, layer), u);
+                uint8_t* vbase = s_kv + KV_CAP * 256;
+                *reinterpret_cast<uint16_t*>(vbase + vkv_off(prow, lane >> 3) + 2 * (lane & 7)) = (uint16_t)(u[0] & 0xffffu);
+                *reinterpret_cast<uint16_t*>(vbase + vkv_off(prow, 8 + (lane >> 3)) + 2 * (lane & 7)) =
+                    (uint16_t)(u[1] & 0xffffu);
+              }
+              const int ncp = pass_rows(ps);
+              BAR();  // B1: q, the new k/v row and the K/V rows are in LDS
+              MQ_STAMP(layer * 40 + 2);
+              attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
+              BAR();  // B2
+              float M0, M1, L0, L1;
+              attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
+              BAR();  // B3
+              attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+              BAR();  // B4: K/V rows consumed
+              MQ_STAMP(layer * 40 + 3);
             }
-            const int ncp = pass_rows(ps);
-            BAR();  // B1: q, the new k/v row and the K/V rows are in LDS
-            MQ_STAMP(layer * 40 + 2);
-            attn_scores(s_kv, s_q, s_sc, s_mx, ncp, P.attn_scale, wave, lane);
-            BAR();  // B2
-            float M0, M1, L0, L1;
-            attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
-            BAR();  // B3
-            attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
-            BAR();  // B4: K/V rows consumed
-            MQ_STAMP(layer * 40 + 3);
           }
         }
         // ---------------- o_proj partials: rows 64m + 16s + 2i + org over the group's 256 columns
@@ -1522,8 +1581,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           for (int ps = 0; ps < npass; ps++) {
             const int ncp = pass_rows(ps);
             BAR();  // B1
-            if (own_p && (SPLIT || m == 0) && ps == npass - 1) {
-              // K/V-cache append (one workgroup per XCD) at slot p (bf16 [L][8][max_seq][128]): lane -> dims 2 lane, 2 lane + 1
+            if (own_p && (SPLIT || m == 0) && ps == npass - 1 && !(PIPE && npass > 1)) {
+              // K/V-cache append (one workgroup per XCD) at slot p (bf16 [L][8][max_seq][128]):
+              // lane -> dims 2 lane, 2 lane + 1; at B1 the new k and v rows are in LDS (at B3
+              // when the passes are pipelined)
               const size_t slot = ((size_t)(layer * NKV + g) * P.max_seq_len + p) * HD;
               const uint32_t k2 = *reinterpret_cast<const uint32_t*>(s_kv + kv_off(prow, lane >> 2) + 4 * (lane & 3));
               const uint32_t v2 =
@@ -1536,6 +1597,16 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             float M0, M1, L0, L1;
             attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
             BAR();  // B3
+            if constexpr (PIPE) {
+              if (own_p && ps == npass - 1 && npass > 1) {
+                const size_t slot = ((size_t)(layer * NKV + g) * P.max_seq_len + p) * HD;
+                const uint32_t k2 = *reinterpret_cast<const uint32_t*>(s_kv + kv_off(prow, lane >> 2) + 4 * (lane & 3));
+                const uint32_t v2 =
+                    *reinterpret_cast<const uint32_t*>(s_kv + KV_CAP * 256 + vkv_off(prow, lane >> 2) + 4 * (lane & 3));
+                st1_plain(reinterpret_cast<uint32_t*>(P.k_cache + slot) + lane, k2);
+                st1_plain(reinterpret_cast<uint32_t*>(P.v_cache + slot) + lane, v2);
+              }
+            }
             attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
             BAR();  // B4
             if (ps == 0) {
@@ -1758,7 +1829,8 @@ static int check_device(int dev) {
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return MQ_ERR_HIP;
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0 || !prop.cooperativeLaunch) return MQ_ERR_DEVICE;
   for (const void* k : {reinterpret_cast<const void*>(mq_decode_kernel<false>),
-                        reinterpret_cast<const void*>(mq_decode_kernel<true>)}) {
+                        reinterpret_cast<const void*>(mq_decode_kernel<true>),
+                        reinterpret_cast<const void*>(mq_decode_kernel<true, true>)}) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NT, 0) != hipSuccess) return MQ_ERR_HIP;
     if (per_cu * prop.multiProcessorCount < NWG) return MQ_ERR_DEVICE;
@@ -1838,9 +1910,10 @@ static int launch(DecodeParams& P, hipStream_t stream, int split_instance = -1, 
   // error after a bounded spin, so an ordinary launch is the default. The
   // cooperative launch (the reference's) is kept as an option, for comparison.
   void* args[] = {&P};
-  const bool split = split_instance < 0 ? P.position >= KV_CAP : split_instance != 0;
-  const void* kern = split ? reinterpret_cast<const void*>(mq_decode_kernel<true>)
-                           : reinterpret_cast<const void*>(mq_decode_kernel<false>);
+  const int inst = split_instance < 0 ? plan_instance(P.position) : split_instance;
+  const void* kern = inst == 2   ? reinterpret_cast<const void*>(mq_decode_kernel<true, true>)
+                     : inst == 1 ? reinterpret_cast<const void*>(mq_decode_kernel<true>)
+                                 : reinterpret_cast<const void*>(mq_decode_kernel<false>);
   const hipError_t e = g_cooperative.load(std::memory_order_relaxed)
                            ? hipLaunchCooperativeKernel(kern, dim3(NWG), dim3(NT), args, 0, stream)
                            : hipLaunchKernel(kern, dim3(NWG), dim3(NT), args, 0, stream);
@@ -1991,7 +2064,7 @@ extern "C" int mq_decode_step_device(MqDecodeStep* step, int* out_ids, int out_c
       !lm_head_weight || !cos_table || !sin_table || !k_cache || !v_cache || !hidden_buffer)
     return MQ_ERR_ARG;
   if (num_layers < 1 || num_layers > MAX_LAYERS || max_seq_len < 1 || bad_scale(attn_scale) ||
-      (split_instance != 0 && split_instance != 1))
+      split_instance < 0 || split_instance > 2)
     return MQ_ERR_ARG;
   DecodeParams P{};
   P.layers = layer_weights;
@@ -2019,7 +2092,7 @@ extern "C" int mq_decode_plan(int position, int* instance, int* nsplit, int* chu
   if (position < 0 || position >= MAX_CTX) return MQ_ERR_ARG;
   const int n = position + 1;
   const int ns = plan_nsplit(n), ch = plan_chunk(n);
-  if (instance) *instance = position >= KV_CAP ? 1 : 0;
+  if (instance) *instance = plan_instance(position);
   if (nsplit) *nsplit = ns;
   if (chunk) *chunk = ch;
   if (npass) *npass = (ch + KV_CAP - 1) / KV_CAP;

@@ -190,8 +190,8 @@ class MegakernelDecoder:
         that the previous launch advanced. Steps run in chunks of `chunk` launches, as
         one replay of a captured HIP graph per chunk (`use_graph`) or as direct launches;
         the host reads the chunk's tokens once at its end, to stop at a stop token. A
-        chunk whose positions all stay below 256 uses the kernel instance for short
-        contexts (see `_abi.decode_plan`). Returns the generated ids (up to and
+        chunk runs the kernel instance that `_abi.decode_plan` names for its last position
+        (short contexts below 256, LDS passes pipelined from 4096). Returns the generated ids (up to and
         excluding a stop token, like `generate`).
         """
         if n_steps < 1:
@@ -210,7 +210,9 @@ class MegakernelDecoder:
         while len(out) < n_steps:
             k = min(chunk, n_steps - len(out))
             p0 = self.position_
-            split = 0 if p0 + k <= 256 else 1
+            # the instance of the chunk's last position serves every earlier one too (past the
+            # 16384-position limit the kernel itself reports the error)
+            split = _abi.decode_plan(min(p0 + k - 1, _abi.MAX_CONTEXT - 1))["instance"]
             _abi.check(lib.mq_decode_step_init(_ptr(step), token, p0, k, _stream()), "mq_decode_step_init")
             if use_graph:
                 key = (k, split)

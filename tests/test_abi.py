@@ -124,15 +124,17 @@ def test_decode_plan_bounds_every_position():
     for p in range(16384):
         assert L.mq_decode_plan(p, *refs) == _abi.MQ_OK
         n = p + 1
-        assert inst.value == (0 if p < 256 else 1)
+        assert inst.value == (0 if p < 256 else 2 if npass.value > 1 else 1)
         assert 1 <= ns.value <= 16 and ch.value <= 1024 and npass.value == (ch.value + 255) // 256 <= 4
         assert ch.value * ns.value >= n and (ns.value - 1) * ch.value < n
         if p < 256:
             assert ns.value == 1 and ch.value == n
     for p in (-1, 16384):
         assert L.mq_decode_plan(p, *refs) == _abi.MQ_ERR_ARG
-    assert _abi.decode_plan(8447) == {"instance": 1, "nsplit": 16, "chunk": 528, "npass": 3}
-    assert _abi.decode_plan(16383) == {"instance": 1, "nsplit": 16, "chunk": 1024, "npass": 4}
+    assert _abi.decode_plan(8447) == {"instance": 2, "nsplit": 16, "chunk": 528, "npass": 3}
+    assert _abi.decode_plan(16383) == {"instance": 2, "nsplit": 16, "chunk": 1024, "npass": 4}
+    assert _abi.decode_plan(4095) == {"instance": 1, "nsplit": 16, "chunk": 256, "npass": 1}
+    assert _abi.decode_plan(4096) == {"instance": 2, "nsplit": 16, "chunk": 257, "npass": 2}
     assert _abi.decode_plan(1023) == {"instance": 1, "nsplit": 4, "chunk": 256, "npass": 1}
 
 
@@ -148,7 +150,7 @@ def test_device_step_entries_reject_invalid_arguments():
     def args(**o):
         a = dict(good, **o)
         return [a["step"], a["out"], a["cap"], a["split"]] + [1] * 10 + [28, 16, 0.088, None]
-    for bad in (dict(step=None), dict(out=None), dict(cap=0), dict(split=2), dict(split=-1)):
+    for bad in (dict(step=None), dict(out=None), dict(cap=0), dict(split=3), dict(split=-1)):
         assert L.mq_decode_step_device(*args(**bad)) == _abi.MQ_ERR_ARG
     a = args()
     a[14] = 0  # num_layers

@@ -8,8 +8,9 @@ tag. This model restates, per workspace region, which launches and layers write 
 clear) it, which read it and with which tag, and checks that property for every read
 against every stale content that a sequence of launches of any kinds can leave behind:
 
-* launch kinds: the two kernel instances (contexts up to 256 positions / longer), each
-  with any attention split count, as full-model launches (28 layers) or single-block
+* launch kinds: the two kernel instances (contexts up to 256 positions / longer; the
+  longer one's variant with pipelined LDS passes exchanges the same words), each with
+  any attention split count, as full-model launches (28 layers) or single-block
   launches (1 layer), in any order and number;
 * 16-bit tags: 1 + ((32 epoch + layer) mod 65535), in the high half of a bf16 word;
   32-bit tags: 32 epoch + layer + 1, beside an fp32 value;

@@ -178,3 +178,70 @@ def test_fused_prefill_names(gpu_weights):
     gen = MK.MegakernelFusedPrefillGenerator(weights_dict=w, max_seq_len=256)
     ids_out = gen.generate_ids(ids, max_new_tokens=4)
     assert ids_out[0] == a and len(ids_out) == 4
+
+
+# ---------------------------------------------------------------- contexts past 4096 positions
+LONG_P0 = 4088  # 16 steps from here cross 4096, where chunks take two LDS passes
+
+
+@pytest.fixture(scope="module")
+def long_decoder(gpu_weights):
+    w = gpu_weights
+    return MK.MegakernelDecoder(w["embed_weight"], w["layer_weights"], w["final_norm_weight"], w["lm_head_weight"],
+                                w["cos_table"], w["sin_table"], 28, 4160)
+
+
+def _fill_caches(dec, upto, seed):
+    """Positions < upto of both caches hold N(0, 1) bf16 values (a pre-filled context)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    for c in (dec.get_k_cache(), dec.get_v_cache()):
+        c.zero_()
+        c[:, :, :upto] = torch.randn(c[:, :, :upto].shape, generator=g, device="cuda").to(torch.bfloat16)
+    torch.cuda.synchronize()
+
+
+def test_device_resident_generation_across_the_pipelined_instance(long_decoder):
+    """Chunks of the device-resident loop before position 4096 run instance 1, later ones
+    instance 2 (a chunk's LDS passes pipelined); tokens and both caches equal the host
+    loop's (which picks the instance per step), directly and as graph replays."""
+    dec = long_decoder
+    assert _abi.decode_plan(4095)["instance"] == 1 and _abi.decode_plan(4096)["instance"] == 2
+    n, tok = 16, 1234
+    _fill_caches(dec, LONG_P0, 0)
+    k0, v0 = dec.get_k_cache().clone(), dec.get_v_cache().clone()
+    dec.set_position(LONG_P0)
+    want, cur = [], tok
+    for _ in range(n):
+        cur = dec.decode_step(cur)
+        want.append(cur)
+    kw, vw = dec.get_k_cache().clone(), dec.get_v_cache().clone()
+    for use_graph in (False, True, True):
+        dec.get_k_cache().copy_(k0)
+        dec.get_v_cache().copy_(v0)
+        dec.set_position(LONG_P0)
+        got = dec.generate_device(tok, n, use_graph=use_graph, chunk=4)
+        print(f"graph={use_graph}: {sum(a == b for a, b in zip(got, want))}/{n} equal", flush=True)
+        assert got == want
+        assert torch.equal(dec.get_k_cache(), kw) and torch.equal(dec.get_v_cache(), vw)
+
+
+def test_pipelined_instance_is_bitwise_identical(long_decoder):
+    """Past 4096 positions instances 1 and 2 differ only in when a chunk's later LDS passes
+    are copied: forced through mq_decode_step_device, both give the same tokens and caches."""
+    dec = long_decoder
+    n, tok, p0 = 8, 777, LONG_P0 + 12
+    L = _abi.lib()
+    outs = []
+    for inst in (1, 2, 1):
+        _fill_caches(dec, p0, 1)
+        step, out_ids = dec._step_buffers(n)
+        _abi.check(L.mq_decode_step_init(MK._ptr(step), tok, p0, n, MK._stream()), "mq_decode_step_init")
+        for _ in range(n):
+            dec._launch_device_step(out_ids.numel(), inst)
+        ids = out_ids[:n].tolist()
+        print(f"instance {inst}: {ids}", flush=True)
+        assert min(ids) >= 0
+        outs.append((ids, dec.get_k_cache().clone(), dec.get_v_cache().clone()))
+    for ids, kc, vc in outs[1:]:
+        assert ids == outs[0][0]
+        assert torch.equal(kc, outs[0][1]) and torch.equal(vc, outs[0][2])
