@@ -1380,9 +1380,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
               __builtin_amdgcn_s_sleep(1);
               ml = ldl4(wsb, bml);
             }
+            MQ_STAMP(layer * 40 + 6);  // (slots 6..9: group B's stream waves elsewhere)
 #pragma unroll
             for (int q = 0; q < CG; q++)
               if (q < nq) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
+            MQ_STAMP_AFTER(layer * 40 + 9, ov[0].x);
             for (;;) {
               bool ok = !mlane || fresh(ml);
 #pragma unroll
@@ -1394,6 +1396,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
               for (int q = 0; q < CG; q++)
                 if (q < nq && !fresh(ov[q])) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
             }
+            MQ_STAMP(layer * 40 + 7);
 #pragma unroll
             for (int q = 0; q < CG; q++)
               if (q < nq) {
@@ -1406,6 +1409,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
                 O1 = O1 * ea + __uint_as_float(ov[q].z) * eb;
                 Mc = nm;
               }
+            MQ_STAMP_AFTER(layer * 40 + 8, O0 + O1 + Lc);
           }
           const float rl = 1.0f / Lc;
           s_x1[pt] = pack_bf2(rbf(O0 * rl), rbf(O1 * rl));

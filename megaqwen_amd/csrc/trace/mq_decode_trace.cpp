@@ -203,6 +203,30 @@ int main(int argc, char** argv) {
     prev = end[i];
   }
   printf("\nLayer period (XCD's last h store to the next): %.2f us; hop stages add up to %.2f us.\n", per, hop);
+  if (nsplit > 1) {
+    // the chunk merge in the group-A workgroups (poll waves), from the XCD's last chunk
+    // partial stored: (m, l) of the round's chunks seen, their accumulators' first loads
+    // back, all of them seen fresh, merged (the last round's), o_proj input in LDS; workgroup
+    // means and the last workgroup
+    const int ks[5] = {6, 9, 7, 8, 19};
+    double mean[5] = {0, 0, 0, 0, 0}, lastv[5] = {0, 0, 0, 0, 0};
+    int cnt = 0, cl = 0;
+    for (int l = 3; l <= 26; l++)
+      for (int g = 0; g < 8; g++) {
+        const int64_t t0 = last(g, l, 35, 0, nsplit);
+        for (int i = 0; i < 5; i++) {
+          for (int j = A0; j < A1; j++) mean[i] += (double)(int32_t)(T(8 * j + g, l, ks[i]) - t0) * 0.01;
+          lastv[i] += (double)(int32_t)(last(g, l, ks[i], A0, A1) - t0) * 0.01;
+        }
+        cnt += A1 - A0;
+        cl++;
+      }
+    printf("chunk merge (group A, from the XCD's last chunk partial stored; workgroup means / last): (m, l) seen "
+           "%.2f / %.2f us, accumulators' first loads back %.2f / %.2f, accumulators seen %.2f / %.2f, merged "
+           "%.2f / %.2f, o_proj input ready %.2f / %.2f\n",
+           mean[0] / cnt, lastv[0] / cl, mean[1] / cnt, lastv[1] / cl, mean[2] / cnt, lastv[2] / cl, mean[3] / cnt,
+           lastv[3] / cl, mean[4] / cnt, lastv[4] / cl);
+  }
   if (nsplit == 1) {
     // the attention's phases in the workgroups that run it (group A; slots 21..23 are
     // group B's elsewhere): the latest of waves 0, 4, 6, 7 done with the phase's work, then
