@@ -1403,7 +1403,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
                 const float mq = __uint_as_float(__builtin_amdgcn_readlane(ml.x, q));
                 const float lq = __uint_as_float(__builtin_amdgcn_readlane(ml.z, q));
                 const float nm = fmaxf(Mc, mq);
-                const float ea = Mc == -INFINITY ? 0.f : expf(Mc - nm), eb = expf(mq - nm);
+                // exp(Mc - nm) and exp(mq - nm): nm is one of the two, whose factor is
+                // exp(0) = 1 exactly, so one exponential (of the same argument) gives both
+                const bool up = mq > Mc;
+                const float e = expf(fminf(Mc, mq) - nm);
+                const float ea = Mc == -INFINITY ? 0.f : (up ? e : 1.f), eb = up ? 1.f : e;
                 Lc = Lc * ea + lq * eb;
                 O0 = O0 * ea + __uint_as_float(ov[q].x) * eb;
                 O1 = O1 * ea + __uint_as_float(ov[q].z) * eb;
