@@ -92,6 +92,10 @@
 #ifndef MQ_LANDED
 #define MQ_LANDED(i) ((void)0)
 #endif
+// MQ_VALUE(slot, v) records the value v in a slot instead of a time (a tracing build only)
+#ifndef MQ_VALUE
+#define MQ_VALUE(i, v) ((void)0)
+#endif
 
 namespace mq {
 
@@ -1382,9 +1386,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             }
             MQ_STAMP(layer * 40 + 6);  // (slots 6..9: group B's stream waves elsewhere)
 #pragma unroll
-            for (int q = 0; q < CG; q++)
-              if (q < nq) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
-            MQ_STAMP_AFTER(layer * 40 + 9, ov[0].x);
+            for (int q = 0; q < CG; q++) ov[q] = q < nq ? ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0) : u32x4{0u, 0u, 0u, 0u};
+            MQ_STAMP_AFTER(layer * 40 + 9, ov[CG - 1].x);
             for (;;) {
               bool ok = !mlane || fresh(ml);
 #pragma unroll
@@ -1397,22 +1400,28 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
                 if (q < nq && !fresh(ov[q])) ov[q] = ldl4(wsb, b0 + 4 * q * APART + 4 + 2 * d0);
             }
             MQ_STAMP(layer * 40 + 7);
+            MQ_VALUE(layer * 40 + 11, spins);
+            // chunk by chunk in order; every step is computed and kept only for q < nq (a
+            // select, not a branch, so the steps' exponentials overlap)
 #pragma unroll
-            for (int q = 0; q < CG; q++)
-              if (q < nq) {
-                const float mq = __uint_as_float(__builtin_amdgcn_readlane(ml.x, q));
-                const float lq = __uint_as_float(__builtin_amdgcn_readlane(ml.z, q));
-                const float nm = fmaxf(Mc, mq);
-                // exp(Mc - nm) and exp(mq - nm): nm is one of the two, whose factor is
-                // exp(0) = 1 exactly, so one exponential (of the same argument) gives both
-                const bool up = mq > Mc;
-                const float e = expf(fminf(Mc, mq) - nm);
-                const float ea = Mc == -INFINITY ? 0.f : (up ? e : 1.f), eb = up ? 1.f : e;
-                Lc = Lc * ea + lq * eb;
-                O0 = O0 * ea + __uint_as_float(ov[q].x) * eb;
-                O1 = O1 * ea + __uint_as_float(ov[q].z) * eb;
-                Mc = nm;
-              }
+            for (int q = 0; q < CG; q++) {
+              const bool in = q < nq;
+              const float mq = __uint_as_float(__builtin_amdgcn_readlane(ml.x, q));
+              const float lq = __uint_as_float(__builtin_amdgcn_readlane(ml.z, q));
+              const float nm = fmaxf(Mc, mq);
+              // exp(Mc - nm) and exp(mq - nm): nm is one of the two, whose factor is
+              // exp(0) = 1 exactly, so one exponential (of the same argument) gives both
+              const bool up = mq > Mc;
+              const float e = expf(fminf(Mc, mq) - nm);
+              const float ea = Mc == -INFINITY ? 0.f : (up ? e : 1.f), eb = up ? 1.f : e;
+              const float nL = Lc * ea + lq * eb;
+              const float n0 = O0 * ea + __uint_as_float(ov[q].x) * eb;
+              const float n1 = O1 * ea + __uint_as_float(ov[q].z) * eb;
+              Lc = in ? nL : Lc;
+              O0 = in ? n0 : O0;
+              O1 = in ? n1 : O1;
+              Mc = in ? nm : Mc;
+            }
             MQ_STAMP_AFTER(layer * 40 + 8, O0 + O1 + Lc);
           }
           const float rl = 1.0f / Lc;

@@ -23,6 +23,11 @@ __device__ unsigned long long* g_trace;
       g_str[(i)] = (uint32_t)c_;                                                      \
     }                                                                                 \
   } while (0)
+#define MQ_VALUE(i, v)                                      \
+  do {                                                      \
+    const int t_ = threadIdx.x;                             \
+    if (t_ == 0 || t_ == 256 || t_ == 384 || t_ == 448) g_str[(i)] = (uint32_t)(v); \
+  } while (0)
 #define MQ_STAMP_AFTER(i, v)                  \
   do {                                        \
     asm volatile("" ::"v"(v) : "memory");     \
@@ -205,7 +210,7 @@ int main(int argc, char** argv) {
   printf("\nLayer period (XCD's last h store to the next): %.2f us; hop stages add up to %.2f us.\n", per, hop);
   if (nsplit > 1) {
     // the chunk merge in the group-A workgroups (poll waves), from the XCD's last chunk
-    // partial stored: (m, l) of the round's chunks seen, their accumulators' first loads
+    // partial stored: (m, l) of the round's chunks seen, the round's accumulator loads
     // back, all of them seen fresh, merged (the last round's), o_proj input in LDS; workgroup
     // means and the last workgroup
     const int ks[5] = {6, 9, 7, 8, 19};
@@ -221,8 +226,14 @@ int main(int argc, char** argv) {
         cnt += A1 - A0;
         cl++;
       }
+    double spins = 0;
+    for (int l = 3; l <= 26; l++)
+      for (int g = 0; g < 8; g++)
+        for (int j = A0; j < A1; j++) spins += (double)T(8 * j + g, l, 11);
+    printf("chunk merge: spins of the (m, l) wait and accumulator re-polls (workgroup mean, last round) %.2f\n",
+           spins / cnt);
     printf("chunk merge (group A, from the XCD's last chunk partial stored; workgroup means / last): (m, l) seen "
-           "%.2f / %.2f us, accumulators' first loads back %.2f / %.2f, accumulators seen %.2f / %.2f, merged "
+           "%.2f / %.2f us, accumulators' loads back %.2f / %.2f, accumulators seen %.2f / %.2f, merged "
            "%.2f / %.2f, o_proj input ready %.2f / %.2f\n",
            mean[0] / cnt, lastv[0] / cl, mean[1] / cnt, lastv[1] / cl, mean[2] / cnt, lastv[2] / cl, mean[3] / cnt,
            lastv[3] / cl, mean[4] / cnt, lastv[4] / cl);
