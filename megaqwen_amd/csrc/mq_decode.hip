@@ -1401,27 +1401,39 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             }
             MQ_STAMP(layer * 40 + 7);
             MQ_VALUE(layer * 40 + 11, spins);
-            // chunk by chunk in order; every step is computed and kept only for q < nq (a
-            // select, not a branch, so the steps' exponentials overlap)
+            // Chunk q's rescale factors in lane q: the running maximum before and after chunk q
+            // (a chain of readlanes and maxima), then one exponential for all chunks at once:
+            // the maximum after a chunk is the previous maximum or the chunk's own, whose
+            // factor is exp(0) = 1 exactly, so exp(min - max) gives the other factor. The sums
+            // then run chunk by chunk in order, as fma(l, eb, L * ea), with the factors read
+            // back by readlane.
+            float pm = Mc, mb = 0.f, ma = 0.f;  // this lane's chunk: running maximum before / after it
 #pragma unroll
             for (int q = 0; q < CG; q++) {
               const bool in = q < nq;
-              const float mq = __uint_as_float(__builtin_amdgcn_readlane(ml.x, q));
+              const float nm = fmaxf(pm, __uint_as_float(__builtin_amdgcn_readlane(ml.x, q)));
+              mb = lane == q ? pm : mb;
+              ma = lane == q ? nm : ma;
+              pm = in ? nm : pm;
+            }
+            const float mq = __uint_as_float(ml.x);
+            const bool up = mq > mb;
+            const float e = expf(fminf(mb, mq) - ma);
+            const float fa = mb == -INFINITY ? 0.f : (up ? e : 1.f), fb = up ? 1.f : e;
+#pragma unroll
+            for (int q = 0; q < CG; q++) {
+              const bool in = q < nq;
+              const float ea = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(fa), q));
+              const float eb = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(fb), q));
               const float lq = __uint_as_float(__builtin_amdgcn_readlane(ml.z, q));
-              const float nm = fmaxf(Mc, mq);
-              // exp(Mc - nm) and exp(mq - nm): nm is one of the two, whose factor is
-              // exp(0) = 1 exactly, so one exponential (of the same argument) gives both
-              const bool up = mq > Mc;
-              const float e = expf(fminf(Mc, mq) - nm);
-              const float ea = Mc == -INFINITY ? 0.f : (up ? e : 1.f), eb = up ? 1.f : e;
-              const float nL = Lc * ea + lq * eb;
-              const float n0 = O0 * ea + __uint_as_float(ov[q].x) * eb;
-              const float n1 = O1 * ea + __uint_as_float(ov[q].z) * eb;
+              const float nL = __builtin_fmaf(lq, eb, Lc * ea);
+              const float n0 = __builtin_fmaf(__uint_as_float(ov[q].x), eb, O0 * ea);
+              const float n1 = __builtin_fmaf(__uint_as_float(ov[q].z), eb, O1 * ea);
               Lc = in ? nL : Lc;
               O0 = in ? n0 : O0;
               O1 = in ? n1 : O1;
-              Mc = in ? nm : Mc;
             }
+            Mc = pm;
             MQ_STAMP_AFTER(layer * 40 + 8, O0 + O1 + Lc);
           }
           const float rl = 1.0f / Lc;
