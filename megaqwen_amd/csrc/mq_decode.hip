@@ -1651,7 +1651,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
 #pragma unroll
               for (int h2 = 0; h2 < 2; h2++) {
                 const float ma = h2 ? Mr1 : Mr0, mb = h2 ? M1 : M0, mm = fmaxf(ma, mb);
-                const float ea = expf(ma - mm), eb = expf(mb - mm);
+                // exp(ma - mm) and exp(mb - mm): mm is one of the two, whose factor is
+                // exp(0) = 1 exactly, so one exponential (of the same argument) gives both
+                const bool up = mb > ma;
+                const float e = expf(fminf(ma, mb) - mm);
+                const float ea = up ? e : 1.f, eb = up ? 1.f : e;
                 if (h2 == hh)
 #pragma unroll
                   for (int e = 0; e < 4; e++) s_ao[hh][dim + e] = s_ao[hh][dim + e] * ea + s_ao1[hh][dim + e] * eb;
