@@ -48,13 +48,14 @@ typedef LDGLayerWeights PrefillLayerWeights;
 
 /* Device-resident decode step (16 bytes, device memory): the input of the next launch of
  * mq_decode_step_device. Each launch reads it at its start and its last workgroup writes
- * {argmax token, position + 1, epoch + 1, count + 1} back (a failed step writes its
+ * {argmax token, position + 1, epoch used, count + 1} back (a failed step writes its
  * negative status as the token and keeps the position; launches that find a negative
  * token, an invalid position or count == capacity do nothing). */
 typedef struct MqDecodeStep {
   int token;      /* input token of the next step */
   int position;   /* KV slot the next step writes (cache_len = position + 1) */
-  unsigned epoch; /* exchange tag base of the next step (set by mq_decode_step_init) */
+  unsigned epoch; /* output only: the exchange epoch the last step used (launches take their
+                     epoch from the library workspace, one more than the previous launch's) */
   int count;      /* steps done: out_ids[count] receives the next step's token */
 } MqDecodeStep;
 
@@ -106,6 +107,24 @@ int launch_ldg_decode_noalloc(int input_token_id, int* output_token_id, const vo
                               void* v_cache, void* hidden_buffer, void* g_normalized, int num_layers, int position,
                               int cache_len, int max_seq_len, float attn_scale, hipStream_t stream);
 
+/* Decode-kernel variants of mq_decode_variant. */
+#define MQ_VARIANT_BASELINE 0 /* the kernel instance for each step's position (launch_ldg_decode's choice) */
+#define MQ_VARIANT_UNSPLIT 1  /* instance 0: one attention workgroup per XCD; positions < 256 only */
+#define MQ_VARIANT_SPLIT 2    /* instances 1/2: attention split into chunks; every position */
+
+/* launch_ldg_decode_with_logits (logits_output may be NULL) with the decode-kernel
+ * instance fixed by a variant instead of chosen per step. The MI355X counterpart of the
+ * reference's variant policy, which compiles one source variant per kernel module
+ * (chat.py:17-29, 36-46, 59-64); the reference's C ABI has no such entry. Returns
+ * MQ_ERR_ARG for an unknown variant or for MQ_VARIANT_UNSPLIT at position >= 256. All
+ * variants give the same tokens, logits and caches (the instances differ only in how
+ * the attention work is split across workgroups). */
+int mq_decode_variant(int variant, int input_token_id, int* output_token_id, float* logits_output,
+                      const void* embed_weight, const LDGLayerWeights* layer_weights, const void* final_norm_weight,
+                      const void* lm_head_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                      void* v_cache, void* hidden_buffer, void* g_normalized, int num_layers, int position,
+                      int cache_len, int max_seq_len, float attn_scale, hipStream_t stream);
+
 /* One decoder block at `position` on a given bf16 hidden vector (no embedding,
  * no LM head): hidden_out = layer(hidden_in); K/V slot `position` of the
  * single-layer caches k_cache/v_cache ([1, 8, max_seq_len, 128]) is written.
@@ -133,7 +152,8 @@ int mq_decode_layer(const void* hidden_in, void* hidden_out, const LDGLayerWeigh
  *     [1184], block_max_idxs i32 [1184]. Every buffer needs 16-byte alignment.
  *     residual, o_proj_out and down_out are accepted and unused (the epilogues fuse
  *     those steps); they may be NULL.
- *   hidden_bf16_out [1024]: the last row's final hidden state (before the final norm).
+ *   hidden_bf16_out [1024]: a copy of final_hidden (the last row after the final norm), as
+ *                    the reference copies it (csrc/megakernel/fused_prefill.cu:843-849).
  *   On return (stream-ordered): *output_token_id = argmax of the last row's bf16
  *   logits (lowest index on ties), or -2 if an input id was outside [0, 151936). */
 int launch_prefill_float(const int* input_token_ids, int* output_token_id, int seq_len, const void* embed_weight,
@@ -147,11 +167,11 @@ int launch_prefill_float(const int* input_token_ids, int* output_token_id, int s
 
 /* Device-resident generation (reference idea: experimental/qwen_persistent_kernel.cu:1028-1033,
  * which reads token and position from device memory so a captured graph can replay).
- * mq_decode_step_init writes {token, position, epoch, 0} to `step` (stream-ordered copy of
- * pageable host memory) and reserves `capacity` launch epochs for it. Then up to
+ * mq_decode_step_init writes {token, position, 0, 0} to `step` (stream-ordered copy of
+ * pageable host memory, then a stream synchronisation). Then up to
  * `capacity` launches of mq_decode_step_device (directly, or as nodes of a captured HIP
  * graph: the launch itself does no memset, copy or allocation) each decode one token of
- * the full model like launch_ldg_decode, taking token/position/epoch from `step`,
+ * the full model like launch_ldg_decode, taking token and position from `step`,
  * appending the greedy token to out_ids[count] and advancing `step`. No host read is
  * needed between steps. split_instance: 0 runs the kernel instance for contexts of at
  * most 256 positions (a step past that fails with a negative token), 1 and 2 the
@@ -183,8 +203,10 @@ int mq_set_launch_mode(int cooperative);
  * reports the flags as a negative token; mq_reset_workspace clears them. Synchronous. */
 int mq_debug_set_error(int device, unsigned flags);
 
-/* Zero this device's workspace (exchange buffers and counters). Needed only
- * after a launch reported a watchdog error. Synchronous. */
+/* Zero this device's workspaces (exchange buffers and counters): the library's allocated
+ * workspace and, once launch_ldg_decode_noalloc has been called on this device, that entry
+ * point's file-scope workspace too (a synchronous memset: it allocates nothing). Needed
+ * only after a launch reported a watchdog error. Synchronous. */
 int mq_reset_workspace(int device);
 
 /* Human-readable name of a status code. */

@@ -17,6 +17,10 @@ MQ_ERR_ARG = -1
 MQ_ERR_HIP = -2
 MQ_ERR_DEVICE = -3
 MQ_ERR_ALLOC = -4
+# decode-kernel variants of mq_decode_variant (include/megaqwen_amd.h)
+MQ_VARIANT_BASELINE = 0
+MQ_VARIANT_UNSPLIT = 1
+MQ_VARIANT_SPLIT = 2
 # Longest context of the decode kernel (positions 0 .. MAX_CONTEXT - 1; mq_decode_plan
 # rejects the rest)
 MAX_CONTEXT = 16384
@@ -60,6 +64,9 @@ SIGNATURES = {
     "launch_ldg_decode": _DECODE_ARGS,
     "launch_ldg_decode_with_logits": _DECODE_ARGS[:2] + [_vp] + _DECODE_ARGS[2:],
     "launch_ldg_decode_noalloc": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp],
+    # variant, token, out, logits, embed, layers, final norm, lm head, cos, sin, k, v, hidden, normed,
+    # num_layers, position, cache_len, max_seq_len, scale, stream
+    "mq_decode_variant": [_i, _i, _vp, _vp] + [_vp] * 10 + [_i, _i, _i, _i, _f, _vp],
     "mq_decode_layer": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _f, _vp],
     # ids, out, seq_len, embed, layers (host array), final norm, lm head, cos, sin, k, v, 17 scratch,
     # num_layers, max_seq_len, scale, stream

@@ -12,15 +12,15 @@ block_max_idxs) are accepted and ignored, except `hidden_buffer` and
 as in the reference.
 
 Variants. The reference's variants are NVIDIA source rewrites (fast-math,
-128-block grids). The MI355X knob is the decode kernel instance
-(`mq_decode_plan`): "unsplit" attends with one workgroup per XCD and serves
-contexts of at most SHORT_CONTEXT_POSITIONS positions; "split" splits the
-attention over up to 16 workgroups per XCD and serves every length (past 4096
-positions the variant of it that pipelines a chunk's LDS passes); "baseline"
-picks per step (the launcher's own choice, always the faster valid instance).
-The host-driven `decode_ldg` path always picks per step; the variant selects the
-instance of the device-resident generation loop, whose launches cannot switch
-instance mid-run.
+128-block grids), one compiled module each (`chat.py:36-46, 59-64`). The MI355X knob
+is the decode kernel instance (`mq_decode_plan`), and a kernel object's variant
+fixes it for every `decode_ldg` launch (C ABI `mq_decode_variant`): "unsplit"
+attends with one workgroup per XCD and serves contexts of at most
+SHORT_CONTEXT_POSITIONS positions (a step past that raises ValueError); "split"
+splits the attention over up to 16 workgroups per XCD and serves every length
+(past 4096 positions the instance that pipelines a chunk's LDS passes);
+"baseline" picks per step (the launcher's own choice, the faster valid instance).
+All three give the same tokens, logits and caches.
 """
 
 from __future__ import annotations
@@ -41,6 +41,9 @@ INTERMEDIATE_SIZE = C.INTERMEDIATE_SIZE
 MAX_SEQ_LEN = 512  # chat.py:15
 
 SUPPORTED_DECODE_KERNEL_VARIANTS = ("baseline", "unsplit", "split")
+# variant -> mq_decode_variant's variant code
+_VARIANT_CODE = {"baseline": _abi.MQ_VARIANT_BASELINE, "unsplit": _abi.MQ_VARIANT_UNSPLIT,
+                 "split": _abi.MQ_VARIANT_SPLIT}
 AUTO_KERNEL_VARIANT = "auto"
 # Longest context the "unsplit" instance serves (the kernel's one-pass LDS capacity).
 SHORT_CONTEXT_POSITIONS = 256
@@ -108,19 +111,19 @@ class LDGKernel:
             raise RuntimeError("call init_ldg_layer_weights and init_ldg_embed_weight first")
         if num_layers > self._num_layers:
             raise ValueError(f"num_layers {num_layers} exceeds the {self._num_layers} initialised layers")
+        if self.variant == "unsplit" and position >= SHORT_CONTEXT_POSITIONS:
+            raise ValueError(f"the 'unsplit' kernel variant serves positions below {SHORT_CONTEXT_POSITIONS}, "
+                             f"got {position}; use 'split' or 'baseline'")
+        # the reference's other scratch tensors (g_activations .. block_max_idxs) are accepted and unused
+        del g_activations, g_residual, g_q, g_k, g_v, g_attn_out, g_mlp_intermediate, block_max_vals, block_max_idxs
         out = torch.empty(1, dtype=torch.int32, device=k_cache.device)
-        args = [int(input_token_id), _ptr(out)]
-        if logits is not None:
-            args.append(_ptr(logits))
-        args += [_ptr(self._embed), _ptr(self._d_layer_weights), _ptr(final_norm_weight), _ptr(lm_head_weight),
-                 _ptr(cos_table), _ptr(sin_table), _ptr(k_cache), _ptr(v_cache), _ptr(hidden_buffer),
-                 _ptr(g_activations), _ptr(g_residual), _ptr(g_q), _ptr(g_k), _ptr(g_v), _ptr(g_attn_out),
-                 _ptr(g_mlp_intermediate), _ptr(g_normalized), _ptr(block_max_vals), _ptr(block_max_idxs),
-                 int(num_layers), int(position), int(cache_len), int(max_seq_len), 1.0 / math.sqrt(HEAD_DIM),
-                 torch.cuda.current_stream().cuda_stream]
+        args = [_VARIANT_CODE[self.variant], int(input_token_id), _ptr(out), _ptr(logits), _ptr(self._embed),
+                _ptr(self._d_layer_weights), _ptr(final_norm_weight), _ptr(lm_head_weight), _ptr(cos_table),
+                _ptr(sin_table), _ptr(k_cache), _ptr(v_cache), _ptr(hidden_buffer), _ptr(g_normalized),
+                int(num_layers), int(position), int(cache_len), int(max_seq_len), 1.0 / math.sqrt(HEAD_DIM),
+                torch.cuda.current_stream().cuda_stream]
         lib = _abi.lib()
-        fn = lib.launch_ldg_decode_with_logits if logits is not None else lib.launch_ldg_decode
-        _abi.check(fn(*args), "launch_ldg_decode")
+        _abi.check(lib.mq_decode_variant(*args), f"decode_ldg ({self.variant} variant)")
         tok = int(out.item())  # the reference synchronises the stream and reads the token (chat.py:250-251)
         if tok < 0:
             lib.mq_reset_workspace(k_cache.device.index or 0)

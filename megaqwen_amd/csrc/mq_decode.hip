@@ -145,6 +145,12 @@ constexpr uint32_t WS_RESERVED = 0;  // (words 0..31 unused)
 constexpr uint32_t WS_ERR = 32;
 constexpr uint32_t WS_FINAL_TICKET = 64;
 // word WS_PREFILL_ERR (96) belongs to the prefill kernels
+// The epoch of the workspace's last completed launch: a launch tags its exchanges with this
+// value + 1 and its last workgroup stores that back, so consecutive launches on one workspace
+// differ by exactly one epoch whichever entry point makes them (host-driven and
+// device-resident launches share the allocated workspace and its count; the no-allocation
+// entry point's workspace keeps its own).
+constexpr uint32_t WS_EPOCH = 128;
 // per-XCD regions of tagged words, written and read only by that XCD's workgroups
 constexpr uint32_t WS_LOCAL = 1024;
 constexpr uint32_t LOCAL_WORDS = 32768;
@@ -213,9 +219,8 @@ struct DecodeParams {
   int max_seq_len;
   float attn_scale;
   int mode;
-  uint32_t epoch;  // launch counter of the device (the host's): tags of this launch's exchanges
-  // MODE_DEVICE_STEP: token, position and epoch come from *step (advanced by the launch's
-  // last workgroup), and each launch's token is appended to out_ids[step->count]
+  // MODE_DEVICE_STEP: token and position come from *step (advanced by the launch's last
+  // workgroup), and each launch's token is appended to out_ids[step->count]
   MqDecodeStep* step;
   int* out_ids;
   int out_capacity;
@@ -843,6 +848,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ float s_bestv[8];
   __shared__ int s_besti[8];
   __shared__ uint32_t s_flag;
+  __shared__ uint32_t s_epoch;                         // this launch's epoch
   float* s_lg = reinterpret_cast<float*>(s_kv);  // this workgroup's logits (K/V rows are dead by then)
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -861,16 +867,18 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   const int m = ga ? j : j - NGA;          // member index within the group
   uint32_t* ws = P.ws;
   const Buf wsb(ws);
-  // token, position, epoch: kernel arguments, or a device-resident step written by the
-  // previous launch's last workgroup (visible at this launch's start)
+  // token and position: kernel arguments, or a device-resident step written by the previous
+  // launch's last workgroup. Launches on one stream do not overlap (a launch's first
+  // workgroup starts after the previous launch's last one has finished), so the step, like
+  // the workspace's epoch word, holds the previous launch's values; both are written and
+  // read with device-scope (sc1) accesses.
   MQ_STAMP(32 * 40 + 4);
   int token = P.token, p = P.position, step_count = 0;
-  uint32_t epoch = P.epoch;
+  uint32_t epoch = 0;  // this launch's exchange epoch: set from the workspace at P00
   if (P.mode & MODE_DEVICE_STEP) {
-    const u32x4 sv = *(const gu32x4*)(const void*)P.step;
+    const u32x4 sv = Buf(P.step).ld4(0);
     token = (int)__builtin_amdgcn_readfirstlane(sv.x);
     p = (int)__builtin_amdgcn_readfirstlane(sv.y);
-    epoch = __builtin_amdgcn_readfirstlane(sv.z);
     step_count = (int)__builtin_amdgcn_readfirstlane(sv.w);
     // Every workgroup reads the same step, so all of them leave here together. The first
     // failing step records its error; later launches find the negative token and return.
@@ -927,9 +935,15 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   if (wave < NSW) {
     // ==================================================================== stream waves
     const int s = wave, st = tid;  // st: stream thread 0..255
+    // the workspace's epoch word, loaded ahead of the pointer table (a wave's loads complete
+    // in order, so it has landed when the table has)
+    uint32_t ew = 0;
+    if (st == 0) ew = wsb.ld1(WS_EPOCH * 4u);
     for (int i = st; i < L * 11; i += NSW * 64)
       s_lw[i / 11][i % 11] = reinterpret_cast<const uint16_t* const*>(P.layers)[i];
-    BAR();  // P00: pointer table visible
+    if (st == 0) s_epoch = ew + 1u;
+    BAR();  // P00: pointer table and epoch visible
+    epoch = __builtin_amdgcn_readfirstlane(s_epoch);
     auto wp = [&](int l, int k) -> const uint16_t* { return uniform_ptr(s_lw[l][k]); };
     if (lm) {
       const u32x2 fn = ldw2(P.final_norm + 4 * st);
@@ -1231,6 +1245,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       else s_sin[i - HD] = bf2f(ldraw16(P.sin_tab + (size_t)p * HD + i - HD));
     }
     BAR();  // P00
+    epoch = __builtin_amdgcn_readfirstlane(s_epoch);
     BAR();  // P0
 
     // RMSNorm of a gathered residual-stream vector (chunks lane + 64k, k < 4): poll wave c
@@ -1504,6 +1519,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     // The workgroup's 64 residual rows (lane = row) from the 8 XCDs' partial sums
     // (identical on every XCD): group A reduces o_proj into h1, group B down_proj into h.
     BAR();  // P00
+    epoch = __builtin_amdgcn_readfirstlane(s_epoch);
     BAR();  // P0
     const int row = ROWS * m + lane;
     // group B with b_h1: this workgroup's 64 rows of the residual stream h (the embedding or
@@ -1585,6 +1601,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       s_ssn = 0u;
     }
     BAR();  // P00
+    epoch = __builtin_amdgcn_readfirstlane(s_epoch);
     BAR();  // P0
     // Every launch writes or clears every exchange word it could ever poll, so that the
     // content a poll can find before the awaited write is at most one launch old, whose
@@ -1832,26 +1849,29 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
     const int res = err ? -(int)(1u + err) : tok;
     *P.out_token = res;
     if (P.mode & MODE_DEVICE_STEP) {
-      // the next launch's input: this token at the next position, with the next epoch (a
-      // failed step keeps its position, and its negative token stops the launches after it)
+      // the next launch's input: this token at the next position (a failed step keeps its
+      // position, and its negative token stops the launches after it); the epoch field
+      // records the epoch this step used
       P.out_ids[step_count] = res;
-      *reinterpret_cast<u32x4*>(P.step) =
-          u32x4{(uint32_t)res, (uint32_t)(res >= 0 ? p + 1 : p), epoch + 1u, (uint32_t)(step_count + 1)};
+      Buf(P.step).st4(u32x4{(uint32_t)res, (uint32_t)(res >= 0 ? p + 1 : p), epoch, (uint32_t)(step_count + 1)}, 0);
     }
     wsb.st1(0u, WS_ERR * 4u);
     wsb.st1(0u, WS_FINAL_TICKET * 4u);
+    wsb.st1(epoch, WS_EPOCH * 4u);
   }
 }
 
 // ---------------------------------------------------------------- host side
+// The library's workspace of a device. A launch takes its exchange epoch from the
+// workspace itself (WS_EPOCH, advanced by each launch's last workgroup), not from the host:
+// launches on one stream run one after another (the next launch's first workgroup starts
+// about 1 us after the previous launch's last workgroup has finished, measured with
+// s_memrealtime stamps for ordinary launches and for HIP graph replays alike), so every
+// workgroup of a launch reads the epoch the previous launch on this workspace stored.
 struct DeviceState {
   bool init = false;
   int status = MQ_OK;
   uint32_t* ws = nullptr;
-  // Launches on the device so far. The epoch comes from the host rather than from the
-  // workspace: an ordinary launch may start its first workgroups on CUs that the previous
-  // launch has already released while that launch's last workgroup is still finishing.
-  std::atomic<uint32_t> launches{0};
 };
 static std::mutex g_mu;
 static DeviceState g_dev[64];
@@ -1936,7 +1956,6 @@ static int launch(DecodeParams& P, hipStream_t stream, int split_instance = -1, 
     P.ws = g_dev[dev].ws;
     if (!P.out_token) P.out_token = reinterpret_cast<int*>(g_dev[dev].ws + WS_WORDS);
   }
-  if (!(P.mode & MODE_DEVICE_STEP)) P.epoch = g_dev[dev].launches.fetch_add(1u, std::memory_order_relaxed) + 1u;
   // All NWG workgroups must be resident at once. Each one needs a whole CU
   // (its LDS use exceeds half a CU's), ensure_device() checked that the GPU has
   // NWG such slots, and every inter-workgroup wait in the kernel ends in an
@@ -1976,7 +1995,8 @@ static int decode_entry(int input_token_id, int* output_token_id, float* logits_
                         const LDGLayerWeights* layer_weights, const void* final_norm_weight,
                         const void* lm_head_weight, const void* cos_table, const void* sin_table, void* k_cache,
                         void* v_cache, void* hidden_buffer, void* g_normalized, int num_layers, int position,
-                        int cache_len, int max_seq_len, float attn_scale, hipStream_t stream, bool noalloc) {
+                        int cache_len, int max_seq_len, float attn_scale, hipStream_t stream, bool noalloc,
+                        int split_instance = -1) {
   if (!output_token_id || !embed_weight || !layer_weights || !final_norm_weight || !lm_head_weight || !cos_table ||
       !sin_table || !k_cache || !v_cache || !hidden_buffer)
     return MQ_ERR_ARG;
@@ -2002,7 +2022,7 @@ static int decode_entry(int input_token_id, int* output_token_id, float* logits_
   P.max_seq_len = max_seq_len;
   P.attn_scale = attn_scale;
   P.mode = logits_output ? MODE_LOGITS : 0;
-  return launch(P, stream, -1, noalloc);
+  return launch(P, stream, split_instance, noalloc);
 }
 
 extern "C" int launch_ldg_decode_with_logits(int input_token_id, int* output_token_id, float* logits_output,
@@ -2047,6 +2067,30 @@ extern "C" int launch_ldg_decode_noalloc(int input_token_id, int* output_token_i
                       position, cache_len, max_seq_len, attn_scale, stream, true);
 }
 
+extern "C" int mq_decode_variant(int variant, int input_token_id, int* output_token_id, float* logits_output,
+                                 const void* embed_weight, const LDGLayerWeights* layer_weights,
+                                 const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
+                                 const void* sin_table, void* k_cache, void* v_cache, void* hidden_buffer,
+                                 void* g_normalized, int num_layers, int position, int cache_len, int max_seq_len,
+                                 float attn_scale, hipStream_t stream) {
+  // variant -> kernel instance: baseline picks per step, unsplit is instance 0 (contexts of
+  // at most KV_CAP positions only), split is instance 1, or 2 where a chunk takes more than
+  // one LDS pass
+  int inst = -1;
+  if (variant == MQ_VARIANT_UNSPLIT) {
+    if (position < 0 || position >= KV_CAP) return MQ_ERR_ARG;
+    inst = 0;
+  } else if (variant == MQ_VARIANT_SPLIT) {
+    if (position < 0 || position >= MAX_CTX) return MQ_ERR_ARG;
+    inst = plan_instance(position) == 0 ? 1 : plan_instance(position);
+  } else if (variant != MQ_VARIANT_BASELINE) {
+    return MQ_ERR_ARG;
+  }
+  return decode_entry(input_token_id, output_token_id, logits_output, embed_weight, layer_weights, final_norm_weight,
+                      lm_head_weight, cos_table, sin_table, k_cache, v_cache, hidden_buffer, g_normalized, num_layers,
+                      position, cache_len, max_seq_len, attn_scale, stream, false, inst);
+}
+
 extern "C" int mq_decode_layer(const void* hidden_in, void* hidden_out, const LDGLayerWeights* layer_weights,
                                const void* cos_table, const void* sin_table, void* k_cache, void* v_cache,
                                int position, int max_seq_len, float attn_scale, hipStream_t stream) {
@@ -2078,9 +2122,7 @@ extern "C" int mq_decode_step_init(MqDecodeStep* step, int token, int position, 
   if (hipGetDevice(&dev) != hipSuccess) return MQ_ERR_HIP;
   const int st = ensure_device(dev);
   if (st != MQ_OK) return st;
-  // the epochs first .. first + capacity - 1 belong to these steps alone
-  const uint32_t first = g_dev[dev].launches.fetch_add((uint32_t)capacity, std::memory_order_relaxed) + 1u;
-  const MqDecodeStep h{token, position, first, 0};
+  const MqDecodeStep h{token, position, 0u, 0};
   return hipMemcpyAsync(step, &h, sizeof(h), hipMemcpyHostToDevice, stream) == hipSuccess &&
                  hipStreamSynchronize(stream) == hipSuccess
              ? MQ_OK
@@ -2155,6 +2197,14 @@ extern "C" int mq_reset_workspace(int device) {
   if (hipGetDevice(&cur) != hipSuccess) return MQ_ERR_HIP;
   if (hipSetDevice(device) != hipSuccess) return MQ_ERR_HIP;
   hipError_t e = hipMemset(g_dev[device].ws, 0, WS_BYTES);
+  // the no-allocation entry point's workspace (`scratch`, through its device address) as well,
+  // once that entry point has set it up on this device (a synchronous memset allocates nothing)
+  uint32_t* na = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_noalloc[device].init && g_noalloc[device].status == MQ_OK) na = g_noalloc[device].ptr;
+  }
+  if (e == hipSuccess && na) e = hipMemset(na, 0, sizeof(uint32_t) * WS_WORDS);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (hipSetDevice(cur) != hipSuccess) return MQ_ERR_HIP;
   return e == hipSuccess ? MQ_OK : MQ_ERR_HIP;

@@ -1207,7 +1207,8 @@ __global__ void __launch_bounds__(64 * F2W) attn_prefill_fa2(const uint16_t* q, 
 constexpr int LMB = 1184;  // partial-argmax blocks (the length of the reference's block_max_* buffers)
 
 // Final norm of the last hidden row (every workgroup computes it; workgroup 0 also
-// writes it to final_hidden and the raw row to hidden_out), then the bf16 logits of
+// writes it to final_hidden and to hidden_out, as the reference copies final_hidden into
+// hidden_bf16_out, csrc/megakernel/fused_prefill.cu:843-849), then the bf16 logits of
 // rows [VOCAB * b / LMB, VOCAB * (b+1) / LMB) of the tied LM head and their argmax
 // (lowest index on ties).
 __global__ void __launch_bounds__(256) lm_partial(const uint16_t* hlast, const uint16_t* fnw, const uint16_t* lm,
@@ -1231,7 +1232,7 @@ __global__ void __launch_bounds__(256) lm_partial(const uint16_t* hlast, const u
   s_x[2 * tid + 1] = n1;
   if (b == 0) {
     reinterpret_cast<u32x2*>(final_hidden)[tid] = u32x2{n0, n1};
-    reinterpret_cast<u32x2*>(hidden_out)[tid] = xw;
+    reinterpret_cast<u32x2*>(hidden_out)[tid] = u32x2{n0, n1};
   }
   __syncthreads();
   const u32x4 xa = reinterpret_cast<const u32x4*>(s_x)[lane], xb = reinterpret_cast<const u32x4*>(s_x)[64 + lane];

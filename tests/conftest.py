@@ -62,5 +62,25 @@ def gpu_weights(state_dict):
     }
 
 
+@pytest.fixture(scope="session")
+def gpu_weights_gamma():
+    """The seeded weights with random norm gains (every norm weight bf16(1 + 0.1 randn),
+    distinct per layer and norm) on the GPU, RoPE tables for 1024 positions."""
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from megaqwen_amd import rope, weights
+
+    sd = weights.make_state_dict(seed=0, norms="random")
+    dev = "cuda"
+    embed = sd["model.embed_tokens.weight"].to(dev)
+    cos, sin = rope.rope_tables(1024)
+    return {"state_dict": sd, "embed_weight": embed,
+            "layer_weights": [t.to(dev) for t in weights.layer_weights_flat(sd)],
+            "final_norm_weight": sd["model.norm.weight"].to(dev), "lm_head_weight": embed,
+            "cos_table": cos.to(dev), "sin_table": sin.to(dev)}
+
+
 def load_npz(name):
     return np.load(golden(name), allow_pickle=False)

@@ -171,3 +171,25 @@ def test_noalloc_entry_rejects_sizes_past_its_limit():
     assert L.launch_ldg_decode_noalloc(*(base + [28, 16384, 16385, 20000, 0.088, None])) == _abi.MQ_ERR_ARG
     assert L.launch_ldg_decode_noalloc(*(base + [33, 0, 1, 16, 0.088, None])) == _abi.MQ_ERR_ARG
     assert L.launch_ldg_decode_noalloc(*([1, None] + [1] * 9 + [1, 28, 0, 1, 16, 0.088, None])) == _abi.MQ_ERR_ARG
+
+
+def test_decode_variant_rejects_invalid_arguments():
+    """mq_decode_variant: an unknown variant, the unsplit variant from position 256 on, and the
+    decode entry's own argument checks give MQ_ERR_ARG before any HIP call."""
+    L = _abi.lib()
+    good = [1, 1, None] + [1] * 10 + [28, 300, 301, 512, 0.088, None]  # token .. stream, position 300
+
+    def call(variant, **kw):
+        a = list(good)
+        if "position" in kw:
+            a[14], a[15] = kw["position"], kw["position"] + 1
+        if "out" in kw:
+            a[1] = kw["out"]
+        return L.mq_decode_variant(variant, *a)
+
+    assert call(3) == _abi.MQ_ERR_ARG and call(-1) == _abi.MQ_ERR_ARG
+    assert call(_abi.MQ_VARIANT_UNSPLIT, position=256) == _abi.MQ_ERR_ARG
+    assert call(_abi.MQ_VARIANT_UNSPLIT, position=300) == _abi.MQ_ERR_ARG
+    assert call(_abi.MQ_VARIANT_SPLIT, position=16384) == _abi.MQ_ERR_ARG
+    for v in (_abi.MQ_VARIANT_BASELINE, _abi.MQ_VARIANT_UNSPLIT, _abi.MQ_VARIANT_SPLIT):
+        assert call(v, position=10, out=None) == _abi.MQ_ERR_ARG

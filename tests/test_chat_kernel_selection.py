@@ -61,3 +61,17 @@ def test_decode_ldg_needs_init():
     t = torch.zeros(1)
     with pytest.raises(RuntimeError, match="init_ldg_layer_weights"):
         k.decode_ldg(1, t, t, t, t, t, t, t, t, t, t, t, t, t, t, t, t, t, 28, 0, 1, 512)
+
+
+def test_unsplit_variant_refuses_long_contexts_before_launching():
+    """The variant fixes the kernel instance of every decode_ldg launch: "unsplit" (instance 0,
+    contexts of at most 256 positions) raises for a step at position 256 or later, on the
+    host, before any launch."""
+    import torch
+
+    k = compile_kernel("unsplit")
+    k._d_layer_weights, k._embed, k._num_layers = torch.zeros(1), torch.zeros(1), 28
+    t = torch.zeros(1)
+    with pytest.raises(ValueError, match="'unsplit' kernel variant serves positions below 256"):
+        k.decode_ldg(1, t, t, t, t, t, t, t, t, t, t, t, t, t, t, t, t, t, 28, SHORT_CONTEXT_POSITIONS,
+                     SHORT_CONTEXT_POSITIONS + 1, 512)

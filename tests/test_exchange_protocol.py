@@ -14,7 +14,11 @@ against every stale content that a sequence of launches of any kinds can leave b
   launches (1 layer), in any order and number;
 * 16-bit tags: 1 + ((32 epoch + layer) mod 65535), in the high half of a bf16 word;
   32-bit tags: 32 epoch + layer + 1, beside an fp32 value;
-* epochs are distinct per launch and increase (one counter per device).
+* epochs: a launch takes the epoch its workspace holds plus one, and its last workgroup
+  stores that epoch back (launches on one stream run one after another), so consecutive
+  launches on one workspace differ by exactly one epoch. Two workspaces exist: the
+  allocated one (host-driven and device-resident launches) and the no-allocation entry
+  point's; launches on the two interleave in any order.
 
 The word-level coverage (each region's words written at each layer by the workgroups'
 lanes) is checked from the kernel's index formulas, restated here.
@@ -211,3 +215,80 @@ def test_cross_xcd_partials_cover_every_row():
         assert 2 * ((m * NXCD + g) * ROWS + lane) == 2 * (m * NXCD * ROWS + lane) + 2 * ROWS * g
     # both arrays fit between the per-XCD regions and the LM-head partials
     assert 2 * NGA * ROWS * NXCD + 2 * NGB * ROWS * NXCD == 32768
+
+
+# ---------------------------------------------------------------- epochs across workspaces
+
+def _launch_polls_ok(region, E, L, prev):
+    """Every poll of a launch (epoch E, L layers) finds no stale word with the polled tag;
+    `prev` = (epoch, layers) of the previous launch on the same workspace, or None (the
+    workspace is zero)."""
+    for layer in reads(region, L):
+        want = expected_tag(region, E, layer, L)
+        fl = fresh_write_layer(region, layer)
+        if fl >= 1:
+            stale = {written_tag(region, E, fl - 1)}
+        else:
+            stale = {0}
+            if prev is not None:
+                stale.add(written_tag(region, prev[0], prev[1] - 1))
+        if want in stale:
+            return False
+    return True
+
+
+def _run(sequence, epoch_of, only=None):
+    """Simulate launches [(workspace, layers)]: epoch_of(state, ws) gives a launch's epoch and
+    advances the state. Returns the first (index, region) whose poll could accept a stale
+    word, or None (only: check the launches on that workspace alone)."""
+    state = {"ws": {}, "counter": 0}
+    last = {}
+    for i, (ws, L) in enumerate(sequence):
+        E = epoch_of(state, ws)
+        for region in REGIONS if only in (None, ws) else ():
+            if not _launch_polls_ok(region, E, L, last.get(ws)):
+                return i, region
+        last[ws] = (E, L)
+    return None
+
+
+def _per_workspace_epoch(state, ws):  # the kernel's rule: the workspace's stored epoch + 1
+    E = state["ws"].get(ws, 0) + 1
+    state["ws"][ws] = E
+    return E
+
+
+def _shared_host_counter(state, ws):  # the earlier rule: one host counter per device
+    state["counter"] += 1
+    return state["counter"]
+
+
+def test_interleaved_workspaces_never_alias():
+    """Launches on the allocated and the no-allocation workspace in any interleaving, of 1, 2,
+    28 or 32 layers: with per-workspace epochs no poll can accept a stale word, including
+    after runs of 2047 and 55295 launches on the other workspace (the distances at which
+    a shared counter aliases, below)."""
+    import random
+
+    rng = random.Random(7)
+    for trial in range(40):
+        seq = [(rng.choice("an"), rng.choice((1, 2, 28, 32))) for _ in range(rng.randint(2, 60))]
+        assert _run(seq, _per_workspace_epoch) is None, seq
+    for gap in (2047, 55295):
+        for Lp in (2, 28):
+            seq = [("n", Lp)] + [("a", 28)] * gap + [("n", 28)]
+            assert _run(seq, _per_workspace_epoch, only="n") is None
+
+
+def test_a_shared_epoch_counter_would_alias():
+    """Why epochs are per workspace: with one counter for both workspaces, a no-allocation
+    launch d epochs after the previous one on its workspace polls its first layer for the
+    tag that launch's last layer (L' layers) left when 32 d == L' - 1 (mod 65535), i.e.
+    d == 2048 (L' - 1): 2048 after a 2-layer launch, 55296 after a 28-layer one."""
+    for Lp in (2, 28):
+        d = (2048 * (Lp - 1)) % 65535
+        assert tag16(100, Lp - 1) == tag16(100 + d, 0)
+        seq = [("n", Lp)] + [("a", 28)] * (d - 1) + [("n", 28)]
+        hit = _run(seq, _shared_host_counter, only="n")
+        assert hit is not None and hit[0] == len(seq) - 1, hit
+        assert _run(seq, _per_workspace_epoch, only="n") is None

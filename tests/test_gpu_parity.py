@@ -23,24 +23,11 @@ import torch
 
 from conftest import load_npz
 from megaqwen_amd import megakernel_decode as MK
-from megaqwen_amd import rope, weights
 from oracle import qwen3_oracle as O
 from parity_helpers import (DECODE_PATH_FLOORS, LOGIT_FRAC_OVER_2E2, LOGIT_MAX_ABS, LOGIT_MEAN_ABS, TIE_TOL, f32,
                             hf_tie_set, logit_stats, ulp_close)
 
 pytestmark = pytest.mark.gpu
-
-
-@pytest.fixture(scope="module")
-def gpu_weights_gamma():
-    sd = weights.make_state_dict(seed=0, norms="random")
-    dev = "cuda"
-    embed = sd["model.embed_tokens.weight"].to(dev)
-    cos, sin = rope.rope_tables(1024)
-    return {"state_dict": sd, "embed_weight": embed,
-            "layer_weights": [t.to(dev) for t in weights.layer_weights_flat(sd)],
-            "final_norm_weight": sd["model.norm.weight"].to(dev), "lm_head_weight": embed,
-            "cos_table": cos.to(dev), "sin_table": sin.to(dev)}
 
 
 def _decoder(w, max_seq=1024):

@@ -75,8 +75,10 @@ def test_prefill_vs_oracle_ragged(state_dict, embed_gpu, S):
     hg = f32(dec.hidden_float_[:S])
     print(f"hidden rel L2 {rel_l2(hg, h):.3g}")
     assert rel_l2(hg, h) < 1e-2
-    assert rel_l2(f32(dec.hidden_buffer_), h[-1]) < 1e-2
     assert np.max(np.abs(f32(dec.final_hidden_) - y[-1])) <= 0.1
+    # hidden_bf16_out receives a copy of final_hidden (the final-norm row), as in the reference
+    # (csrc/megakernel/fused_prefill.cu:843-849)
+    assert torch.equal(dec.hidden_buffer_, dec.final_hidden_)
     top2 = np.sort(olg)[-2:]
     if top2[1] - top2[0] > 2 * LOGIT_MAX_ABS:
         assert tok == otok
