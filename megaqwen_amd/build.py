@@ -51,19 +51,23 @@ def build(verbose: bool = False) -> str:
 
 TRACE_SRC = os.path.join(CSRC, "trace", "mq_decode_trace.cpp")
 TRACE_BIN = os.path.join(CSRC, "trace", "mq_decode_trace")
+PROBE_SRC = os.path.join(CSRC, "trace", "stream_order_probe.hip")
+PROBE_BIN = os.path.join(CSRC, "trace", "stream_order_probe")
 
 
 def build_trace(verbose: bool = False) -> str:
-    """Compile the tracing build of the decode kernel (a stand-alone executable that prints
-    the per-stage critical path of a layer); returns its path."""
+    """Compile the profiling tools: the tracing build of the decode kernel (a stand-alone
+    executable that prints the per-stage critical path of a layer) and the stream-order
+    probe; returns the tracing build's path."""
     flags = [f for f in FLAGS if f not in ("-fPIC", "-shared")]
-    cmd = [HIPCC, *flags, TRACE_SRC, "-o", TRACE_BIN]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
+    for src, out in ((TRACE_SRC, TRACE_BIN), (PROBE_SRC, PROBE_BIN)):
+        cmd = [HIPCC, *flags, src, "-o", out]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            sys.stderr.write(res.stdout + res.stderr)
+            raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
     return TRACE_BIN
 
 
