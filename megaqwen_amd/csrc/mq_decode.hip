@@ -385,10 +385,12 @@ __device__ __forceinline__ void wait_count(uint32_t* cnt, uint32_t target) {
 // whole launch: the LDS copy is cleared once and the copies only ever fill rows < nc).
 //
 // Scores s_sc[h][r] = (q_h . k_r) * scale for r < nc (-inf past nc), from MFMA tiles
-// of 16 rows: wave v takes row blocks v and v + 8. Each wave also leaves the maximum
-// of its scores per head in s_mx[v].
-__device__ __forceinline__ void attn_scores(const uint8_t* s_kv, const uint16_t* s_q, float (*s_sc)[KV_CAP],
-                                            float (*s_mx)[2], int nc, float scale, int v, int lane) {
+// of 16 rows: wave v takes row blocks v and v + 8, NB of them (the blocks that hold a row
+// below nc; the others are neither read nor written: no later phase reads s_sc past nc).
+// Returns the wave's maximum of its scores per head (lanes 0 and 1: heads 0 and 1).
+template <int NB>
+__device__ __forceinline__ float attn_score_blocks(const uint8_t* s_kv, const uint16_t* s_q, float (*s_sc)[KV_CAP],
+                                                   int nc, float scale, int v, int lane) {
   const int r16 = lane & 15, kg = lane >> 4;
   u32x4 qb[4];
 #pragma unroll
@@ -396,24 +398,24 @@ __device__ __forceinline__ void attn_scores(const uint8_t* s_kv, const uint16_t*
     const u32x4 t = *reinterpret_cast<const u32x4*>(s_q + (r16 & 1) * HD + 32 * s4 + 8 * kg);
     qb[s4] = r16 < 2 ? t : u32x4{0u, 0u, 0u, 0u};
   }
-  // blocks v and v + 8 together (rows < 256 always lie in the LDS copy; rows at or past nc
-  // are masked): both blocks' K operands are read before the two MFMA chains run
+  // the blocks' K operands are all read before the MFMA chains run
   float mx = -INFINITY;
-  u32x4 ka[2][4];
+  u32x4 ka[NB][4];
 #pragma unroll
-  for (int bi = 0; bi < 2; bi++)
+  for (int bi = 0; bi < NB; bi++)
 #pragma unroll
     for (int s4 = 0; s4 < 4; s4++)
       ka[bi][s4] = *reinterpret_cast<const u32x4*>(s_kv + kv_off(16 * (v + 8 * bi) + r16, 4 * s4 + kg));
-  f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  f32x4 acc[NB];
 #pragma unroll
-  for (int s4 = 0; s4 < 4; s4++) {
-    acc[0] = mfma_16x16x32(ka[0][s4], qb[s4], acc[0]);
-    acc[1] = mfma_16x16x32(ka[1][s4], qb[s4], acc[1]);
-  }
+  for (int bi = 0; bi < NB; bi++) acc[bi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s4 = 0; s4 < 4; s4++)
+#pragma unroll
+    for (int bi = 0; bi < NB; bi++) acc[bi] = mfma_16x16x32(ka[bi][s4], qb[s4], acc[bi]);
   // lane (column r16 = head, rows 4kg + e): one 16-byte write of its four scores per block
 #pragma unroll
-  for (int bi = 0; bi < 2; bi++) {
+  for (int bi = 0; bi < NB; bi++) {
     const int r = 16 * (v + 8 * bi) + 4 * kg;
     f32x4 val;
 #pragma unroll
@@ -423,6 +425,15 @@ __device__ __forceinline__ void attn_scores(const uint8_t* s_kv, const uint16_t*
     }
     if (r16 < 2) *reinterpret_cast<f32x4*>(&s_sc[r16][r]) = val;
   }
+  return mx;
+}
+// Scores of wave v's blocks (see attn_score_blocks); leaves the wave's per-head maxima in s_mx[v].
+__device__ __forceinline__ void attn_scores(const uint8_t* s_kv, const uint16_t* s_q, float (*s_sc)[KV_CAP],
+                                            float (*s_mx)[2], int nc, float scale, int v, int lane) {
+  const int nb16 = (nc + 15) >> 4;  // 16-row blocks that hold a row below nc
+  float mx = v + 8 < nb16 ? attn_score_blocks<2>(s_kv, s_q, s_sc, nc, scale, v, lane)
+             : v < nb16   ? attn_score_blocks<1>(s_kv, s_q, s_sc, nc, scale, v, lane)
+                          : -INFINITY;
   // per-head maximum over the lanes of column 0 (head 0) and column 1 (head 1): lane groups
   // kg meet through permlane swaps; lanes 0 and 1 hold the two heads' maxima
   {
@@ -465,16 +476,23 @@ __device__ __forceinline__ void attn_softmax(const float (*s_sc)[KV_CAP], uint16
 // The MFMA operand (8 rows of one dim per lane) comes from two LDS transpose reads:
 // within each 16-lane group, lane j addresses row base + j / 4, dims 4 (j % 4) .. +3 of
 // the wave's 16, and lane i receives that column's 4 rows (ds_read_b64_tr_b16).
-// Writes acc / l (fin) or the raw acc (a split-K partial) to s_ao and returns the
-// per-head sums l.
+// Writes acc / l (fin) or the raw acc (a split-K partial) to s_ao, or with out16 the
+// bf16-rounded acc / l to out16[h * 128 + d] (the o_proj input), and returns the per-head
+// sums l (the waves' sums s_l[k][h], k = 0..7, added in order).
 __device__ __forceinline__ void attn_pv(const uint8_t* s_kv, const uint16_t* s_p, const float (*s_l)[2],
-                                        float (*s_ao)[HD], int nc, int v, int lane, bool fin, float& L0, float& L1) {
+                                        float (*s_ao)[HD], int nc, int v, int lane, bool fin, float& L0, float& L1,
+                                        uint16_t* out16 = nullptr) {
   typedef short v4s __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) v4s lds_v4s;
   const int r16 = lane & 15, kg = lane >> 4;
   const int dim = 16 * v + r16;
   const int dq = 16 * v + 4 * (r16 & 3);                // this lane's 4 dims in the transpose reads
   const uint32_t vb0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(s_kv + KV_CAP * 256);
+  // the softmax sums as four 16-byte reads (s_l[2i], s_l[2i + 1] in each), ahead of the products
+  const f32x4* sl = reinterpret_cast<const f32x4*>(&s_l[0][0]);
+  const f32x4 l01 = sl[0], l23 = sl[1], l45 = sl[2], l67 = sl[3];
+  L0 = 0.f + l01[0] + l01[2] + l23[0] + l23[2] + l45[0] + l45[2] + l67[0] + l67[2];
+  L1 = 0.f + l01[1] + l01[3] + l23[1] + l23[3] + l45[1] + l45[3] + l67[1] + l67[3];
   // 32-row blocks in pairs with two accumulators (a block past nc has p = 0: rows < 256
   // always lie in the LDS copy and hold finite values)
   const int nb = (nc + 31) >> 5;
@@ -502,16 +520,14 @@ __device__ __forceinline__ void attn_pv(const uint8_t* s_kv, const uint16_t* s_p
     acc2[1] = mfma_16x16x32(pa[3], vb[3], acc2[1]);
   }
   const f32x4 acc = acc2[0] + acc2[1];
-  L0 = 0.f;
-  L1 = 0.f;
-#pragma unroll
-  for (int k = 0; k < 8; k++) {
-    L0 += s_l[k][0];
-    L1 += s_l[k][1];
-  }
   if (kg == 0) {
-    s_ao[0][dim] = fin ? acc[0] * (1.0f / L0) : acc[0];
-    s_ao[1][dim] = fin ? acc[1] * (1.0f / L1) : acc[1];
+    if (out16) {
+      out16[dim] = (uint16_t)f2bf(acc[0] * (1.0f / L0));
+      out16[HD + dim] = (uint16_t)f2bf(acc[1] * (1.0f / L1));
+    } else {
+      s_ao[0][dim] = fin ? acc[0] * (1.0f / L0) : acc[0];
+      s_ao[1][dim] = fin ? acc[1] * (1.0f / L1) : acc[1];
+    }
   }
 }
 
@@ -836,7 +852,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ __align__(16) float s_sc[2][KV_CAP];      // attention scores
   __shared__ float s_ao[2][HD];                        // attention output (or unnormalised partial)
   __shared__ float s_ao1[2][HD];                       // a later LDS pass's unnormalised partial
-  __shared__ float s_mx[8][2], s_l[8][2];              // per-wave score maxima and softmax sums
+  __shared__ float s_mx[8][2];                          // per-wave score maxima
+  __shared__ __align__(16) float s_l[8][2];             // per-wave softmax sums
   __shared__ float s_hrow[ROWS];                       // the residual rows this workgroup reduces
   __shared__ float s_res[ROWS];                        // stream-wave dot products for the store wave
   __shared__ uint32_t s_cnt;                           // stream-wave results published so far
@@ -850,6 +867,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ uint32_t s_flag;
   __shared__ uint32_t s_epoch;                         // this launch's epoch
   float* s_lg = reinterpret_cast<float*>(s_kv);  // this workgroup's logits (K/V rows are dead by then)
+  // The unsplit instance: every group-A workgroup attends over the whole context in one pass,
+  // and P.V writes the bf16 attention output straight into the o_proj input (s_x1), so the
+  // o_proj dot products follow the attention's last barrier (B4) with no hand-out.
+  uint16_t* const pv16 = SPLIT ? nullptr : reinterpret_cast<uint16_t*>(s_x1);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1055,7 +1076,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
                   kv_dma<1>(kv_nt, P, layer, g, c0 + KV_CAP * (ps + 1), pass_rows(ps + 1), p, lds_kv, s, lane);
               }
               BAR();  // B3: the pass's V rows and the new v row are in LDS
-              attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+              attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1, pv16);
               BAR();  // B4: the pass's V rows consumed
               MQ_STAMP(layer * 40 + 3);
             }
@@ -1084,14 +1105,14 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
               float M0, M1, L0, L1;
               attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
               BAR();  // B3
-              attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+              attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1, pv16);
               BAR();  // B4: K/V rows consumed
               MQ_STAMP(layer * 40 + 3);
             }
           }
         }
         // ---------------- o_proj partials: rows 64m + 16s + 2i + org over the group's 256 columns
-        BAR();  // C1: attention output of the group in s_x1
+        if constexpr (SPLIT) BAR();  // C1: attention output of the group in s_x1 (unsplit: at B4)
         MQ_STAMP(layer * 40 + 4);
         {
           const u32x4 xa = x1v[oc];
@@ -1355,14 +1376,15 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             MQ_STAMP(layer * 40 + 22);
             BAR();  // B3
             MQ_STAMP(layer * 40 + 27);
-            attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+            attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1, pv16);
             MQ_STAMP(layer * 40 + 23);
             BAR();  // B4
           }
           MQ_STAMP(layer * 40 + 17);
         }
         // ---------------- o_proj input: the group's 256 attention outputs as bf16 pairs in s_x1
-        if (nsplit == 1) {
+        // (the unsplit instance's P.V has written them)
+        if (SPLIT && nsplit == 1) {
           // poll wave 0: the attention workgroup has them in LDS, the others gather them
           if (c == 0) {
             if (att) {
@@ -1376,7 +1398,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
               reinterpret_cast<u32x2*>(s_x1)[lane] = u32x2{pair_lo(v.x, v.y), pair_lo(v.z, v.w)};
             }
           }
-        } else {
+        } else if (SPLIT) {
           // every A workgroup merges the XCD's chunk partials itself, straight into its o_proj
           // input: thread pt takes dims d0, d0 + 1 of head hh (a poll wave per head), CG chunks
           // per round; lane q loads chunk q's (m, l), which the wave then reads by readlane
@@ -1455,7 +1477,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           s_x1[pt] = pack_bf2(rbf(O0 * rl), rbf(O1 * rl));
         }
         MQ_STAMP(layer * 40 + 19);
-        BAR();  // C1
+        if constexpr (SPLIT) BAR();  // C1
         MQ_STAMP(layer * 40 + 20);
       }
     } else {
@@ -1555,11 +1577,11 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
             float M0, M1, L0, L1;
             attn_softmax(s_sc, s_p, s_mx, s_l, ncp, wave, lane, M0, M1);
             BAR();  // B3
-            attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+            attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1, pv16);
             BAR();  // B4
           }
         }
-        BAR();  // C1
+        if constexpr (SPLIT) BAR();  // C1
         MQ_STAMP(layer * 40 + 29);
         if (!b_h1) {
           // h1 = bf16(h + bf16(o)) (modeling_qwen3.py:297-298)
@@ -1653,7 +1675,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
                 st1_plain(reinterpret_cast<uint32_t*>(P.v_cache + slot) + lane, v2);
               }
             }
-            attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1);
+            attn_pv(s_kv, s_p, s_l, ps ? s_ao1 : s_ao, ncp, wave, lane, nsplit == 1, L0, L1, pv16);
             BAR();  // B4
             if (ps == 0) {
               Mr0 = M0;
@@ -1709,7 +1731,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         }
         MQ_STAMP(layer * 40 + 35);
         // o_proj partials of rows 64m .. 64m+63 over this XCD's two heads
-        BAR();  // C1
+        if constexpr (SPLIT) BAR();  // C1
         target += NSW;
         wait_count(&s_cnt, target);  // (the stream waves store the partials themselves)
         if (m == 0 && lane == 0) st1_plain(ws + lb + LX_CUE_A, tag);
