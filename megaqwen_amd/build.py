@@ -26,6 +26,10 @@ FLAGS = [
     "-ffp-contract=fast",
     # packed-fp32 (v_pk_*_f32) forms are disabled on this fleet
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: attn_prefill_fa3 parks its block of scores in the AGPRs
+    # and needs every MFMA to accumulate in VGPRs; no other kernel's code changes with it
+    # (checked instruction for instruction)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I" + os.path.join(ROOT, "include"),
     "-Wno-unused-command-line-argument",
 ]

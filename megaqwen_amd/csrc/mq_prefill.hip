@@ -5,7 +5,7 @@
 // slots 0..S-1 of every layer are written, and the greedy next token is taken
 // from the last row. After embed_rows and the first layer's rmsnorm_rows, per layer:
 //   gemm_nt (q, k, v in one launch; its epilogue applies QK-norm and RoPE and appends K/V)
-//   -> attn_prefill or, past 1024 tokens, attn_prefill_fa, past 5120 attn_prefill_fa2 (causal, MFMA)
+//   -> attn_prefill or, past 1024 tokens, attn_prefill_fa3, past 5120 attn_prefill_fa2 (causal, MFMA)
 //   -> gemm_nt (o_proj, k split four ways)
 //   -> resid_norm_rows (partials + residual, post-attention RMSNorm)
 //   -> gemm_nt (gate and up, SiLU(gate) * up epilogue) -> gemm_nt (down_proj, k split)
@@ -93,12 +93,25 @@ struct QknArgs {
   uint16_t *q_out, *kc, *vc;
   int max_seq;
 };
+// Tile order across XCDs. The hardware deals workgroup L (linear id within the grid) to
+// XCD L % 8, and each XCD has its own L2, so the tiles that share an operand should run on
+// one XCD. With `xg` > 0 the grid's tiles (per k split) are dealt as 8 rectangles, 8 / xg
+// row bands by xg column bands, one per XCD class L % 8; inside its rectangle an XCD takes
+// panels of `xp` row tiles, column by column inside a panel (row tile fastest), so the
+// workgroups that run together (one panel) share xp A row tiles and a run of W tiles, and
+// each A row tile comes from HBM once per XCD instead of once per XCD for every column
+// band. xg = 0: blockIdx order (column tile = blockIdx.x). Either order computes every
+// tile the same way.
+struct XcdMap {
+  int xg, xp;
+};
 struct GemmArgs {
   const uint16_t* a;  // [m, lda] bf16
   int lda, m, k, nseg;
   GemmSeg seg[3];
   PartSet part;  // EPI_PART: set z takes the partial sums of k split z (blockIdx.z)
   QknArgs qkn;   // EPI_QKN
+  XcdMap xm;
 };
 
 // LDS slot (in 16-byte chunks) of chunk kc (0..7) of tile row r.
@@ -119,8 +132,17 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
                 "a DMA instruction covers 64 slots of one operand of one k-step");
   __shared__ u32x4 sbuf[NST][KS][SCH];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv / WN, wn = wv % WN;
-  int nt = blockIdx.x;
-  const int mt = blockIdx.y, z = blockIdx.z;  // column tile, row tile, k split
+  int nt = blockIdx.x, mt = blockIdx.y;  // column tile, row tile
+  const int z = blockIdx.z;               // k split
+  if (G.xm.xg > 0) {
+    // (the host sets xg only when 8 divides the tile count, xg the column tiles, 8 / xg the
+    // row tiles and xp the row tiles of a band)
+    const int nx = gridDim.x, L = blockIdx.x + nx * blockIdx.y, c = L & 7, s = L >> 3;
+    const int cw = nx / G.xm.xg, rh = (int)gridDim.y / (8 / G.xm.xg), pn = G.xm.xp * cw;
+    const int r = s / pn * G.xm.xp + s % pn % G.xm.xp, cc = s % pn / G.xm.xp;
+    mt = c / G.xm.xg * rh + r;
+    nt = c % G.xm.xg * cw + cc;
+  }
   int si = 0;
   while (si + 1 < G.nseg && nt >= G.seg[si].ntiles) nt -= G.seg[si++].ntiles;
   const GemmSeg S = G.seg[si];
@@ -738,24 +760,20 @@ __global__ void __launch_bounds__(64 * AW) attn_prefill(const uint16_t* q, const
     }
 }
 
-// ------------------------------------------------------------------ causal attention, flash form
-// Workgroup (KV group g, query block): query rows r0 .. r0 + 16 RT - 1 of both query heads of
-// the group (2g, 2g + 1), one wave per (head, 16-row tile), 2 RT waves. Every K/V chunk
-// copied into LDS therefore serves 32 RT query rows. Keys run in blocks of 512 (torch's CPU
-// flash blocks) with a running maximum, as attn_prefill.
+// ------------------------------------------------------------------ causal attention, flash forms
+// Long prompts (attn_prefill_fa2, attn_prefill_fa3). A workgroup takes a block of query rows of
+// both query heads of KV group g (2g, 2g + 1); a wave holds 16 query rows of both heads. Keys
+// run in blocks of 512 (torch's CPU flash blocks) with a running maximum, as attn_prefill.
 //
 // Scores are computed transposed, S^T = K Q^T (K rows from LDS as the A operand, the wave's
-// Q rows as the B operand, held in registers): lane (r16, kg) holds the scores of query row
-// r16 against keys 16 t + 4 kg + e of tile t. So a whole block's scores stay in registers
-// (32 tiles), the softmax of a query row is the lane's own plus a reduction over its four
-// lane groups, and the bf16 probabilities are already the B operand of O^T = V^T P^T: keys
-// 4 kg + i of tiles 2j, 2j + 1 (i < 4) form k-slots 8 kg + i of key step j, and V^T is read
-// in the same key order by LDS transpose reads. No score or probability goes through LDS.
-//
-// K and V reach LDS in 64-key chunks (16 KB, 1 KB DMA instructions) through a ring of FNB
-// buffers, two chunks ahead: for each 512-key block its K chunks, then its V chunks.
-constexpr int FK = 64, FNB = 4, FKB = 512;
-constexpr int FLASH_MIN_S = 1024;  // prompts longer than this take the flash form
+// Q rows as the B operand, in registers): lane (r16, kg) holds the scores of query row r16
+// against keys 16 t + 4 kg + e of key tile t. So the softmax of a query row is the lane's own
+// plus a reduction over its four lane groups, and the bf16 probabilities are already the B
+// operand of O^T = V^T P^T: keys 4 kg + i of tiles 2j, 2j + 1 (i < 4) form k-slots 8 kg + i
+// of key step j, and V^T is read in the same key order by LDS transpose reads. No score or
+// probability goes through LDS. K and V rows move into LDS in 64-key chunks (16 KB, 1 KB DMA
+// instructions).
+constexpr int FLASH_MIN_S = 1024;  // prompts longer than this take a flash form
 
 __device__ __forceinline__ float lane_group_max(float v) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -771,174 +789,6 @@ __device__ __forceinline__ float lane_group_sum(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int RT>
-__global__ void __launch_bounds__(128 * RT) attn_prefill_fa(const uint16_t* q, const uint16_t* kc,
-                                                            const uint16_t* vc, uint16_t* out, int S, int max_seq,
-                                                            float scale) {
-  constexpr int NW = 2 * RT, QB = 16 * RT, PER = 16 / NW;  // waves, query rows, DMA instructions per chunk and wave
-  typedef short v4s __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(3))) v4s lds_v4s;
-  __shared__ __align__(16) uint8_t s_kv[FNB][FK * 256];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int hh = wv / RT, rt = wv - RT * hh;
-  // XCD-aware order: workgroup id runs on XCD id % 8, made the KV group; the longest query
-  // blocks (the most keys) are dispatched first
-  const int id = blockIdx.x, g = id & 7, nqb = gridDim.x >> 3;
-  const int r0 = (nqb - 1 - (id >> 3)) * QB, h = 2 * g + hh;
-  const int r16 = lane & 15, kg = lane >> 4;
-  const int row = r0 + 16 * rt + r16;       // this lane's query row
-  const int wrow1 = r0 + 16 * rt + 15;  // the wave's last query row
-  const int nkey = min(S, r0 + QB);
-  const int nblk = (nkey + FKB - 1) / FKB;
-  const int nch_last = (nkey - FKB * (nblk - 1) + FK - 1) / FK;
-  const int total = 2 * (8 * (nblk - 1) + nch_last);  // chunks: K then V of every block
-  const uint16_t* K = kc + (size_t)g * max_seq * HD;
-  const uint16_t* V = vc + (size_t)g * max_seq * HD;
-  const uint32_t kv0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_kv[0][0];
-
-  // chunk n of the sequence into ring buffer n % FNB: instruction i of wave wv moves rows
-  // 4 q .. 4 q + 3 (q = wv + NW i; lane -> row 4 q + lane / 16, slot lane % 16); rows past
-  // the block's last key repeat it
-  auto issue = [&](int n) {
-    if (n >= total) return;
-    int b = n >> 4, rem = n & 15, nchb = 8;
-    if (b >= nblk - 1) {
-      b = nblk - 1;
-      rem = n - 16 * b;
-      nchb = nch_last;
-    }
-    const bool isv = rem >= nchb;
-    const int c = isv ? rem - nchb : rem;
-    const int kb0 = FKB * b, klast = min(nkey, kb0 + FKB) - 1;
-    const uint16_t* src = isv ? V : K;
-    const uint32_t lds = kv0 + (uint32_t)(n % FNB) * (FK * 256);
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int qq = wv + NW * i, r = 4 * qq + (lane >> 4), chunk = (lane & 15) ^ (r & 15);
-      dma16(src + (size_t)min(kb0 + FK * c + r, klast) * HD + 8 * chunk, __builtin_amdgcn_readfirstlane(lds + 1024u * qq));
-    }
-  };
-  // chunk n has landed for every wave (chunks up to n + 1 are in flight), and every wave is
-  // done with chunk n - 1, whose successor in the ring the caller may then refill
-  auto arrive = [&](int n) {
-    if (n + 1 < total)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  };
-
-  // Q^T (B operand): lane (row r16, kg) holds dims 32 ks + 8 kg .. +7 of its row
-  u32x4 qf[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ks++) qf[ks] = ldw(q + (size_t)min(row, S - 1) * QS + HD * h + 32 * ks + 8 * kg);
-  f32x4 o[8];
-#pragma unroll
-  for (int dt = 0; dt < 8; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-
-  issue(0);
-  issue(1);
-  int n = 0;
-  for (int b = 0; b < nblk; b++) {
-    const int kb0 = FKB * b, kb1 = min(nkey, kb0 + FKB), nchb = (kb1 - kb0 + FK - 1) / FK;
-    f32x4 sc[32];
-    // ---- scores of the block: chunk c holds tiles 4c .. 4c + 3
-#pragma unroll
-    for (int c = 0; c < 8; c++) {
-      if (c < nchb) {
-        arrive(n);
-        issue(n + 2);
-        const uint8_t* kb = s_kv[n % FNB];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const int t = 4 * c + j, key0 = kb0 + 16 * t;
-          if (key0 <= wrow1) {
-            u32x4 kf[4];
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-              kf[ks] = *reinterpret_cast<const u32x4*>(kb + akv_off(16 * j + r16, 4 * ks + kg));
-            f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) a = mfma_16x16x32(kf[ks], qf[ks], a);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-              const int key = key0 + 4 * kg + e;
-              sc[t][e] = (key < kb1 && key <= row) ? a[e] * scale : -INFINITY;
-            }
-          } else {
-            sc[t] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-          }
-        }
-        n++;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; j++) sc[4 * c + j] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-      }
-    }
-    // ---- softmax with the running maximum: query row = lane column r16
-    float mx = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < 32; t++) mx = fmaxf(fmaxf(mx, fmaxf(sc[t][0], sc[t][1])), fmaxf(sc[t][2], sc[t][3]));
-    mx = lane_group_max(mx);
-    const float mn = fmaxf(m_run, mx), base = mn == -INFINITY ? 0.f : mn;
-    const float al = m_run == -INFINITY ? 0.f : expf(m_run - base);
-    u32x2 pb[32];
-    float sum = 0.f;
-#pragma unroll
-    for (int t = 0; t < 32; t++) {
-      float e4[4];
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        e4[e] = exp_fast(sc[t][e] - base);  // exp(-inf) = 0 past the keys
-        sum += e4[e];
-      }
-      pb[t] = u32x2{pack_bf2(e4[0], e4[1]), pack_bf2(e4[2], e4[3])};
-    }
-    sum = lane_group_sum(sum);
-    l_run = sum + al * l_run;
-    m_run = mn;
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++) o[dt] *= al;
-    // ---- O^T += V^T P^T: chunk c holds key steps 2c, 2c + 1 (tiles 4c .. 4c + 3)
-#pragma unroll
-    for (int c = 0; c < 8; c++) {
-      if (c < nchb) {
-        arrive(n);
-        issue(n + 2);
-        const uint32_t vb = kv0 + (uint32_t)(n % FNB) * (FK * 256);
-#pragma unroll
-        for (int j2 = 0; j2 < 2; j2++) {
-          const int t0 = 4 * c + 2 * j2;
-          if (kb0 + 16 * t0 <= wrow1) {
-            const u32x4 pf = u32x4{pb[t0].x, pb[t0].y, pb[t0 + 1].x, pb[t0 + 1].y};
-            const int ra = 32 * j2 + 4 * kg + (r16 >> 2);
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++) {
-              const int dq = 16 * dt + 4 * (r16 & 3);
-              const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                  (lds_v4s*)(uintptr_t)(vb + akv_off(ra, dq >> 3) + 2 * (dq & 7)));
-              const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                  (lds_v4s*)(uintptr_t)(vb + akv_off(ra + 16, dq >> 3) + 2 * (dq & 7)));
-              const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-              o[dt] = mfma_16x16x32(u32x4{l2.x, l2.y, h2.x, h2.y}, pf, o[dt]);
-            }
-          }
-        }
-        n++;
-      }
-    }
-  }
-  if (row < S) {
-    const float inv = 1.0f / l_run;
-    uint16_t* op = out + (size_t)row * QS + HD * h + 4 * kg;
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++)
-      *reinterpret_cast<u32x2*>(op + 16 * dt) =
-          u32x2{pack_bf2(o[dt][0] * inv, o[dt][1] * inv), pack_bf2(o[dt][2] * inv, o[dt][3] * inv)};
-  }
-}
-
 // ------------------------------------------------------------------ causal attention, two passes
 // Workgroup (KV group g, query block): query rows r0 .. r0 + 127 of both query heads of the
 // group, eight waves of 16 rows each, every wave holding both heads' rows, so that each K
@@ -946,17 +796,18 @@ __global__ void __launch_bounds__(128 * RT) attn_prefill_fa(const uint16_t* q, c
 // blocks) with a running maximum; a block's softmax needs its row maxima before any
 // exponential, so each block is swept twice over its 64-key chunks: pass 1 computes the
 // scores and keeps only the row maxima, pass 2 recomputes them, takes the bf16
-// probabilities (held in registers as the B operand of O^T = V^T P^T, as in
-// attn_prefill_fa) and runs that chunk's P.V at once. The sums, the P.V chains and the
-// rescaling happen in the same order as in attn_prefill_fa, so both give the same bits.
+// probabilities (held in registers as the B operand of O^T = V^T P^T) and runs that
+// chunk's P.V at once. The sums, the P.V chains and the rescaling happen in the same order
+// as in attn_prefill_fa3, so both give the same bits.
 //
 // LDS: the block's 512 K rows (128 KB, resident for both passes) and a two-chunk V ring
 // (32 KB). During pass 2 the next block's K chunk c - 1 is copied into the slot that
 // chunk c - 1 has just left, and V runs one chunk ahead, so pass 1 of the next block finds
 // its K rows in place.
 constexpr int F2W = 8, F2Q = 16 * F2W, F2KB = 512, F2K = 64, F2NC = F2KB / F2K;
-// prompts longer than this take the two-pass form (at most 8 S / 128 workgroups, so shorter
-// prompts run faster on attn_prefill_fa's 8 S / 64; the two give the same bits)
+// prompts longer than this take the two-pass form; shorter ones run faster on
+// attn_prefill_fa3 (8 S / 64 workgroups against 8 S / 128; same-box timings: 5121 tokens
+// 258 against 258 us, 5600 304 against 285, 8192 545 against 452); the two give the same bits
 constexpr int FLASH2_MIN_S = 5120;
 // V rows live in LDS with their own chunk swizzle, chunk c of row r in slot c ^ vsw_pf(r):
 // a P.V transpose read takes, per half wave, rows 4 kg + i (kg < 2, i < 4, plus a multiple
@@ -1200,6 +1051,293 @@ __global__ void __launch_bounds__(64 * F2W) attn_prefill_fa2(const uint16_t* q, 
   }
 }
 
+// ------------------------------------------------------------------ causal attention, scores kept
+// Workgroup (KV group g, query block): query rows r0 .. r0 + 63 of both query heads of the
+// group, four waves (one per SIMD) of 16 rows each, every wave holding both heads' rows. Keys
+// run in blocks of 512 with a running maximum, as in attn_prefill_fa2, but each score is
+// computed once: a wave keeps its whole block of scores in registers (2 heads x 512 keys x 16
+// rows: 256 registers a lane, which one wave per SIMD can hold), takes the row maxima, then
+// the probabilities and P.V chunk by chunk. The operations and their order are those of
+// attn_prefill_fa2 (scores, maxima, exponentials, in-lane sums, P.V chains, rescaling), so the
+// two give the same bits; this one does a third less MFMA work and reads K from LDS once per
+// block instead of twice.
+//
+// LDS: the workgroup's Q rows (32 KB, both heads, read back at the start of every block, so
+// that the Q fragments hold no registers while the probabilities and P.V run), and a ring of
+// F3R chunk buffers (16 KB: 64 K or V rows) through which each block streams its K chunks and
+// then its V chunks ("items"), F3R - 1 items in flight. Before item n a wave
+// waits for its own DMAs of item n; the barrier that follows tells that every wave's have
+// landed and that every wave is done with item n - 1, whose buffer then takes item n + F3R - 1.
+// Past the last item the ring takes dummy copies (K row 0), so every wave issues the same
+// number of DMAs before each wait and the vmcnt count stays exact.
+constexpr int F3W = 4, F3Q = 16 * F3W, F3R = 8, F3I = 4;  // waves, query rows, ring, DMAs per item and wave
+// A block's scores are parked in accumulation registers (AGPRs) once the maxima have read
+// them, and brought back to VGPRs chunk by chunk for the exponentials (an empty asm with an
+// AGPR / VGPR operand: the compiler moves the value there), so that the 256 registers of
+// scores sit in the AGPR file and the VGPRs keep the operands, accumulators and addresses.
+__device__ __forceinline__ f32x4 park_agpr(f32x4 x) {
+  f32x4 r;
+  asm("; park %0" : "=a"(r) : "0"(x));
+  return r;
+}
+__device__ __forceinline__ f32x4 unpark_agpr(f32x4 x) {
+  f32x4 r;
+  asm("; unpark %0" : "=v"(r) : "0"(x));
+  return r;
+}
+
+// Item n of attn_prefill_fa3's ring (see there) into its buffer. A function of scalars: as a
+// lambda over the kernel's locals, the compiler kept the selected pointer and chunk offset in
+// scratch memory and reloaded them behind the DMAs in flight (a full vmcnt wait per item).
+__device__ __forceinline__ void fa3_issue(const uint16_t* K, const uint16_t* V, int dchk_k, int dchk_v, int drow,
+                                          uint32_t dl, int n, int nitems, int nblk, int nclast, int nkey) {
+  const uint16_t* src = K;
+  int dchk = dchk_k, base = 0, kl = 0;
+  if (n < nitems) {
+    const int b = n >> 4, r = n & 15, nc = b + 1 < nblk ? F2NC : nclast;
+    const bool isv = r >= nc;
+    src = isv ? V : K;
+    dchk = isv ? dchk_v : dchk_k;
+    base = F2KB * b + F2K * (isv ? r - nc : r);
+    kl = min(nkey, F2KB * b + F2KB) - 1;
+  }
+  const uint32_t lds = dl + (uint32_t)(n % F3R) * (F2K * 256);
+#pragma unroll
+  for (int i = 0; i < F3I; i++) dma16(src + (size_t)min(base + drow + 16 * i, kl) * HD + dchk, lds + 4096u * i);
+}
+
+__global__ void __launch_bounds__(64 * F3W) attn_prefill_fa3(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                                                              uint16_t* out, int S, int max_seq, float scale) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  __shared__ __align__(16) uint8_t s_ring[F3R][F2K * 256];
+  __shared__ __align__(16) uint8_t s_q[2][F3Q * 256];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // XCD-aware order as attn_prefill_fa2: KV group = XCD, longest query blocks first
+  const int id = blockIdx.x, g = id & 7, nqb = gridDim.x >> 3;
+  const int r0 = (nqb - 1 - (id >> 3)) * F3Q;
+  const int r16 = lane & 15, kg = lane >> 4;
+  const int row = r0 + 16 * wv + r16;                  // this lane's query row
+  const int wrow0 = r0 + 16 * wv, wrow1 = wrow0 + 15;  // the wave's query rows
+  const int nkey = min(S, r0 + F3Q);
+  const int nblk = (nkey + F2KB - 1) / F2KB;
+  const int nclast = (nkey - F2KB * (nblk - 1) + F2K - 1) / F2K;  // chunks of the last block
+  const int nitems = 2 * F2NC * (nblk - 1) + 2 * nclast;
+  const uint16_t* K = kc + (size_t)g * max_seq * HD;
+  const uint16_t* V = vc + (size_t)g * max_seq * HD;
+  const uint32_t lr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_ring[0][0];
+
+  // item n: block n / 16, then its K chunks (n % 16 < chunks of the block), then its V chunks.
+  // DMA instruction i of wave wv moves rows 16 i + 4 wv + lane / 16 of the chunk, lane -> slot
+  // lane % 16 of its row, which holds the row's source chunk slot ^ (row % 16) for K and
+  // slot ^ vsw_pf(row) for V; row % 16 is the same for the four instructions.
+  const int drow = 4 * wv + (lane >> 4);
+  const int dchk_k = 8 * ((lane & 15) ^ drow), dchk_v = 8 * ((lane & 15) ^ vsw_pf(drow));
+  const uint32_t dl = __builtin_amdgcn_readfirstlane(lr + 1024u * wv);
+  auto issue = [&](int n) { fa3_issue(K, V, dchk_k, dchk_v, drow, dl, n, nitems, nblk, nclast, nkey); };
+
+  // the Q rows into LDS: [head][row][16-byte chunk slot], chunk c of row r in slot c ^ (r % 16);
+  // instruction i of wave wv moves rows 4 (wv + 4 i) .. +3 of the [2][64] rows, lane -> slot
+  // lane % 16 of row 4 (wv + 4 i) + lane / 16
+  const uint32_t lq = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_q[0][0];
+#pragma unroll
+  for (int i = 0; i < 2 * F3Q / 16; i++) {
+    const int rr = 4 * (wv + 4 * i) + (lane >> 4), hh = rr / F3Q, qr = rr % F3Q;
+    dma16(q + (size_t)min(r0 + qr, S - 1) * QS + HD * (2 * g + hh) + 8 * ((lane & 15) ^ (qr & 15)),
+          __builtin_amdgcn_readfirstlane(lq + 1024u * (wv + 4 * i)));
+  }
+  f32x4 o[2][8];
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) o[hh][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  for (int n = 0; n < F3R - 1; n++) issue(n);
+  wait_vmem();
+  // (the barrier that starts item 0 publishes every wave's Q rows)
+
+  // LDS byte offsets of this lane's fragment reads within a chunk buffer: K (A operand) row
+  // 16 j + r16, 16-byte chunk 4 ks + kg -> 4096 j + koff[ks]; V^T (transpose reads) rows
+  // 32 j2 + 4 kg + r16 / 4 (+ 16), dims 16 dt + 4 (r16 % 4) .. +3 -> 8192 j2 + voff[dt] (+ 4096)
+  uint32_t koff[4], voff[8];
+#pragma unroll
+  for (int ks = 0; ks < 4; ks++) koff[ks] = akv_off(r16, 4 * ks + kg);
+#pragma unroll
+  for (int dt = 0; dt < 8; dt++) {
+    const int dq = 16 * dt + 4 * (r16 & 3);
+    voff[dt] = vkv_off_pf(4 * kg + (r16 >> 2), dq >> 3) + 2 * (dq & 7);
+  }
+  // raw scores (q . k, unscaled) of key tile j of the K chunk at LDS address kbase, both heads
+  auto raw_scores = [&](uint32_t kbase, int j, const u32x4 (&qf)[2][4], f32x4 (&a)[2]) {
+    u32x4 kf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+      kf[ks] = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(kbase + 4096u * j + koff[ks]);
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      a[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) a[hh] = mfma_16x16x32(kf[ks], qf[hh][ks], a[hh]);
+    }
+  };
+
+  int n = 0;  // the next item
+  for (int b = 0; b < nblk; b++) {
+    const int kb0 = F2KB * b, kb1 = min(nkey, kb0 + F2KB), nc = (kb1 - kb0 + F2K - 1) / F2K;
+    // ---- the block's scores, kept; the row maxima over the unscaled scores (scale > 0 and
+    // rounding is monotonic, so max(a * scale) = max(a) * scale, both rounded)
+    f32x4 sc[F2NC][4][2];
+    float mx[2] = {-INFINITY, -INFINITY};
+    // Q^T (B operand) of both heads: lane (row r16, kg) holds dims 32 ks + 8 kg .. +7 of its
+    // row (the first item's barrier has published the Q rows; they are never overwritten)
+    u32x4 qf[2][4];
+#pragma unroll
+    for (int c = 0; c < F2NC; c++) {
+      if (c < nc) {
+        AWAIT((F3R - 2) * F3I);
+        ABAR();
+        issue(n + F3R - 1);
+        const uint32_t kbase = lr + (uint32_t)(n % F3R) * (F2K * 256);
+        n++;
+        if (c == 0) {
+#pragma unroll
+          for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+              qf[hh][ks] = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(
+                  lq + 16384u * hh + 256u * 16 * wv + akv_off(r16, 4 * ks + kg));
+        }
+        const int ck0 = kb0 + F2K * c;  // the chunk's first key
+        if (ck0 + F2K - 1 < kb1 && ck0 + F2K - 1 <= wrow0) {
+          // no score of the chunk is masked
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            raw_scores(kbase, j, qf, sc[c][j]);
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+              mx[hh] = fmaxf(fmaxf(mx[hh], fmaxf(sc[c][j][hh][0], sc[c][j][hh][1])),
+                             fmaxf(sc[c][j][hh][2], sc[c][j][hh][3]));
+              sc[c][j][hh] = park_agpr(sc[c][j][hh]);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int key0 = ck0 + 16 * j;
+            if (key0 <= wrow1) {
+              raw_scores(kbase, j, qf, sc[c][j]);
+#pragma unroll
+              for (int hh = 0; hh < 2; hh++) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                  const int key = key0 + 4 * kg + e;
+                  mx[hh] = fmaxf(mx[hh], (key < kb1 && key <= row) ? sc[c][j][hh][e] : -INFINITY);
+                }
+                sc[c][j][hh] = park_agpr(sc[c][j][hh]);
+              }
+            }
+          }
+        }
+      }
+    }
+    float base[2], al[2], sum[2] = {0.f, 0.f};
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      const float mn = fmaxf(m_run[hh], lane_group_max(mx[hh]) * scale);
+      base[hh] = mn == -INFINITY ? 0.f : mn;
+      al[hh] = m_run[hh] == -INFINITY ? 0.f : expf(m_run[hh] - base[hh]);
+      m_run[hh] = mn;
+#pragma unroll
+      for (int dt = 0; dt < 8; dt++) o[hh][dt] *= al[hh];
+    }
+    // ---- probabilities and P.V, chunk by chunk
+#pragma unroll
+    for (int c = 0; c < F2NC; c++) {
+      if (c < nc) {
+        AWAIT((F3R - 2) * F3I);
+        ABAR();
+        issue(n + F3R - 1);
+        const uint32_t vb = lr + (uint32_t)(n % F3R) * (F2K * 256);
+        n++;
+        const int ck0 = kb0 + F2K * c;
+        u32x2 pb[2][4];
+        if (ck0 + F2K - 1 < kb1 && ck0 + F2K - 1 <= wrow0) {
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+              const f32x4 a = unpark_agpr(sc[c][j][hh]);
+              float e4[4];
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                e4[e] = exp_fast(unfused(a[e] * scale) - base[hh]);
+                sum[hh] += e4[e];
+              }
+              pb[hh][j] = u32x2{pack_bf2(e4[0], e4[1]), pack_bf2(e4[2], e4[3])};
+            }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int key0 = ck0 + 16 * j;
+            if (key0 <= wrow1) {
+#pragma unroll
+              for (int hh = 0; hh < 2; hh++) {
+                const f32x4 a = unpark_agpr(sc[c][j][hh]);
+                float e4[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                  // the score a * scale, or -inf where masked (exp(-inf) = 0)
+                  const int key = key0 + 4 * kg + e;
+                  const float sv = (key < kb1 && key <= row) ? unfused(a[e] * scale) : -INFINITY;
+                  e4[e] = exp_fast(sv - base[hh]);
+                  sum[hh] += e4[e];
+                }
+                pb[hh][j] = u32x2{pack_bf2(e4[0], e4[1]), pack_bf2(e4[2], e4[3])};
+              }
+            } else {
+              pb[0][j] = pb[1][j] = u32x2{0u, 0u};
+            }
+          }
+        }
+#pragma unroll
+        for (int j2 = 0; j2 < 2; j2++) {
+          // (the second half's V reads are not hoisted above the first half's products: one
+          // half's 32 registers of V fragments at a time keeps the kernel within its VGPRs)
+          if (j2 == 1) asm volatile("" ::: "memory");
+          if (ck0 + 32 * j2 <= wrow1) {
+            const u32x4 pf0 = u32x4{pb[0][2 * j2].x, pb[0][2 * j2].y, pb[0][2 * j2 + 1].x, pb[0][2 * j2 + 1].y};
+            const u32x4 pf1 = u32x4{pb[1][2 * j2].x, pb[1][2 * j2].y, pb[1][2 * j2 + 1].x, pb[1][2 * j2 + 1].y};
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+              const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(vb + 8192 * j2 + voff[dt]));
+              const v4s hi =
+                  __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(vb + 8192 * j2 + 4096 + voff[dt]));
+              const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+              const u32x4 vf = u32x4{l2.x, l2.y, h2.x, h2.y};
+              o[0][dt] = mfma_16x16x32(vf, pf0, o[0][dt]);
+              o[1][dt] = mfma_16x16x32(vf, pf1, o[1][dt]);
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) l_run[hh] = lane_group_sum(sum[hh]) + al[hh] * l_run[hh];
+  }
+  wait_vmem();  // the ring's last (dummy) copies: no DMA may target this LDS after the exit
+  if (row < S) {
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      const float inv = 1.0f / l_run[hh];
+      uint16_t* op = out + (size_t)row * QS + HD * (2 * g + hh) + 4 * kg;
+#pragma unroll
+      for (int dt = 0; dt < 8; dt++)
+        *reinterpret_cast<u32x2*>(op + 16 * dt) =
+            u32x2{pack_bf2(o[hh][dt][0] * inv, o[hh][dt][1] * inv), pack_bf2(o[hh][dt][2] * inv, o[hh][dt][3] * inv)};
+    }
+  }
+}
+
 #undef AWAIT
 #undef ABAR
 
@@ -1333,22 +1471,38 @@ using namespace mq::pf;
 constexpr int RES_SPLIT = 4;
 
 // one launch of gemm_nt over a [m, sum of the segments' widths] output, k split `split` ways
+// The XCD order of a grid of nx column tiles by ny row tiles (XcdMap) with xg column bands and
+// panels of at most xp row tiles (the largest that divides a band), or blockIdx order when
+// the grid does not split into 8 such rectangles.
+static XcdMap xcd_map(int nx, int ny, int xg, int xp) {
+  const int gy = xg > 0 && xg <= 8 && 8 % xg == 0 ? 8 / xg : 0;
+  if (gy == 0 || xp < 1 || nx % xg || ny % gy) return XcdMap{0, 0};
+  const int rh = ny / gy;
+  xp = xp < rh ? xp : rh;
+  while (rh % xp) xp--;
+  return XcdMap{xg, xp};
+}
 template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
-void gemm(const GemmArgs& g, int ntiles, hipStream_t stream, int split = 1) {
-  gemm_nt<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, (g.m + TM - 1) / TM, split), 64 * WM * WN, 0, stream>>>(g);
+void gemm(GemmArgs g, int ntiles, hipStream_t stream, int split = 1, int xg = 0, int xp = 1) {
+  const int ny = (g.m + TM - 1) / TM;
+  g.xm = xcd_map(ntiles, ny, xg, xp);
+  gemm_nt<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, ny, split), 64 * WM * WN, 0, stream>>>(g);
 }
 static void gemm_qkv(GemmArgs g, hipStream_t stream) {
   g.seg[0].ntiles = QS / HD;
   g.seg[1].ntiles = g.seg[2].ntiles = KVS / HD;
   const int nt = (QS + 2 * KVS) / HD;
-  if (g.m >= 2048) gemm<EPI_QKN, 256, HD, 3, 1, 4, 2>(g, nt, stream);
+  // long prompts: an XCD takes an eighth of the row tiles and every head, 4 row tiles by 8
+  // heads at a time, so each A row tile is fetched from HBM by one XCD (S = 8192: 107.5 ->
+  // 99.3 us against blockIdx order, same-box medians)
+  if (g.m >= 2048) gemm<EPI_QKN, 256, HD, 3, 1, 4, 2>(g, nt, stream, 1, 1, 4);
   else if (g.m >= 1024) gemm<EPI_QKN, 128, HD, 4, 1, 4, 2>(g, nt, stream);
   else gemm<EPI_QKN, 64, HD, 4, 1, 2, 4>(g, nt, stream);
 }
 static void gemm_gate_up(GemmArgs g, hipStream_t stream) {
   if (g.m >= 2048) {
     g.seg[0].ntiles = I / 128;
-    gemm<EPI_SILU, 256, 256, 2, 1, 4, 4>(g, I / 128, stream);
+    gemm<EPI_SILU, 256, 256, 2, 1, 4, 4>(g, I / 128, stream);  // (the XCD order measured no gain here)
   } else if (g.m >= 1024) {
     g.seg[0].ntiles = I / 128;
     gemm<EPI_SILU, 128, 256, 3, 1, 4, 4>(g, I / 128, stream);
@@ -1365,7 +1519,10 @@ static void gemm_residual_add(GemmArgs g, uint16_t* h, hipStream_t stream) {
   g.seg[0].out = h;
   g.seg[0].ldo = H;
   g.seg[0].ntiles = H / 128;
-  gemm<EPI_RESADD, 256, 128, 3, 1, 4, 2>(g, H / 128, stream);
+  // an XCD takes a quarter of the row tiles and half the column tiles, 4 row tiles at a time:
+  // each A row tile is fetched by two XCDs instead of eight (S = 8192, same-box medians:
+  // o_proj 49.3 -> 41.0 us, down_proj 67.8 -> 55.1 us)
+  gemm<EPI_RESADD, 256, 128, 3, 1, 4, 2>(g, H / 128, stream, 1, 2, 4);
 }
 static void gemm_residual(GemmArgs g, hipStream_t stream) {
   if (g.m >= 4096) {
@@ -1460,13 +1617,14 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     gemm_qkv(g, stream);
     chk();
     // long prompts: the two-pass flash form (128 rows of both heads a workgroup), then the
-    // one-pass flash form (64 rows); short ones: 32 rows of one head a workgroup, which fills
-    // more CUs (256 workgroups at S = 512)
+    // flash form with the scores kept (64 rows); short ones: 32 rows of one head a workgroup,
+    // which fills more CUs (256 workgroups at S = 512)
     if (S > FLASH2_MIN_S)
       attn_prefill_fa2<<<NKV * ((S + F2Q - 1) / F2Q), 64 * F2W, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len,
                                                                              attn_scale);
     else if (S > FLASH_MIN_S)
-      attn_prefill_fa<4><<<NKV * ((S + 63) / 64), 512, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
+      attn_prefill_fa3<<<NKV * ((S + F3Q - 1) / F3Q), 64 * F3W, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len,
+                                                                             attn_scale);
     else
       attn_prefill<<<NQ * ((S + AQ - 1) / AQ), 64 * AW, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
     chk();
