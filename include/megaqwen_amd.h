@@ -165,6 +165,28 @@ int launch_prefill_float(const int* input_token_ids, int* output_token_id, int s
                          void* block_max_vals, void* block_max_idxs, void* hidden_bf16_out, int num_layers,
                          int max_seq_len, float attn_scale, hipStream_t stream);
 
+/* Prefill through the reference's fused-prefill launcher name and arguments.
+ * Replaces `launch_prefill_megakernel` (csrc/megakernel/fused_prefill_megakernel.cu:938-1016;
+ * its Python caller, csrc/megakernel/megakernel_decode.py:911-937). The same MFMA prefill as
+ * launch_prefill_float (the same tokens, caches and logits), with the reference's fp32 scratch:
+ *   hidden / residual / normalized [seq_len, 1024], q_proj / attn_out [seq_len, 2048],
+ *   k_proj / v_proj [seq_len, 1024], mlp_intermediate [seq_len, 3072], all float32 and
+ *   16-byte aligned (the bf16 activations and the fp32 partial sums are carved from them).
+ *   final_hidden: float32 [1024], the final-norm output of the last row (HF's bf16 values
+ *                 as fp32; the reference writes the unrounded fp32 product).
+ *   hidden_bf16_out: bf16 [1024], the last row before the final norm, as the reference
+ *                 writes it (csrc/megakernel/fused_prefill_megakernel.cu:728).
+ *   block_max_vals f32 [1184], block_max_idxs i32 [1184]; other arguments and the result
+ *   as launch_prefill_float. The reference's launcher returns void and needs a cooperative
+ *   launch; this one returns a status and runs ordinary launches. */
+int launch_prefill_megakernel(const int* token_ids, int* output_token_id, int seq_len, const void* embed_weight,
+                              const PrefillLayerWeights* layer_weights, const void* final_norm_weight,
+                              const void* lm_head_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                              void* v_cache, void* hidden, void* residual, void* normalized, void* q_proj,
+                              void* k_proj, void* v_proj, void* attn_out, void* mlp_intermediate, void* final_hidden,
+                              void* hidden_bf16_out, void* block_max_vals, void* block_max_idxs, int num_layers,
+                              int max_seq_len, float attn_scale, hipStream_t stream);
+
 /* Device-resident generation (reference idea: experimental/qwen_persistent_kernel.cu:1028-1033,
  * which reads token and position from device memory so a captured graph can replay).
  * mq_decode_step_init writes {token, position, 0, 0} to `step` (stream-ordered copy of

@@ -71,6 +71,7 @@ SIGNATURES = {
     # ids, out, seq_len, embed, layers (host array), final norm, lm head, cos, sin, k, v, 17 scratch,
     # num_layers, max_seq_len, scale, stream
     "launch_prefill_float": [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_vp] * 17 + [_i, _i, _f, _vp],
+    "launch_prefill_megakernel": [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_vp] * 12 + [_i, _i, _f, _vp],
     "mq_decode_step_init": [_vp, _i, _i, _i, _vp],
     # step, out_ids, capacity, split_instance, embed, layers, final norm, lm head, cos, sin, k, v,
     # hidden_buffer, g_normalized, num_layers, max_seq_len, scale, stream

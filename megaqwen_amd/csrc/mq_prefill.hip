@@ -1344,13 +1344,16 @@ __global__ void __launch_bounds__(64 * F3W) attn_prefill_fa3(const uint16_t* q, 
 // ------------------------------------------------------------------ LM head
 constexpr int LMB = 1184;  // partial-argmax blocks (the length of the reference's block_max_* buffers)
 
-// Final norm of the last hidden row (every workgroup computes it; workgroup 0 also
-// writes it to final_hidden and to hidden_out, as the reference copies final_hidden into
-// hidden_bf16_out, csrc/megakernel/fused_prefill.cu:843-849), then the bf16 logits of
-// rows [VOCAB * b / LMB, VOCAB * (b+1) / LMB) of the tied LM head and their argmax
-// (lowest index on ties).
+// Final norm of the last hidden row (every workgroup computes it), then the bf16 logits of
+// rows [VOCAB * b / LMB, VOCAB * (b+1) / LMB) of the tied LM head and their argmax (lowest
+// index on ties). Workgroup 0 also writes the row out, as each reference launcher does:
+// - launch_prefill_float: the final-norm row (bf16) to final_hidden and to hidden_out (the
+//   reference copies final_hidden into hidden_bf16_out, csrc/megakernel/fused_prefill.cu:843-849);
+// - launch_prefill_megakernel: the final-norm row as fp32 to final_f32 and the pre-norm row
+//   to hidden_out (csrc/megakernel/fused_prefill_megakernel.cu:723-728).
 __global__ void __launch_bounds__(256) lm_partial(const uint16_t* hlast, const uint16_t* fnw, const uint16_t* lm,
-                                                  uint16_t* final_hidden, uint16_t* hidden_out, float* bmv, int* bmi) {
+                                                  uint16_t* final_hidden, float* final_f32, uint16_t* hidden_out,
+                                                  int prenorm_out, float* bmv, int* bmi) {
   __shared__ __align__(16) uint32_t s_x[H / 2];
   __shared__ float s_ss[4], s_bv[4];
   __shared__ int s_bi[4];
@@ -1369,8 +1372,10 @@ __global__ void __launch_bounds__(256) lm_partial(const uint16_t* hlast, const u
   s_x[2 * tid] = n0;
   s_x[2 * tid + 1] = n1;
   if (b == 0) {
-    reinterpret_cast<u32x2*>(final_hidden)[tid] = u32x2{n0, n1};
-    reinterpret_cast<u32x2*>(hidden_out)[tid] = u32x2{n0, n1};
+    if (final_hidden) reinterpret_cast<u32x2*>(final_hidden)[tid] = u32x2{n0, n1};
+    if (final_f32)
+      reinterpret_cast<f32x4*>(final_f32)[tid] = f32x4{bflo(n0), bfhi(n0), bflo(n1), bfhi(n1)};
+    reinterpret_cast<u32x2*>(hidden_out)[tid] = prenorm_out ? xw : u32x2{n0, n1};
   }
   __syncthreads();
   const u32x4 xa = reinterpret_cast<const u32x4*>(s_x)[lane], xb = reinterpret_cast<const u32x4*>(s_x)[64 + lane];
@@ -1537,31 +1542,44 @@ static void gemm_residual(GemmArgs g, hipStream_t stream) {
   }
 }
 
-extern "C" int launch_prefill_float(const int* input_token_ids, int* output_token_id, int seq_len,
-                                    const void* embed_weight, const PrefillLayerWeights* layer_weights,
-                                    const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
-                                    const void* sin_table, void* k_cache, void* v_cache, void* hidden_bf16,
-                                    void* residual, void* normalized, void* q_proj, void* k_proj, void* v_proj,
-                                    void* attn_out, void* o_proj_out, void* mlp_norm, void* gate_out, void* up_out,
-                                    void* mlp_intermediate, void* down_out, void* final_hidden, void* block_max_vals,
-                                    void* block_max_idxs, void* hidden_bf16_out, int num_layers, int max_seq_len,
-                                    float attn_scale, hipStream_t stream) {
-  (void)residual; (void)o_proj_out; (void)down_out;
-  if (!input_token_ids || !output_token_id || !embed_weight || !layer_weights || !final_norm_weight ||
-      !lm_head_weight || !cos_table || !sin_table || !k_cache || !v_cache || !hidden_bf16 || !normalized ||
-      !q_proj || !k_proj || !v_proj || !attn_out || !mlp_norm || !gate_out || !up_out || !mlp_intermediate ||
-      !final_hidden || !block_max_vals || !block_max_idxs || !hidden_bf16_out)
-    return MQ_ERR_ARG;
-  if (seq_len < 1 || max_seq_len < 1 || seq_len > max_seq_len || num_layers < 1 || num_layers > MAX_LAYERS ||
-      !(attn_scale > 0.f) || !isfinite(attn_scale))
-    return MQ_ERR_ARG;
+// The buffers of one prefill run, carved from a launcher's scratch arguments: the bf16
+// activations, the fp32 partial sums of the k-split o_proj and down_proj, and where the
+// last row's final norm and hidden state go (see lm_partial).
+struct PrefillBufs {
+  uint16_t *h, *nrm, *qp, *att, *mln, *mid;
+  PartSet parts;
+  uint16_t* final_bf16;  // final-norm row (bf16), or null
+  float* final_f32;      // final-norm row (fp32), or null
+  uint16_t* hidden_out;  // the final-norm row, or with prenorm_out the pre-norm row
+  int prenorm_out;
+  float* bmv;  // per-block LM-head maxima and their indices
+  int* bmi;
+};
+
+// Argument checks shared by the prefill launchers (before any HIP call).
+static bool prefill_args_ok(const int* ids, const int* out, int S, const void* embed, const PrefillLayerWeights* lw,
+                            const void* fnw, const void* lm, const void* cos_t, const void* sin_t, const void* kc,
+                            const void* vc, int num_layers, int max_seq, float scale) {
+  if (!ids || !out || !embed || !lw || !fnw || !lm || !cos_t || !sin_t || !kc || !vc) return false;
+  if (S < 1 || max_seq < 1 || S > max_seq || num_layers < 1 || num_layers > MAX_LAYERS || !(scale > 0.f) ||
+      !isfinite(scale))
+    return false;
   for (int l = 0; l < num_layers; l++) {
-    const PrefillLayerWeights& w = layer_weights[l];
+    const PrefillLayerWeights& w = lw[l];
     if (!w.input_layernorm_weight || !w.q_proj_weight || !w.k_proj_weight || !w.v_proj_weight ||
         !w.q_norm_weight || !w.k_norm_weight || !w.o_proj_weight || !w.post_attn_layernorm_weight ||
         !w.gate_proj_weight || !w.up_proj_weight || !w.down_proj_weight)
-      return MQ_ERR_ARG;
+      return false;
   }
+  return true;
+}
+
+// One prefill: embedding, every layer, the LM head's argmax of the last row.
+static int prefill_run(const int* input_token_ids, int* output_token_id, int seq_len, const void* embed_weight,
+                       const PrefillLayerWeights* layer_weights, const void* final_norm_weight,
+                       const void* lm_head_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                       void* v_cache, const PrefillBufs& B, int num_layers, int max_seq_len, float attn_scale,
+                       hipStream_t stream) {
   uint32_t* ws = nullptr;
   const int st = current_workspace(&ws);
   if (st != MQ_OK) return st;
@@ -1570,12 +1588,13 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
   const int S = seq_len;
   auto bf = [](const void* p) { return static_cast<const uint16_t*>(p); };
   auto bfm = [](void* p) { return static_cast<uint16_t*>(p); };
-  uint16_t* h = bfm(hidden_bf16);
-  uint16_t* nrm = bfm(normalized);
-  uint16_t* qp = bfm(q_proj);
-  uint16_t* att = bfm(attn_out);
-  uint16_t* mln = bfm(mlp_norm);
-  uint16_t* mid = bfm(mlp_intermediate);
+  uint16_t* h = B.h;
+  uint16_t* nrm = B.nrm;
+  uint16_t* qp = B.qp;
+  uint16_t* att = B.att;
+  uint16_t* mln = B.mln;
+  uint16_t* mid = B.mid;
+  const PartSet parts = B.parts;
   const size_t kv_layer = (size_t)NKV * max_seq_len * HD;
 
   hipError_t launch_err = hipSuccess;
@@ -1584,22 +1603,6 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     if (e != hipSuccess && launch_err == hipSuccess) launch_err = e;
   };
   (void)hipGetLastError();  // clear an error left by an unrelated earlier call
-  // fp32 partial sums of the k-split o_proj and down_proj, [S, 1024] a split, in scratch
-  // that is dead while they live: gate_out and up_out (unused otherwise), q_proj (read by
-  // the attention before o_proj) and k_proj | v_proj as the two column halves of the
-  // fourth set (unused: the q/k/v epilogue writes k and v straight to the caches)
-  auto f32 = [](void* p) { return static_cast<float*>(p); };
-  PartSet parts{};
-  parts.n = RES_SPLIT;
-  float* const whole[3] = {f32(gate_out), f32(up_out), f32(q_proj)};
-  for (int z = 0; z < 3; z++) {
-    parts.lo[z] = whole[z];
-    parts.hi[z] = whole[z] + PART_HALF;
-    parts.ld[z] = H;
-  }
-  parts.lo[3] = f32(k_proj);
-  parts.hi[3] = f32(v_proj);
-  parts.ld[3] = PART_HALF;
   embed_rows<<<S, 128, 0, stream>>>(input_token_ids, bf(embed_weight), h, err);
   chk();
   rmsnorm_rows<<<S, 64, 0, stream>>>(h, bf(layer_weights[0].input_layernorm_weight), nrm, S);
@@ -1665,11 +1668,105 @@ extern "C" int launch_prefill_float(const int* input_token_ids, int* output_toke
     chk();
   }
   lm_partial<<<LMB, 256, 0, stream>>>(h + (size_t)(S - 1) * H, bf(final_norm_weight), bf(lm_head_weight),
-                                      bfm(final_hidden), bfm(hidden_bf16_out), static_cast<float*>(block_max_vals),
-                                      static_cast<int*>(block_max_idxs));
+                                      B.final_bf16, B.final_f32, B.hidden_out, B.prenorm_out, B.bmv, B.bmi);
   chk();
-  argmax_final<<<1, 256, 0, stream>>>(static_cast<const float*>(block_max_vals),
-                                      static_cast<const int*>(block_max_idxs), output_token_id, err);
+  argmax_final<<<1, 256, 0, stream>>>(B.bmv, B.bmi, output_token_id, err);
   chk();
   return launch_err == hipSuccess ? MQ_OK : MQ_ERR_HIP;
+}
+
+extern "C" int launch_prefill_float(const int* input_token_ids, int* output_token_id, int seq_len,
+                                    const void* embed_weight, const PrefillLayerWeights* layer_weights,
+                                    const void* final_norm_weight, const void* lm_head_weight, const void* cos_table,
+                                    const void* sin_table, void* k_cache, void* v_cache, void* hidden_bf16,
+                                    void* residual, void* normalized, void* q_proj, void* k_proj, void* v_proj,
+                                    void* attn_out, void* o_proj_out, void* mlp_norm, void* gate_out, void* up_out,
+                                    void* mlp_intermediate, void* down_out, void* final_hidden, void* block_max_vals,
+                                    void* block_max_idxs, void* hidden_bf16_out, int num_layers, int max_seq_len,
+                                    float attn_scale, hipStream_t stream) {
+  (void)residual; (void)o_proj_out; (void)down_out;
+  if (!prefill_args_ok(input_token_ids, output_token_id, seq_len, embed_weight, layer_weights, final_norm_weight,
+                       lm_head_weight, cos_table, sin_table, k_cache, v_cache, num_layers, max_seq_len, attn_scale) ||
+      !hidden_bf16 || !normalized || !q_proj || !k_proj || !v_proj || !attn_out || !mlp_norm || !gate_out ||
+      !up_out || !mlp_intermediate || !final_hidden || !block_max_vals || !block_max_idxs || !hidden_bf16_out)
+    return MQ_ERR_ARG;
+  auto bfm = [](void* p) { return static_cast<uint16_t*>(p); };
+  PrefillBufs B{};
+  B.h = bfm(hidden_bf16);
+  B.nrm = bfm(normalized);
+  B.qp = bfm(q_proj);
+  B.att = bfm(attn_out);
+  B.mln = bfm(mlp_norm);
+  B.mid = bfm(mlp_intermediate);
+  // fp32 partial sums of the k-split o_proj and down_proj, [S, 1024] a split, in scratch
+  // that is dead while they live: gate_out and up_out (unused otherwise), q_proj (read by
+  // the attention before o_proj) and k_proj | v_proj as the two column halves of the
+  // fourth set (unused: the q/k/v epilogue writes k and v straight to the caches)
+  auto f32 = [](void* p) { return static_cast<float*>(p); };
+  B.parts.n = RES_SPLIT;
+  float* const whole[3] = {f32(gate_out), f32(up_out), f32(q_proj)};
+  for (int z = 0; z < 3; z++) {
+    B.parts.lo[z] = whole[z];
+    B.parts.hi[z] = whole[z] + PART_HALF;
+    B.parts.ld[z] = H;
+  }
+  B.parts.lo[3] = f32(k_proj);
+  B.parts.hi[3] = f32(v_proj);
+  B.parts.ld[3] = PART_HALF;
+  B.final_bf16 = bfm(final_hidden);
+  B.hidden_out = bfm(hidden_bf16_out);
+  B.bmv = static_cast<float*>(block_max_vals);
+  B.bmi = static_cast<int*>(block_max_idxs);
+  return prefill_run(input_token_ids, output_token_id, seq_len, embed_weight, layer_weights, final_norm_weight,
+                     lm_head_weight, cos_table, sin_table, k_cache, v_cache, B, num_layers, max_seq_len, attn_scale,
+                     stream);
+}
+
+// The reference's fused-prefill launcher (csrc/megakernel/fused_prefill_megakernel.cu:938-1016),
+// on the same MFMA prefill. Its scratch is fp32 ([seq_len, n] rows of 4 n bytes), twice the
+// bytes of the bf16 activations, so the activations and the fp32 partial sums are carved from
+// it: h, the post-attention norm output, the input norm output, q and the attention output in
+// the first half of hidden, residual, normalized, q_proj and attn_out; the partial sums in
+// k_proj and v_proj (whole), q_proj (once the attention has read q) and the second half of
+// mlp_intermediate (whose first half holds the MLP activations). final_hidden receives the
+// final-norm row as fp32 and hidden_bf16_out the pre-norm last row, as the reference writes.
+extern "C" int launch_prefill_megakernel(const int* token_ids, int* output_token_id, int seq_len,
+                                         const void* embed_weight, const PrefillLayerWeights* layer_weights,
+                                         const void* final_norm_weight, const void* lm_head_weight,
+                                         const void* cos_table, const void* sin_table, void* k_cache, void* v_cache,
+                                         void* hidden, void* residual, void* normalized, void* q_proj, void* k_proj,
+                                         void* v_proj, void* attn_out, void* mlp_intermediate, void* final_hidden,
+                                         void* hidden_bf16_out, void* block_max_vals, void* block_max_idxs,
+                                         int num_layers, int max_seq_len, float attn_scale, hipStream_t stream) {
+  if (!prefill_args_ok(token_ids, output_token_id, seq_len, embed_weight, layer_weights, final_norm_weight,
+                       lm_head_weight, cos_table, sin_table, k_cache, v_cache, num_layers, max_seq_len, attn_scale) ||
+      !hidden || !residual || !normalized || !q_proj || !k_proj || !v_proj || !attn_out || !mlp_intermediate ||
+      !final_hidden || !hidden_bf16_out || !block_max_vals || !block_max_idxs)
+    return MQ_ERR_ARG;
+  auto bfm = [](void* p) { return static_cast<uint16_t*>(p); };
+  auto f32 = [](void* p) { return static_cast<float*>(p); };
+  const size_t S = (size_t)seq_len;
+  PrefillBufs B{};
+  B.h = bfm(hidden);
+  B.mln = bfm(residual);
+  B.nrm = bfm(normalized);
+  B.qp = bfm(q_proj);
+  B.att = bfm(attn_out);
+  B.mid = bfm(mlp_intermediate);  // [S, 3072] bf16: the first S * 6 KB of S * 12 KB
+  B.parts.n = RES_SPLIT;
+  float* const sets[RES_SPLIT] = {f32(k_proj), f32(v_proj), f32(q_proj),
+                                  f32(mlp_intermediate) + S * (I / 2)};  // byte offset S * 6 KB
+  for (int z = 0; z < RES_SPLIT; z++) {
+    B.parts.lo[z] = sets[z];
+    B.parts.hi[z] = sets[z] + PART_HALF;
+    B.parts.ld[z] = H;
+  }
+  B.final_f32 = f32(final_hidden);
+  B.hidden_out = bfm(hidden_bf16_out);
+  B.prenorm_out = 1;
+  B.bmv = f32(block_max_vals);
+  B.bmi = static_cast<int*>(block_max_idxs);
+  return prefill_run(token_ids, output_token_id, seq_len, embed_weight, layer_weights, final_norm_weight,
+                     lm_head_weight, cos_table, sin_table, k_cache, v_cache, B, num_layers, max_seq_len, attn_scale,
+                     stream);
 }

@@ -355,13 +355,56 @@ class MegakernelPrefillDecoder(MegakernelDecoder):
 class MegakernelFusedPrefillDecoder(MegakernelPrefillDecoder):
     """The reference's fused-prefill decoder (megakernel_decode.py:788-943: a cooperative
     batched-GEMV prefill megakernel for prompts of at most 64 tokens). Same constructor,
-    methods and errors; on MI355X the prompt runs through the MFMA prefill kernels, which
-    serve short prompts as well (default max_prefill_len 64, as in the reference)."""
+    methods and errors, and the same launcher: `launch_prefill_megakernel` with the
+    reference's fp32 scratch ([max_prefill_len, n] float32, :859-868). On MI355X that
+    launcher runs the MFMA prefill kernels, which serve short prompts as well (default
+    max_prefill_len 64, as in the reference); tokens and caches equal launch_prefill_float's.
+    After prefill_step, `final_hidden_` holds the last row's final-norm output as fp32 and
+    `hidden_buffer_` the last row before the final norm (bf16), as the reference writes them."""
 
     def __init__(self, embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight, cos_table, sin_table,
                  num_layers: int, max_seq_len: int, max_prefill_len: int = 64):
         super().__init__(embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight, cos_table, sin_table,
                          num_layers, max_seq_len, max_prefill_len)
+        # the reference's fused-prefill scratch: all float32 (megakernel_decode.py:859-868)
+        P, dev = self.max_prefill_len_, embed_weight.device
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.hidden_ = torch.empty(P, HIDDEN_SIZE, **f32)
+        self.residual_ = torch.empty(P, HIDDEN_SIZE, **f32)
+        self.normalized_ = torch.empty(P, HIDDEN_SIZE, **f32)
+        self.q_proj_ = torch.empty(P, Q_SIZE, **f32)
+        self.k_proj_ = torch.empty(P, KV_SIZE, **f32)
+        self.v_proj_ = torch.empty(P, KV_SIZE, **f32)
+        self.attn_out_ = torch.empty(P, Q_SIZE, **f32)
+        self.mlp_intermediate_ = torch.empty(P, INTERMEDIATE_SIZE, **f32)
+        self.final_hidden_ = torch.empty(HIDDEN_SIZE, **f32)
+        # the bf16 buffers of launch_prefill_float are not used by this launcher
+        del self.hidden_float_, self.mlp_norm_, self.gate_out_, self.up_out_
+
+    def prefill_step_async(self, input_token_ids) -> torch.Tensor:
+        ids = torch.as_tensor(input_token_ids, dtype=torch.int32).reshape(-1)
+        n = int(ids.numel())
+        if n == 0:
+            raise RuntimeError("Empty input sequence")
+        if n > self.max_prefill_len_:
+            raise RuntimeError("Prefill sequence length exceeds maximum")
+        self.input_tokens_[:n].copy_(ids.to(self.input_tokens_.device), non_blocking=False)
+        st = _abi.lib().launch_prefill_megakernel(
+            _ptr(self.input_tokens_), _ptr(self.output_token_), n, _ptr(self.embed_weight_),
+            ctypes.addressof(self.h_layer_weights_), _ptr(self.final_norm_weight_), _ptr(self.lm_head_weight_),
+            _ptr(self.cos_table_), _ptr(self.sin_table_), _ptr(self.k_cache_), _ptr(self.v_cache_),
+            _ptr(self.hidden_), _ptr(self.residual_), _ptr(self.normalized_), _ptr(self.q_proj_), _ptr(self.k_proj_),
+            _ptr(self.v_proj_), _ptr(self.attn_out_), _ptr(self.mlp_intermediate_), _ptr(self.final_hidden_),
+            _ptr(self.hidden_buffer_), _ptr(self.block_max_vals_), _ptr(self.block_max_idxs_), self.num_layers_,
+            self.max_seq_len_, self.attn_scale_, _stream())
+        _abi.check(st, "launch_prefill_megakernel")
+        self.position_ = n
+        return self.output_token_
+
+    def final_normed_state(self) -> torch.Tensor:
+        """Final-norm output of the prompt's last row after prefill_step, as bf16 [1024] (the
+        launcher writes it as fp32 holding bf16 values)."""
+        return self.final_hidden_.to(torch.bfloat16)
 
 
 def decode_layer(hidden_in: torch.Tensor, layer_weights: list, cos_table, sin_table, k_cache, v_cache,

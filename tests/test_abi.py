@@ -27,7 +27,7 @@ def declared_functions():
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("launch_ldg_decode", "launch_ldg_decode_with_logits", "mq_decode_layer", "launch_prefill_float",
-              "mq_reset_workspace", "mq_strerror"):
+              "launch_prefill_megakernel", "mq_reset_workspace", "mq_strerror"):
         assert n in names, n
 
 
@@ -102,6 +102,25 @@ def _prefill_args(**over):
 def test_prefill_rejects_invalid_arguments(bad):
     keep, args = _prefill_args(**bad)
     assert _abi.lib().launch_prefill_float(*args) == _abi.MQ_ERR_ARG
+    del keep
+
+
+@pytest.mark.parametrize("bad", [
+    dict(ids=None), dict(out=None), dict(layers=None), dict(k=None), dict(null_scratch=True),
+    dict(null_layer_field=True), dict(seq_len=0), dict(seq_len=17), dict(num_layers=0), dict(num_layers=33),
+    dict(max_seq_len=0), dict(scale=0.0), dict(scale=float("nan")),
+])
+def test_prefill_megakernel_rejects_invalid_arguments(bad):
+    """launch_prefill_megakernel (the reference's fused-prefill launcher,
+    csrc/megakernel/fused_prefill_megakernel.cu:938-1016): every scratch argument is required
+    (the activations and partial sums are carved from them); bad sizes and pointers are refused
+    on the host before any HIP call."""
+    keep, args = _prefill_args(**{k: v for k, v in bad.items() if k != "null_scratch"})
+    scratch = [1] * 12  # hidden .. block_max_idxs
+    if bad.get("null_scratch"):
+        scratch[7] = None  # mlp_intermediate
+    margs = args[:11] + scratch + args[28:]
+    assert _abi.lib().launch_prefill_megakernel(*margs) == _abi.MQ_ERR_ARG
     del keep
 
 

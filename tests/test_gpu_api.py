@@ -172,7 +172,16 @@ def test_fused_prefill_names(gpu_weights):
     ids = list(range(1000, 1040))
     a = fused.prefill_step(ids)
     b = plain.prefill_step(ids)
+    # launch_prefill_megakernel (fp32 scratch) against launch_prefill_float: the same token
+    # and caches, bit for bit
     assert a == b and torch.equal(fused.get_k_cache()[:, :, :40], plain.get_k_cache()[:, :, :40])
+    assert torch.equal(fused.get_v_cache()[:, :, :40], plain.get_v_cache()[:, :, :40])
+    # its outputs as the reference's fused launcher writes them: final_hidden the final-norm
+    # row as fp32, hidden_bf16_out the last row before the final norm
+    assert fused.final_hidden_.dtype == torch.float32
+    assert torch.equal(fused.final_hidden_, plain.final_hidden_.float())
+    assert torch.equal(fused.final_normed_state(), plain.final_normed_state())
+    assert torch.equal(fused.hidden_buffer_, plain.hidden_float_[39])
     with pytest.raises(RuntimeError):
         fused.prefill_step(list(range(65)))
     gen = MK.MegakernelFusedPrefillGenerator(weights_dict=w, max_seq_len=256)
