@@ -1187,13 +1187,13 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       BAR();  // P0
       load_gu(0);
       load_d(0);
-      // long contexts (chunks of several LDS passes): this workgroup reads the first pass's
-      // K/V rows of chunk m two layers ahead into its (otherwise unused) K/V LDS array, so
-      // that they sit in the XCD's L2 when the chunk's attention workgroup copies them (its
-      // copy is issued a layer before their use, behind its own weight burst)
+      // split contexts of more than one chunk: this workgroup reads the first pass's K/V rows
+      // of chunk m two layers ahead into its (otherwise unused) K/V LDS array, so that they
+      // sit in the XCD's L2 when the chunk's attention workgroup copies them (its copy is
+      // issued a layer before their use, behind its own weight burst)
       auto warm_kv = [&](int l) {
-        if constexpr (PIPE) {
-          if (l < L && m < nsplit) {
+        if constexpr (SPLIT) {
+          if (l < L && m < nsplit && nsplit > 1) {
             const int wc0 = m * CH;
             kv_dma(false, P, l, g, wc0, min(min(n_ctx, wc0 + CH) - wc0, KV_CAP), p, lds_kv, s, lane);
           }
@@ -1259,11 +1259,12 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           load_d(layer + 1);
           put_norms();
           MQ_LANDED(layer * 40 + 11);
-          if constexpr (PIPE) {
+          if constexpr (SPLIT) {
             // once chunk m's attention of the next layer is done (its partial record carries
-            // that layer's tag), the XCD's L2 has room: warm the chunk's first pass of the
-            // layer after it, which its attention workgroup copies after its o_proj partials
-            if (layer + 2 < L && m < nsplit) {
+            // that layer's tag; there are records only with more than one chunk), the XCD's
+            // L2 has room: warm the chunk's first pass of the layer after it, which its
+            // attention workgroup copies after its o_proj partials
+            if (layer + 2 < L && m < nsplit && nsplit > 1) {
               const uint32_t rec = lb + LX_PART + 2 * (m * 2 * APART) + 1, want = epoch * 32u + (uint32_t)layer + 2u;
               uint32_t spins = 0;
               while (ldl1(wsb, rec) != want) {
