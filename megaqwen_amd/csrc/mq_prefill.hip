@@ -105,6 +105,26 @@ struct QknArgs {
 struct XcdMap {
   int xg, xp;
 };
+// Cache warm-up by workgroups that no tile uses. A launch that leaves CUs idle (gate/up at
+// S = 512 has 192 workgroups for 256 CUs) appends one row of workgroups (blockIdx.y ==
+// `row`) that read the weights of the launches after it, each column tile of a consumer on
+// the XCD that will read it: in blockIdx order with a multiple of 8 column tiles, a
+// consumer's column tile t runs on XCD t % 8 whatever its row tile and k split. Nothing is
+// stored: the reads leave the rows in that XCD's L2 and in the memory-side cache, and the
+// product's own tiles run on other CUs, so their loads do not queue behind these.
+constexpr int MAX_WARM = 5, NUM_CUS = 256;  // (MI355X: 8 XCDs of 32 CUs)
+// Prompts up to this length warm in gate/up (whole prefill, same box, base -> warm-up:
+// S = 64 1.642 -> 1.605 ms, 128 1.769 -> 1.693, 192 1.721 -> 1.690, 256 1.808 -> 1.762;
+// from 320 on within +-1.6% either way, 512 1.956 -> 1.987 on one box)
+constexpr int WARM_MAX_S = 256;
+struct WarmSet {
+  const uint16_t* w[MAX_WARM];  // weight matrices [n, k] bf16, in the order they are read
+  int tile_bytes[MAX_WARM];     // bytes of one consumer column tile (a multiple of 1 KB)
+  int ntiles[MAX_WARM];         // the consumer's column tiles in this matrix
+  int xcd0[MAX_WARM];           // XCD of the matrix's first tile (its first tile index mod 8)
+  int n;                        // ranges; 0: no warm-up row
+  int row;                      // blockIdx.y of the warm-up row (set by the launcher)
+};
 struct GemmArgs {
   const uint16_t* a;  // [m, lda] bf16
   int lda, m, k, nseg;
@@ -112,7 +132,29 @@ struct GemmArgs {
   PartSet part;  // EPI_PART: set z takes the partial sums of k split z (blockIdx.z)
   QknArgs qkn;   // EPI_QKN
   XcdMap xm;
+  WarmSet warm;
 };
+
+// The warm-up row's work. Its gridDim.x / 8 workgroups on XCD c (linear id L, L % 8 == c;
+// the launcher keeps gridDim.x a multiple of 8 and one k split) split every tile t with
+// (xcd0 + t) % 8 == c into equal runs of 1 KB units; a wave reads one unit per DMA (64
+// lanes x 16 bytes) into its own 1 KB of the workgroup's LDS, which nothing reads.
+template <int NW>
+__device__ void warm_tiles(const WarmSet& W, uint32_t lds, int wv, int lane) {
+  const int L = blockIdx.x + gridDim.x * blockIdx.y, c = L & 7;
+  const int nwg = gridDim.x >> 3, j = (L >> 3) - (gridDim.x >> 3) * W.row;
+  const uint32_t dst = __builtin_amdgcn_readfirstlane(lds + 1024u * (uint32_t)wv);
+#pragma unroll
+  for (int r = 0; r < MAX_WARM; r++) {
+    if (r >= W.n) break;
+    const int units = W.tile_bytes[r] >> 10, u0 = units * j / nwg, u1 = units * (j + 1) / nwg;
+    for (int t = (c - W.xcd0[r]) & 7; t < W.ntiles[r]; t += 8) {
+      const char* base = reinterpret_cast<const char*>(W.w[r]) + (size_t)t * W.tile_bytes[r] + 16 * lane;
+      for (int u = u0 + wv; u < u1; u += NW) dma16(base + ((size_t)u << 10), dst);
+    }
+  }
+  wait_vmem();  // no DMA may still target this workgroup's LDS when it exits
+}
 
 // LDS slot (in 16-byte chunks) of chunk kc (0..7) of tile row r.
 __device__ __forceinline__ int tslot(int r, int kc) { return r * 8 + (kc ^ (r & 7)); }
@@ -132,6 +174,11 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
                 "a DMA instruction covers 64 slots of one operand of one k-step");
   __shared__ u32x4 sbuf[NST][KS][SCH];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv / WN, wn = wv % WN;
+  if (G.warm.n > 0 && (int)blockIdx.y == G.warm.row) {
+    static_assert(NW * 1024 <= NST * KS * SCH * 16, "a wave's DMA unit fits the ring");
+    warm_tiles<NW>(G.warm, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sbuf[0][0][0], wv, lane);
+    return;
+  }
   int nt = blockIdx.x, mt = blockIdx.y;  // column tile, row tile
   const int z = blockIdx.z;               // k split
   if (G.xm.xg > 0) {
@@ -1491,7 +1538,11 @@ template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
 void gemm(GemmArgs g, int ntiles, hipStream_t stream, int split = 1, int xg = 0, int xp = 1) {
   const int ny = (g.m + TM - 1) / TM;
   g.xm = xcd_map(ntiles, ny, xg, xp);
-  gemm_nt<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, ny, split), 64 * WM * WN, 0, stream>>>(g);
+  // a warm-up row only where its workgroups land on CUs no tile uses, eight to an XCD
+  // class, in blockIdx order
+  if (g.warm.n > 0 && (ntiles % 8 || split != 1 || g.xm.xg > 0 || ntiles * (ny + 1) > NUM_CUS)) g.warm.n = 0;
+  g.warm.row = ny;
+  gemm_nt<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, ny + (g.warm.n > 0), split), 64 * WM * WN, 0, stream>>>(g);
 }
 static void gemm_qkv(GemmArgs g, hipStream_t stream) {
   g.seg[0].ntiles = QS / HD;
@@ -1648,6 +1699,24 @@ static int prefill_run(const int* input_token_ids, int* output_token_id, int seq
     GemmArgs gu{};
     gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
     gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, 0, I};
+    if (S <= WARM_MAX_S) {
+      // short prompts: the idle CUs of gate/up read down_proj's weights and the next layer's
+      // q/k/v and o_proj weights, each column tile on the XCD of the launch that reads it
+      // (the 64x128 q/k/v tiles: q tiles 0-15, k 16-23, v 24-31; the 128x64 k-split
+      // residual tiles: 16)
+      WarmSet& W = gu.warm;
+      auto add = [&](const void* wp, int tile_bytes, int ntiles, int xcd0) {
+        W.w[W.n] = bf(wp); W.tile_bytes[W.n] = tile_bytes; W.ntiles[W.n] = ntiles; W.xcd0[W.n] = xcd0; W.n++;
+      };
+      add(w.down_proj_weight, 64 * I * 2, H / 64, 0);
+      if (l + 1 < num_layers) {
+        const PrefillLayerWeights& wn = layer_weights[l + 1];
+        add(wn.q_proj_weight, HD * H * 2, QS / HD, 0);
+        add(wn.k_proj_weight, HD * H * 2, KVS / HD, (QS / HD) % 8);
+        add(wn.v_proj_weight, HD * H * 2, KVS / HD, (QS / HD + KVS / HD) % 8);
+        add(wn.o_proj_weight, 64 * QS * 2, H / 64, 0);
+      }
+    }
     gemm_gate_up(gu, stream);
     chk();
     GemmArgs gd{};
