@@ -113,9 +113,9 @@ struct XcdMap {
 // stored: the reads leave the rows in that XCD's L2 and in the memory-side cache, and the
 // product's own tiles run on other CUs, so their loads do not queue behind these.
 constexpr int MAX_WARM = 5, NUM_CUS = 256;  // (MI355X: 8 XCDs of 32 CUs)
-// Prompts up to this length warm in gate/up (whole prefill, same box, base -> warm-up:
-// S = 64 1.642 -> 1.605 ms, 128 1.769 -> 1.693, 192 1.721 -> 1.690, 256 1.808 -> 1.762;
-// from 320 on within +-1.6% either way, 512 1.956 -> 1.987 on one box)
+// Prompts up to this length warm in gate/up (whole prefill, same box, without -> with the
+// warm-up: S = 64 1.465 -> 1.408 ms, 128 1.511 -> 1.474, 256 1.675 -> 1.639; with the
+// S = 512 tile shapes, from 320 on within +-1.6% either way, 512 1.956 -> 1.987 on one box)
 constexpr int WARM_MAX_S = 256;
 struct WarmSet {
   const uint16_t* w[MAX_WARM];  // weight matrices [n, k] bf16, in the order they are read
@@ -1544,6 +1544,13 @@ void gemm(GemmArgs g, int ntiles, hipStream_t stream, int split = 1, int xg = 0,
   g.warm.row = ny;
   gemm_nt<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, ny + (g.warm.n > 0), split), 64 * WM * WN, 0, stream>>>(g);
 }
+// Prompts of at most SHORT_S tokens fill few CUs with the tiles of S = 512 (gate/up 48 x 2
+// workgroups at S = 256), so they take smaller row tiles: q/k/v 32 x 128, gate/up 64 x 128
+// (32 x 128 up to 128 tokens, 64 x 64 up to 64), the k-split residual products 64 x 64 (32 x
+// 64 up to 128). Every tile sums its k range in the same order whatever its shape, so the
+// outputs are the same bits. Whole prefill, same box, with the warm-up (ms): S = 64 1.600 ->
+// 1.408, 96 1.644 -> 1.451, 128 1.699 -> 1.474, 192 1.706 -> 1.591, 256 1.780 -> 1.639.
+constexpr int SHORT_S = 256;
 static void gemm_qkv(GemmArgs g, hipStream_t stream) {
   g.seg[0].ntiles = QS / HD;
   g.seg[1].ntiles = g.seg[2].ntiles = KVS / HD;
@@ -1553,7 +1560,8 @@ static void gemm_qkv(GemmArgs g, hipStream_t stream) {
   // 99.3 us against blockIdx order, same-box medians)
   if (g.m >= 2048) gemm<EPI_QKN, 256, HD, 3, 1, 4, 2>(g, nt, stream, 1, 1, 4);
   else if (g.m >= 1024) gemm<EPI_QKN, 128, HD, 4, 1, 4, 2>(g, nt, stream);
-  else gemm<EPI_QKN, 64, HD, 4, 1, 2, 4>(g, nt, stream);
+  else if (g.m > SHORT_S) gemm<EPI_QKN, 64, HD, 4, 1, 2, 4>(g, nt, stream);
+  else gemm<EPI_QKN, 32, HD, 4, 1, 2, 2>(g, nt, stream);
 }
 static void gemm_gate_up(GemmArgs g, hipStream_t stream) {
   if (g.m >= 2048) {
@@ -1562,9 +1570,18 @@ static void gemm_gate_up(GemmArgs g, hipStream_t stream) {
   } else if (g.m >= 1024) {
     g.seg[0].ntiles = I / 128;
     gemm<EPI_SILU, 128, 256, 3, 1, 4, 4>(g, I / 128, stream);
-  } else {
+  } else if (g.m > SHORT_S) {
     g.seg[0].ntiles = I / 64;
     gemm<EPI_SILU, 128, 128, 3, 1, 4, 4>(g, I / 64, stream);
+  } else if (g.m > 128) {
+    g.seg[0].ntiles = I / 64;
+    gemm<EPI_SILU, 64, 128, 3, 1, 2, 4>(g, I / 64, stream);
+  } else if (g.m > 64) {
+    g.seg[0].ntiles = I / 64;
+    gemm<EPI_SILU, 32, 128, 4, 1, 2, 2>(g, I / 64, stream);
+  } else {
+    g.seg[0].ntiles = I / 32;
+    gemm<EPI_SILU, 64, 64, 4, 1, 2, 2>(g, I / 32, stream);
   }
 }
 // Long prompts: o_proj / down_proj with the residual add in the epilogue (the four k quarters
@@ -1589,7 +1606,9 @@ static void gemm_residual(GemmArgs g, hipStream_t stream) {
     gemm<EPI_PART, 128, 256, 3, 1, 2, 4>(g, H / 256, stream, RES_SPLIT);
   } else {
     g.seg[0].ntiles = H / 64;
-    gemm<EPI_PART, 128, 64, 4, 1, 4, 2>(g, H / 64, stream, RES_SPLIT);
+    if (g.m > SHORT_S) gemm<EPI_PART, 128, 64, 4, 1, 4, 2>(g, H / 64, stream, RES_SPLIT);
+    else if (g.m > 128) gemm<EPI_PART, 64, 64, 4, 1, 2, 2>(g, H / 64, stream, RES_SPLIT);
+    else gemm<EPI_PART, 32, 64, 4, 1, 2, 2>(g, H / 64, stream, RES_SPLIT);
   }
 }
 
@@ -1702,8 +1721,8 @@ static int prefill_run(const int* input_token_ids, int* output_token_id, int seq
     if (S <= WARM_MAX_S) {
       // short prompts: the idle CUs of gate/up read down_proj's weights and the next layer's
       // q/k/v and o_proj weights, each column tile on the XCD of the launch that reads it
-      // (the 64x128 q/k/v tiles: q tiles 0-15, k 16-23, v 24-31; the 128x64 k-split
-      // residual tiles: 16)
+      // (q/k/v column tiles of one head: q 0-15, k 16-23, v 24-31; the k-split residual
+      // products' 64-column tiles: 16)
       WarmSet& W = gu.warm;
       auto add = [&](const void* wp, int tile_bytes, int ntiles, int xcd0) {
         W.w[W.n] = bf(wp); W.tile_bytes[W.n] = tile_bytes; W.ntiles[W.n] = ntiles; W.xcd0[W.n] = xcd0; W.n++;
