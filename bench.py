@@ -44,8 +44,8 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (for rocprofv3 counter scaling)")
     ap.add_argument("--cpu-decode-tokens", type=int, default=32)
-    ap.add_argument("--prefill-lens", type=str, default="512,8192",
-                    help="prompt lengths of the prefill timings (configs 4 and 5)")
+    ap.add_argument("--prefill-lens", type=str, default="128,512,8192",
+                    help="prompt lengths of the prefill timings (a short prompt, configs 4 and 5)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-coop", action="store_true", help="skip the cooperative-launch comparison")
     return ap.parse_args()
