@@ -291,7 +291,109 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
 
   // lane holds rows 4 * (lane / 16) + e of column lane % 16 of each block
   const int col = lane & 15, rq = 4 * (lane >> 4);
-  if constexpr (EPI == EPI_QKN) {
+  if constexpr (EPI == EPI_QKN && TN == 2 * HD) {
+    // Two heads a tile (long prompts: 256 x 256 tiles on sixteen waves): both heads'
+    // bf16-rounded outputs go through LDS as bf16 (exact, the values being bf16), [2][TM][HD]
+    // with each row's 16-byte chunks in slots chunk ^ (row % 16), so that the whole tile fits
+    // the ring and every accumulator is dead before the rows are processed; then each row of
+    // both heads is processed as in the one-head epilogue below, term for term (the norm
+    // weights and the row's cos/sin loaded once for both heads).
+    constexpr int RPI = 8 * NW, NPASS = TM / RPI;
+    static_assert(2 * TM * HD * 2 <= NST * KS * SCH * 16 && TM % RPI == 0, "both heads' rows fit the ring");
+    uint16_t* tile = reinterpret_cast<uint16_t*>(&sbuf[0][0][0]);
+    auto slot = [](int hh, int r, int d) { return (hh * TM + r) * HD + 8 * ((d >> 3) ^ (r & 15)) + (d & 7); };
+    __syncthreads();  // every wave is past its last read of the ring
+#pragma unroll
+    for (int i = 0; i < RB; i++)
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int j = 0; j < CB; j++) {
+          const int c = 16 * jb[j] + col;
+          tile[slot(c >> 7, 16 * (RB * wm + i) + rq + e, c & (HD - 1))] = (uint16_t)f2bf(acc[i][j][e]);
+        }
+    __syncthreads();
+    const QknArgs& Q = G.qkn;
+    const int pd = 8 * (lane & 7), rr = lane >> 3;
+    auto bf8 = [](const u32x4 v, float (&f)[8]) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        f[2 * e] = bf2f(v[e] & 0xffffu);
+        f[2 * e + 1] = bf2f(v[e] >> 16);
+      }
+    };
+    if (si == 2) {
+      // v rows: a copy
+#pragma unroll
+      for (int it = 0; it < NPASS; it++) {
+        const int r = RPI * it + 8 * wv + rr, t = m0 + r;
+        if (t >= G.m) continue;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+          uint16_t* dst = Q.vc + ((size_t)(2 * nt + hh) * Q.max_seq + t) * HD;
+          *reinterpret_cast<u32x4*>(dst + pd) = *reinterpret_cast<const u32x4*>(tile + slot(hh, r, pd));
+          *reinterpret_cast<u32x4*>(dst + 64 + pd) = *reinterpret_cast<const u32x4*>(tile + slot(hh, r, 64 + pd));
+        }
+      }
+      return;
+    }
+    const uint16_t* nwp = si == 0 ? Q.qn : Q.kn;
+    float w1[8], w2[8];
+    bf8(ldw(nwp + pd), w1);
+    bf8(ldw(nwp + 64 + pd), w2);
+    u32x4 cs[NPASS][4];
+#pragma unroll
+    for (int it = 0; it < NPASS; it++) {
+      const size_t t = (size_t)min(m0 + RPI * it + 8 * wv + rr, G.m - 1) * HD;  // rows past the prompt: never stored
+      cs[it][0] = ldw(Q.cos_t + t + pd);
+      cs[it][1] = ldw(Q.cos_t + t + 64 + pd);
+      cs[it][2] = ldw(Q.sin_t + t + pd);
+      cs[it][3] = ldw(Q.sin_t + t + 64 + pd);
+    }
+#pragma unroll
+    for (int it = 0; it < NPASS; it++) {
+      const int r = RPI * it + 8 * wv + rr, t = m0 + r;
+      float c1[8], c2[8], s1[8], s2[8];
+      bf8(cs[it][0], c1);
+      bf8(cs[it][1], c2);
+      bf8(cs[it][2], s1);
+      bf8(cs[it][3], s2);
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) {
+        float x1[8], x2[8];
+        bf8(*reinterpret_cast<const u32x4*>(tile + slot(hh, r, pd)), x1);
+        bf8(*reinterpret_cast<const u32x4*>(tile + slot(hh, r, 64 + pd)), x2);
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = x1[e] * x1[e] + x2[e] * x2[e];
+        float ss = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+        ss += dpp<0xB1>(ss);
+        ss += dpp<0x4E>(ss);
+        ss += dpp<0x141>(ss);
+        const float rstd = 1.0f / sqrtf(ss * (1.0f / HD) + EPS);
+        uint32_t o1[4], o2[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          float r1[2], r2[2];
+#pragma unroll
+          for (int u = 0; u < 2; u++) {
+            const float n1 = rbf(w1[e + u] * rbf(x1[e + u] * rstd)), n2 = rbf(w2[e + u] * rbf(x2[e + u] * rstd));
+            r1[u] = rbf(rbf(n1 * c1[e + u]) - rbf(n2 * s1[e + u]));
+            r2[u] = rbf(rbf(n2 * c2[e + u]) + rbf(n1 * s2[e + u]));
+          }
+          o1[e / 2] = pack_bf2(r1[0], r1[1]);
+          o2[e / 2] = pack_bf2(r2[0], r2[1]);
+        }
+        if (t >= G.m) continue;
+        const int h = 2 * nt + hh;
+        uint16_t* dst = si == 0 ? Q.q_out + (size_t)t * QS + HD * h : Q.kc + ((size_t)h * Q.max_seq + t) * HD;
+        *reinterpret_cast<u32x4*>(dst + pd) = u32x4{o1[0], o1[1], o1[2], o1[3]};
+        *reinterpret_cast<u32x4*>(dst + 64 + pd) = u32x4{o2[0], o2[1], o2[2], o2[3]};
+      }
+    }
+    return;
+  }
+  if constexpr (EPI == EPI_QKN && TN == HD) {
     // QK-norm (per head over 128, weights q_norm/k_norm) and RoPE (modeling_qwen3.py:247-257,
     // rotate_half form, three bf16 ops) of the tile's rows, which are tokens m0.. of head
     // nt of segment si (q, k or v); per token the reference's ldg_qk_norm_rope_cache
@@ -1562,6 +1664,21 @@ void gemm(GemmArgs g, int ntiles, hipStream_t stream, int split = 1, int xg = 0,
 // 1.408, 96 1.644 -> 1.451, 128 1.699 -> 1.474, 192 1.706 -> 1.591, 256 1.780 -> 1.639.
 constexpr int SHORT_S = 256;
 static void gemm_qkv(GemmArgs g, hipStream_t stream) {
+  // Long prompts: two heads a tile on sixteen waves (256 x 256, two stages; the epilogue stages
+  // both heads through the ring as bf16), blockIdx order, the same bits as the one-head
+  // 256 x 128 tiles. A two-head tile takes about 1.7 times as long as a one-head tile and there
+  // are half as many, so it is used where its rounds of 256 workgroups, ceil(16 ny / 256), cost
+  // less than the one-head tiles' ceil(32 ny / 256) (ny row tiles). Same box, the q/k/v launch
+  // alone: S = 2600 49.9 -> 40.2 us, 3072 51.9 -> 41.7, 4096 55.0 -> 44.8, 6400 98.8 -> 76.5,
+  // 7168 101.1 -> 80.1, 8192 98.1 -> 82.3; where the model says no: 2048 28.7 -> 39.0, 5000
+  // 74.4 -> 74.0, and the whole S = 6000 prefill 16.58 -> 16.68 ms.
+  const int ny = (g.m + 255) / 256;
+  if (g.m >= 2048 && 17 * ((ny + 15) / 16) < 10 * ((ny + 7) / 8)) {
+    g.seg[0].ntiles = QS / (2 * HD);
+    g.seg[1].ntiles = g.seg[2].ntiles = KVS / (2 * HD);
+    gemm<EPI_QKN, 256, 2 * HD, 2, 1, 4, 4>(g, (QS + 2 * KVS) / (2 * HD), stream);
+    return;
+  }
   g.seg[0].ntiles = QS / HD;
   g.seg[1].ntiles = g.seg[2].ntiles = KVS / HD;
   const int nt = (QS + 2 * KVS) / HD;
