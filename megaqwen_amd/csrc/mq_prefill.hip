@@ -1696,7 +1696,15 @@ static void gemm_qkv(GemmArgs g, hipStream_t stream) {
   else gemm<EPI_QKN, 32, HD, 4, 1, 2, 2>(g, nt, stream);
 }
 static void gemm_gate_up(GemmArgs g, hipStream_t stream) {
-  if (g.m >= 2048) {
+  // 2049..3584 tokens: 128 x 256 tiles, twice the workgroups of the 256 x 256 tiles, each
+  // taking about 0.6 of the time; they fill the last round of 256 workgroups better there
+  // (same bits; the launch alone, same box: S = 3072 67.9 -> 61.1 us; at 2048, 5000, 6000
+  // and 7000 the 256 x 256 tiles are as fast or faster, and at 4096 the launch alone gains
+  // (72.0 -> 66.9) but the whole prefill loses, 9.99 -> 10.18 ms)
+  if (g.m > 2048 && g.m <= 3584) {
+    g.seg[0].ntiles = I / 128;
+    gemm<EPI_SILU, 128, 256, 3, 1, 4, 4>(g, I / 128, stream);
+  } else if (g.m >= 2048) {
     g.seg[0].ntiles = I / 128;
     gemm<EPI_SILU, 256, 256, 2, 1, 4, 4>(g, I / 128, stream);  // (the XCD order measured no gain here)
   } else if (g.m >= 1024) {
@@ -1730,7 +1738,10 @@ static void gemm_residual_add(GemmArgs g, uint16_t* h, hipStream_t stream) {
   gemm<EPI_RESADD, 256, 128, 3, 1, 4, 2>(g, H / 128, stream, 1, 2, 4);
 }
 static void gemm_residual(GemmArgs g, hipStream_t stream) {
-  if (g.m >= 4096) {
+  // 256 x 256 tiles from 2049 tokens (at most one round of 256 workgroups up to 4096, where
+  // the 128 x 256 tiles need two; same bits, down_proj's shape alone, same box: S = 3072
+  // 37.8 -> 29.9 us; at 2048 the 128 x 256 tiles are faster, 23.1 against 25.1)
+  if (g.m > 2048) {
     g.seg[0].ntiles = H / 256;
     gemm<EPI_PART, 256, 256, 2, 1, 4, 4>(g, H / 256, stream, RES_SPLIT);
   } else if (g.m >= 1024) {
