@@ -1684,6 +1684,16 @@ static void gemm_qkv(GemmArgs g, hipStream_t stream) {
     gemm<EPI_QKN, 256, 2 * HD, 2, 1, 4, 4>(g, (QS + 2 * KVS) / (2 * HD), stream);
     return;
   }
+  if (g.m > 1024 && g.m < 2048) {
+    // 1025..2047 tokens: two heads a tile on 128 x 256 tiles (sixteen waves, three stages), one
+    // round of at most 256 workgroups where the one-head 128 x 128 tiles need two (the same
+    // rounds argument as above); same bits, the launch alone, same box: S = 1100 30.6 -> 23.5
+    // us, 1536 31.6 -> 24.4, 2047 33.7 -> 27.2 (at 1024 both take one round)
+    g.seg[0].ntiles = QS / (2 * HD);
+    g.seg[1].ntiles = g.seg[2].ntiles = KVS / (2 * HD);
+    gemm<EPI_QKN, 128, 2 * HD, 3, 1, 4, 4>(g, (QS + 2 * KVS) / (2 * HD), stream);
+    return;
+  }
   g.seg[0].ntiles = QS / HD;
   g.seg[1].ntiles = g.seg[2].ntiles = KVS / HD;
   const int nt = (QS + 2 * KVS) / HD;
@@ -1704,7 +1714,9 @@ static void gemm_gate_up(GemmArgs g, hipStream_t stream) {
   if (g.m > 2048 && g.m <= 3584) {
     g.seg[0].ntiles = I / 128;
     gemm<EPI_SILU, 128, 256, 3, 1, 4, 4>(g, I / 128, stream);
-  } else if (g.m >= 2048) {
+  } else if (g.m > 1408) {
+    // (from 1409 tokens the 128 x 256 tiles need more than one round of 256 workgroups; the
+    // 256 x 256 tiles: S = 1536 38.2 -> 34.5 us, 2047 40.8 -> 38.8; at 1100 22.2 -> 34.5)
     g.seg[0].ntiles = I / 128;
     gemm<EPI_SILU, 256, 256, 2, 1, 4, 4>(g, I / 128, stream);  // (the XCD order measured no gain here)
   } else if (g.m >= 1024) {
