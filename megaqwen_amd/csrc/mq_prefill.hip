@@ -1684,6 +1684,16 @@ static void gemm_qkv(GemmArgs g, hipStream_t stream) {
     gemm<EPI_QKN, 256, 2 * HD, 2, 1, 4, 4>(g, (QS + 2 * KVS) / (2 * HD), stream);
     return;
   }
+  if (g.m > 512 && g.m < 1024) {
+    // 513..1023 tokens: two heads a tile on 64 x 256 tiles (eight waves, four stages), one round
+    // of at most 256 workgroups where the one-head 64 x 128 tiles need two; same bits, the
+    // launch alone, same box: S = 640 19.0 -> 17.1 us, 768 19.6 -> 17.4, 1000 21.2 -> 19.1
+    // (up to 512 tokens the one-head tiles are faster: 11.3 against 16.6 us at S = 512)
+    g.seg[0].ntiles = QS / (2 * HD);
+    g.seg[1].ntiles = g.seg[2].ntiles = KVS / (2 * HD);
+    gemm<EPI_QKN, 64, 2 * HD, 4, 1, 2, 4>(g, (QS + 2 * KVS) / (2 * HD), stream);
+    return;
+  }
   if (g.m > 1024 && g.m < 2048) {
     // 1025..2047 tokens: two heads a tile on 128 x 256 tiles (sixteen waves, three stages), one
     // round of at most 256 workgroups where the one-head 128 x 128 tiles need two (the same
@@ -1720,6 +1730,11 @@ static void gemm_gate_up(GemmArgs g, hipStream_t stream) {
     g.seg[0].ntiles = I / 128;
     gemm<EPI_SILU, 256, 256, 2, 1, 4, 4>(g, I / 128, stream);  // (the XCD order measured no gain here)
   } else if (g.m >= 1024) {
+    g.seg[0].ntiles = I / 128;
+    gemm<EPI_SILU, 128, 256, 3, 1, 4, 4>(g, I / 128, stream);
+  } else if (g.m > 640) {
+    // (641..1023 tokens: the 128 x 128 tiles need a second round of 256 workgroups, the
+    // 128 x 256 tiles one; S = 768 24.6 -> 20.5 us, 1000 25.3 -> 21.6; at 640 14.6 -> 19.9)
     g.seg[0].ntiles = I / 128;
     gemm<EPI_SILU, 128, 256, 3, 1, 4, 4>(g, I / 128, stream);
   } else if (g.m > SHORT_S) {
@@ -1759,6 +1774,11 @@ static void gemm_residual(GemmArgs g, hipStream_t stream) {
   } else if (g.m >= 1024) {
     g.seg[0].ntiles = H / 256;
     gemm<EPI_PART, 128, 256, 3, 1, 2, 4>(g, H / 256, stream, RES_SPLIT);
+  } else if (g.m > 512) {
+    // (513..1023 tokens: one round of 256 workgroups on 128 x 128 tiles where 128 x 64 tiles
+    // need two; S = 640 15.1 -> 12.5 us, 1000 17.1 -> 15.2)
+    g.seg[0].ntiles = H / 128;
+    gemm<EPI_PART, 128, 128, 4, 1, 4, 2>(g, H / 128, stream, RES_SPLIT);
   } else {
     g.seg[0].ntiles = H / 64;
     if (g.m > SHORT_S) gemm<EPI_PART, 128, 64, 4, 1, 4, 2>(g, H / 64, stream, RES_SPLIT);
