@@ -111,7 +111,10 @@ struct XcdMap {
 // the XCD that will read it: in blockIdx order with a multiple of 8 column tiles, a
 // consumer's column tile t runs on XCD t % 8 whatever its row tile and k split. Nothing is
 // stored: the reads leave the rows in that XCD's L2 and in the memory-side cache, and the
-// product's own tiles run on other CUs, so their loads do not queue behind these.
+// product's own tiles run on other CUs, so their loads do not queue behind these. The set is
+// the second argument of its own kernel (gemm_nt_warm), not a field of GemmArgs: with it in
+// every launch's argument block the launches without a warm-up row ran slower (whole
+// prefill, same box: S = 300 1.779 -> 1.807 ms, 512 1.962 -> 1.992).
 constexpr int MAX_WARM = 5, NUM_CUS = 256;  // (MI355X: 8 XCDs of 32 CUs)
 // Prompts up to this length warm in gate/up (whole prefill, same box, without -> with the
 // warm-up: S = 64 1.465 -> 1.408 ms, 128 1.511 -> 1.474, 256 1.675 -> 1.639; with the
@@ -132,7 +135,6 @@ struct GemmArgs {
   PartSet part;  // EPI_PART: set z takes the partial sums of k split z (blockIdx.z)
   QknArgs qkn;   // EPI_QKN
   XcdMap xm;
-  WarmSet warm;
 };
 
 // The warm-up row's work. Its gridDim.x / 8 workgroups on XCD c (linear id L, L % 8 == c;
@@ -159,8 +161,8 @@ __device__ void warm_tiles(const WarmSet& W, uint32_t lds, int wv, int lane) {
 // LDS slot (in 16-byte chunks) of chunk kc (0..7) of tile row r.
 __device__ __forceinline__ int tslot(int r, int kc) { return r * 8 + (kc ^ (r & 7)); }
 
-template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
+template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN, bool WARM>
+__device__ __forceinline__ void gemm_tiles(const GemmArgs& G, const WarmSet* W) {
   constexpr int NW = WM * WN, NT = 64 * NW;
   constexpr int RB = TM / (16 * WM);      // 16-row blocks per wave
   constexpr int CB = TN / (16 * WN);      // 16-column blocks per wave
@@ -174,9 +176,9 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
                 "a DMA instruction covers 64 slots of one operand of one k-step");
   __shared__ u32x4 sbuf[NST][KS][SCH];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv / WN, wn = wv % WN;
-  if (G.warm.n > 0 && (int)blockIdx.y == G.warm.row) {
+  if (WARM && (int)blockIdx.y == W->row) {
     static_assert(NW * 1024 <= NST * KS * SCH * 16, "a wave's DMA unit fits the ring");
-    warm_tiles<NW>(G.warm, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sbuf[0][0][0], wv, lane);
+    warm_tiles<NW>(*W, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sbuf[0][0][0], wv, lane);
     return;
   }
   int nt = blockIdx.x, mt = blockIdx.y;  // column tile, row tile
@@ -544,6 +546,15 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
         for (int j = 0; j < CB; j++) orow[TN * nt + 16 * jb[j] + col] = (uint16_t)f2bf(acc[i][j][e]);
       }
     }
+}
+template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
+  gemm_tiles<EPI, TM, TN, NST, KS, WM, WN, false>(G, nullptr);
+}
+// the same product with a warm-up row of workgroups (blockIdx.y == W.row) after its tiles
+template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_nt_warm(GemmArgs G, WarmSet W) {
+  gemm_tiles<EPI, TM, TN, NST, KS, WM, WN, true>(G, &W);
 }
 
 // ------------------------------------------------------------------ row-wise kernels
@@ -1652,14 +1663,19 @@ static XcdMap xcd_map(int nx, int ny, int xg, int xp) {
   return XcdMap{xg, xp};
 }
 template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
-void gemm(GemmArgs g, int ntiles, hipStream_t stream, int split = 1, int xg = 0, int xp = 1) {
+void gemm(GemmArgs g, int ntiles, hipStream_t stream, int split = 1, int xg = 0, int xp = 1,
+          const WarmSet* warm = nullptr) {
   const int ny = (g.m + TM - 1) / TM;
   g.xm = xcd_map(ntiles, ny, xg, xp);
   // a warm-up row only where its workgroups land on CUs no tile uses, eight to an XCD
   // class, in blockIdx order
-  if (g.warm.n > 0 && (ntiles % 8 || split != 1 || g.xm.xg > 0 || ntiles * (ny + 1) > NUM_CUS)) g.warm.n = 0;
-  g.warm.row = ny;
-  gemm_nt<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, ny + (g.warm.n > 0), split), 64 * WM * WN, 0, stream>>>(g);
+  if (warm && warm->n > 0 && ntiles % 8 == 0 && split == 1 && g.xm.xg == 0 && ntiles * (ny + 1) <= NUM_CUS) {
+    WarmSet W = *warm;
+    W.row = ny;
+    gemm_nt_warm<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, ny + 1, split), 64 * WM * WN, 0, stream>>>(g, W);
+  } else {
+    gemm_nt<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, ny, split), 64 * WM * WN, 0, stream>>>(g);
+  }
 }
 // Prompts of at most SHORT_S tokens fill few CUs with the tiles of S = 512 (gate/up 48 x 2
 // workgroups at S = 256), so they take smaller row tiles: q/k/v 32 x 128, gate/up 64 x 128
@@ -1715,7 +1731,9 @@ static void gemm_qkv(GemmArgs g, hipStream_t stream) {
   else if (g.m > SHORT_S) gemm<EPI_QKN, 64, HD, 4, 1, 2, 4>(g, nt, stream);
   else gemm<EPI_QKN, 32, HD, 4, 1, 2, 2>(g, nt, stream);
 }
-static void gemm_gate_up(GemmArgs g, hipStream_t stream) {
+// warm: the warm-up set of a short prompt (at most WARM_MAX_S tokens), or null
+static void gemm_gate_up(GemmArgs g, hipStream_t stream, const WarmSet* warm = nullptr) {
+  static_assert(WARM_MAX_S <= SHORT_S, "only the short-prompt tile shapes take a warm-up row");
   // 2049..3584 tokens: 128 x 256 tiles, twice the workgroups of the 256 x 256 tiles, each
   // taking about 0.6 of the time; they fill the last round of 256 workgroups better there
   // (same bits; the launch alone, same box: S = 3072 67.9 -> 61.1 us; at 2048, 5000, 6000
@@ -1742,13 +1760,13 @@ static void gemm_gate_up(GemmArgs g, hipStream_t stream) {
     gemm<EPI_SILU, 128, 128, 3, 1, 4, 4>(g, I / 64, stream);
   } else if (g.m > 128) {
     g.seg[0].ntiles = I / 64;
-    gemm<EPI_SILU, 64, 128, 3, 1, 2, 4>(g, I / 64, stream);
+    gemm<EPI_SILU, 64, 128, 3, 1, 2, 4>(g, I / 64, stream, 1, 0, 1, warm);
   } else if (g.m > 64) {
     g.seg[0].ntiles = I / 64;
-    gemm<EPI_SILU, 32, 128, 4, 1, 2, 2>(g, I / 64, stream);
+    gemm<EPI_SILU, 32, 128, 4, 1, 2, 2>(g, I / 64, stream, 1, 0, 1, warm);
   } else {
     g.seg[0].ntiles = I / 32;
-    gemm<EPI_SILU, 64, 64, 4, 1, 2, 2>(g, I / 32, stream);
+    gemm<EPI_SILU, 64, 64, 4, 1, 2, 2>(g, I / 32, stream, 1, 0, 1, warm);
   }
 }
 // Long prompts: o_proj / down_proj with the residual add in the epilogue (the four k quarters
@@ -1895,12 +1913,12 @@ static int prefill_run(const int* input_token_ids, int* output_token_id, int seq
     GemmArgs gu{};
     gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
     gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, 0, I};
+    WarmSet W{};
     if (S <= WARM_MAX_S) {
       // short prompts: the idle CUs of gate/up read down_proj's weights and the next layer's
       // q/k/v and o_proj weights, each column tile on the XCD of the launch that reads it
       // (q/k/v column tiles of one head: q 0-15, k 16-23, v 24-31; the k-split residual
       // products' 64-column tiles: 16)
-      WarmSet& W = gu.warm;
       auto add = [&](const void* wp, int tile_bytes, int ntiles, int xcd0) {
         W.w[W.n] = bf(wp); W.tile_bytes[W.n] = tile_bytes; W.ntiles[W.n] = ntiles; W.xcd0[W.n] = xcd0; W.n++;
       };
@@ -1913,7 +1931,7 @@ static int prefill_run(const int* input_token_ids, int* output_token_id, int seq
         add(wn.o_proj_weight, 64 * QS * 2, H / 64, 0);
       }
     }
-    gemm_gate_up(gu, stream);
+    gemm_gate_up(gu, stream, W.n > 0 ? &W : nullptr);
     chk();
     GemmArgs gd{};
     gd.a = mid; gd.lda = I; gd.m = S; gd.k = I; gd.nseg = 1;
