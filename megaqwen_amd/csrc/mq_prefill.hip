@@ -130,21 +130,43 @@ struct WarmSet {
 };
 struct GemmArgs {
   const uint16_t* a;  // [m, lda] bf16
-  int lda, m, k, nseg;
-  GemmSeg seg[3];
+  int lda, m, k;
+  GemmSeg seg[3];  // q/k/v: q, k, v; the others: one
   PartSet part;  // EPI_PART: set z takes the partial sums of k split z (blockIdx.z)
   QknArgs qkn;   // EPI_QKN
   XcdMap xm;
 };
+// One launch's argument block: only the fields its epilogue reads (q/k/v: three segments
+// and the QK-norm/RoPE block, 200 bytes; the k-split products: one segment and the
+// partial-sum set, 160; the others: one segment, 72). The whole GemmArgs (280 bytes) in
+// every launch ran slower (whole prefill, same box: S = 128 1.422 -> 1.401 ms, 512
+// 1.958 -> 1.946, 2048 5.333 -> 5.329; same bits). The grid's size comes in the block
+// too: a kernel that reads gridDim gets the 256 bytes of hidden arguments appended to its
+// block (S = 128 1.402 -> 1.395 ms, 512 1.954 -> 1.937 without them, the attention
+// kernels' likewise).
+template <int EPI> struct EpiBlock {};
+template <> struct EpiBlock<EPI_PART> { PartSet part; };
+template <> struct EpiBlock<EPI_QKN> { QknArgs qkn; };
+template <int EPI>
+struct KernArgs : EpiBlock<EPI> {
+  static constexpr int NSEG = EPI == EPI_QKN ? 3 : 1;
+  const uint16_t* a;
+  int lda, m, k;
+  XcdMap xm;
+  int nx, ny, kp;  // the grid's column tiles and row tiles (no warm-up row), k per split
+  GemmSeg seg[NSEG];
+};
+static_assert(sizeof(KernArgs<EPI_SILU>) == 72 && sizeof(KernArgs<EPI_PART>) == 160 &&
+              sizeof(KernArgs<EPI_QKN>) == 200, "the argument block sizes stated above");
 
 // The warm-up row's work. Its gridDim.x / 8 workgroups on XCD c (linear id L, L % 8 == c;
 // the launcher keeps gridDim.x a multiple of 8 and one k split) split every tile t with
 // (xcd0 + t) % 8 == c into equal runs of 1 KB units; a wave reads one unit per DMA (64
 // lanes x 16 bytes) into its own 1 KB of the workgroup's LDS, which nothing reads.
 template <int NW>
-__device__ void warm_tiles(const WarmSet& W, uint32_t lds, int wv, int lane) {
-  const int L = blockIdx.x + gridDim.x * blockIdx.y, c = L & 7;
-  const int nwg = gridDim.x >> 3, j = (L >> 3) - (gridDim.x >> 3) * W.row;
+__device__ void warm_tiles(const WarmSet& W, int nx, uint32_t lds, int wv, int lane) {
+  const int L = blockIdx.x + nx * blockIdx.y, c = L & 7;
+  const int nwg = nx >> 3, j = (L >> 3) - (nx >> 3) * W.row;
   const uint32_t dst = __builtin_amdgcn_readfirstlane(lds + 1024u * (uint32_t)wv);
 #pragma unroll
   for (int r = 0; r < MAX_WARM; r++) {
@@ -162,7 +184,7 @@ __device__ void warm_tiles(const WarmSet& W, uint32_t lds, int wv, int lane) {
 __device__ __forceinline__ int tslot(int r, int kc) { return r * 8 + (kc ^ (r & 7)); }
 
 template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN, bool WARM>
-__device__ __forceinline__ void gemm_tiles(const GemmArgs& G, const WarmSet* W) {
+__device__ __forceinline__ void gemm_tiles(const KernArgs<EPI>& G, const WarmSet* W) {
   constexpr int NW = WM * WN, NT = 64 * NW;
   constexpr int RB = TM / (16 * WM);      // 16-row blocks per wave
   constexpr int CB = TN / (16 * WN);      // 16-column blocks per wave
@@ -178,7 +200,7 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& G, const WarmSet* W) 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wm = wv / WN, wn = wv % WN;
   if (WARM && (int)blockIdx.y == W->row) {
     static_assert(NW * 1024 <= NST * KS * SCH * 16, "a wave's DMA unit fits the ring");
-    warm_tiles<NW>(*W, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sbuf[0][0][0], wv, lane);
+    warm_tiles<NW>(*W, G.nx, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&sbuf[0][0][0], wv, lane);
     return;
   }
   int nt = blockIdx.x, mt = blockIdx.y;  // column tile, row tile
@@ -186,17 +208,18 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& G, const WarmSet* W) 
   if (G.xm.xg > 0) {
     // (the host sets xg only when 8 divides the tile count, xg the column tiles, 8 / xg the
     // row tiles and xp the row tiles of a band)
-    const int nx = gridDim.x, L = blockIdx.x + nx * blockIdx.y, c = L & 7, s = L >> 3;
-    const int cw = nx / G.xm.xg, rh = (int)gridDim.y / (8 / G.xm.xg), pn = G.xm.xp * cw;
+    const int nx = G.nx, L = blockIdx.x + nx * blockIdx.y, c = L & 7, s = L >> 3;
+    const int cw = nx / G.xm.xg, rh = G.ny / (8 / G.xm.xg), pn = G.xm.xp * cw;
     const int r = s / pn * G.xm.xp + s % pn % G.xm.xp, cc = s % pn / G.xm.xp;
     mt = c / G.xm.xg * rh + r;
     nt = c % G.xm.xg * cw + cc;
   }
   int si = 0;
-  while (si + 1 < G.nseg && nt >= G.seg[si].ntiles) nt -= G.seg[si++].ntiles;
+  if constexpr (KernArgs<EPI>::NSEG > 1)
+    while (si + 1 < KernArgs<EPI>::NSEG && nt >= G.seg[si].ntiles) nt -= G.seg[si++].ntiles;
   const GemmSeg S = G.seg[si];
   const int m0 = mt * TM;
-  const int kp = G.k / (int)gridDim.z, kz = kp * z;  // this split's k range
+  const int kp = G.kp, kz = kp * z;  // this split's k range
   const int KT = kp / (TK * KS);
 
   // the wave's column blocks; EPI_SILU: blocks j < CB / 2 are gate blocks, each paired with
@@ -524,7 +547,7 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& G, const WarmSet* W) 
         }
         continue;
       }
-      if (EPI == EPI_PART) {
+      if constexpr (EPI == EPI_PART) {
         static_assert(PART_HALF % TN == 0, "a tile lies in one column half");
         const int c0 = TN * nt;
         float* prow = (c0 < PART_HALF ? G.part.lo[z] : G.part.hi[z]) + (size_t)row * G.part.ld[z] + c0 % PART_HALF;
@@ -548,12 +571,12 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& G, const WarmSet* W) 
     }
 }
 template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_nt(GemmArgs G) {
+__global__ void __launch_bounds__(64 * WM * WN) gemm_nt(KernArgs<EPI> G) {
   gemm_tiles<EPI, TM, TN, NST, KS, WM, WN, false>(G, nullptr);
 }
 // the same product with a warm-up row of workgroups (blockIdx.y == W.row) after its tiles
 template <int EPI, int TM, int TN, int NST, int KS, int WM, int WN>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_nt_warm(GemmArgs G, WarmSet W) {
+__global__ void __launch_bounds__(64 * WM * WN) gemm_nt_warm(KernArgs<EPI> G, WarmSet W) {
   gemm_tiles<EPI, TM, TN, NST, KS, WM, WN, true>(G, &W);
 }
 
@@ -750,7 +773,7 @@ __global__ void __launch_bounds__(64 * AW) attn_prefill(const uint16_t* q, const
   // 32 workgroups reading one group's K/V rows share one L2; the longest query blocks
   // (the most keys) are dispatched first
   const int id = blockIdx.x, g = id & 7, r = id >> 3, h = 2 * g + (r & 1);
-  const int r0 = (gridDim.x / NQ - 1 - (r >> 1)) * AQ;
+  const int r0 = ((S + AQ - 1) / AQ - 1 - (r >> 1)) * AQ;  // (the grid: NQ x that many blocks)
   const uint16_t* K = kc + (size_t)g * max_seq * HD;
   const uint16_t* V = vc + (size_t)g * max_seq * HD;
   const int nkey = min(S, r0 + AQ);
@@ -995,7 +1018,7 @@ __global__ void __launch_bounds__(64 * F2W) attn_prefill_fa2(const uint16_t* q, 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   // XCD-aware order: workgroup id runs on XCD id % 8, made the KV group; the longest query
   // blocks (the most keys) are dispatched first
-  const int id = blockIdx.x, g = id & 7, nqb = gridDim.x >> 3;
+  const int id = blockIdx.x, g = id & 7, nqb = (S + F2Q - 1) / F2Q;  // (the grid: 8 x nqb blocks)
   const int r0 = (nqb - 1 - (id >> 3)) * F2Q;
   const int r16 = lane & 15, kg = lane >> 4;
   const int row = r0 + 16 * wv + r16;  // this lane's query row
@@ -1289,7 +1312,7 @@ __global__ void __launch_bounds__(64 * F3W) attn_prefill_fa3(const uint16_t* q, 
   __shared__ __align__(16) uint8_t s_q[2][F3Q * 256];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   // XCD-aware order as attn_prefill_fa2: KV group = XCD, longest query blocks first
-  const int id = blockIdx.x, g = id & 7, nqb = gridDim.x >> 3;
+  const int id = blockIdx.x, g = id & 7, nqb = (S + F3Q - 1) / F3Q;  // (the grid: 8 x nqb blocks)
   const int r0 = (nqb - 1 - (id >> 3)) * F3Q;
   const int r16 = lane & 15, kg = lane >> 4;
   const int row = r0 + 16 * wv + r16;                  // this lane's query row
@@ -1669,12 +1692,18 @@ void gemm(GemmArgs g, int ntiles, hipStream_t stream, int split = 1, int xg = 0,
   g.xm = xcd_map(ntiles, ny, xg, xp);
   // a warm-up row only where its workgroups land on CUs no tile uses, eight to an XCD
   // class, in blockIdx order
+  KernArgs<EPI> ka{};
+  ka.a = g.a; ka.lda = g.lda; ka.m = g.m; ka.k = g.k; ka.xm = g.xm;
+  ka.nx = ntiles; ka.ny = ny; ka.kp = g.k / split;
+  for (int i = 0; i < KernArgs<EPI>::NSEG; i++) ka.seg[i] = g.seg[i];
+  if constexpr (EPI == EPI_PART) ka.part = g.part;
+  if constexpr (EPI == EPI_QKN) ka.qkn = g.qkn;
   if (warm && warm->n > 0 && ntiles % 8 == 0 && split == 1 && g.xm.xg == 0 && ntiles * (ny + 1) <= NUM_CUS) {
     WarmSet W = *warm;
     W.row = ny;
-    gemm_nt_warm<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, ny + 1, split), 64 * WM * WN, 0, stream>>>(g, W);
+    gemm_nt_warm<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, ny + 1, split), 64 * WM * WN, 0, stream>>>(ka, W);
   } else {
-    gemm_nt<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, ny, split), 64 * WM * WN, 0, stream>>>(g);
+    gemm_nt<EPI, TM, TN, NST, KS, WM, WN><<<dim3(ntiles, ny, split), 64 * WM * WN, 0, stream>>>(ka);
   }
 }
 // Prompts of at most SHORT_S tokens fill few CUs with the tiles of S = 512 (gate/up 48 x 2
@@ -1875,7 +1904,7 @@ static int prefill_run(const int* input_token_ids, int* output_token_id, int seq
     uint16_t* kcl = bfm(k_cache) + l * kv_layer;
     uint16_t* vcl = bfm(v_cache) + l * kv_layer;
     GemmArgs g{};
-    g.a = nrm; g.lda = H; g.m = S; g.k = H; g.nseg = 3;
+    g.a = nrm; g.lda = H; g.m = S; g.k = H;
     g.seg[0] = GemmSeg{bf(w.q_proj_weight), nullptr, nullptr, 0, QS};
     g.seg[1] = GemmSeg{bf(w.k_proj_weight), nullptr, nullptr, 0, KVS};
     g.seg[2] = GemmSeg{bf(w.v_proj_weight), nullptr, nullptr, 0, KVS};
@@ -1897,7 +1926,7 @@ static int prefill_run(const int* input_token_ids, int* output_token_id, int seq
       attn_prefill<false><<<NQ * ((S + AQ - 1) / AQ), 64 * AW, 0, stream>>>(qp, kcl, vcl, att, S, max_seq_len, attn_scale);
     chk();
     GemmArgs go{};
-    go.a = att; go.lda = QS; go.m = S; go.k = QS; go.nseg = 1;
+    go.a = att; go.lda = QS; go.m = S; go.k = QS;
     go.seg[0] = GemmSeg{bf(w.o_proj_weight), nullptr, nullptr, 0, H};
     if (S >= RESADD_MIN_S) {
       gemm_residual_add(go, h, stream);
@@ -1911,7 +1940,7 @@ static int prefill_run(const int* input_token_ids, int* output_token_id, int seq
     }
     chk();
     GemmArgs gu{};
-    gu.a = mln; gu.lda = H; gu.m = S; gu.k = H; gu.nseg = 1;
+    gu.a = mln; gu.lda = H; gu.m = S; gu.k = H;
     gu.seg[0] = GemmSeg{bf(w.gate_proj_weight), bf(w.up_proj_weight), mid, 0, I};
     WarmSet W{};
     if (S <= WARM_MAX_S) {
@@ -1934,7 +1963,7 @@ static int prefill_run(const int* input_token_ids, int* output_token_id, int seq
     gemm_gate_up(gu, stream, W.n > 0 ? &W : nullptr);
     chk();
     GemmArgs gd{};
-    gd.a = mid; gd.lda = I; gd.m = S; gd.k = I; gd.nseg = 1;
+    gd.a = mid; gd.lda = I; gd.m = S; gd.k = I;
     gd.seg[0] = GemmSeg{bf(w.down_proj_weight), nullptr, nullptr, 0, H};
     // then the next layer's input RMSNorm (none after the last: the final norm is the LM head's)
     if (S >= RESADD_MIN_S) {
