@@ -117,9 +117,10 @@ struct XcdMap {
 // prefill, same box: S = 300 1.779 -> 1.807 ms, 512 1.962 -> 1.992).
 constexpr int MAX_WARM = 5, NUM_CUS = 256;  // (MI355X: 8 XCDs of 32 CUs)
 // Prompts up to this length warm in gate/up (whole prefill, same box, without -> with the
-// warm-up: S = 64 1.465 -> 1.408 ms, 128 1.511 -> 1.474, 256 1.675 -> 1.639; with the
-// S = 512 tile shapes, from 320 on within +-1.6% either way, 512 1.956 -> 1.987 on one box)
-constexpr int WARM_MAX_S = 256;
+// warm-up: S = 64 1.465 -> 1.408 ms, 128 1.511 -> 1.474, 256 1.675 -> 1.639, 288 1.755 ->
+// 1.730, 352 1.804 -> 1.760, 384 1.839 -> 1.782; from 385 tokens gate/up has 192 tile
+// workgroups, and with the warm-up row S = 400 measured 1.794 -> 1.801, 512 1.930 -> 1.927)
+constexpr int WARM_MAX_S = 384;
 struct WarmSet {
   const uint16_t* w[MAX_WARM];  // weight matrices [n, k] bf16, in the order they are read
   int tile_bytes[MAX_WARM];     // bytes of one consumer column tile (a multiple of 1 KB)
@@ -1760,9 +1761,9 @@ static void gemm_qkv(GemmArgs g, hipStream_t stream) {
   else if (g.m > SHORT_S) gemm<EPI_QKN, 64, HD, 4, 1, 2, 4>(g, nt, stream);
   else gemm<EPI_QKN, 32, HD, 4, 1, 2, 2>(g, nt, stream);
 }
-// warm: the warm-up set of a short prompt (at most WARM_MAX_S tokens), or null
+// warm: the warm-up set of a prompt of at most WARM_MAX_S tokens, or null
 static void gemm_gate_up(GemmArgs g, hipStream_t stream, const WarmSet* warm = nullptr) {
-  static_assert(WARM_MAX_S <= SHORT_S, "only the short-prompt tile shapes take a warm-up row");
+  static_assert(WARM_MAX_S <= 512, "the warm-up set's column tiles are those of the shapes up to 512 tokens");
   // 2049..3584 tokens: 128 x 256 tiles, twice the workgroups of the 256 x 256 tiles, each
   // taking about 0.6 of the time; they fill the last round of 256 workgroups better there
   // (same bits; the launch alone, same box: S = 3072 67.9 -> 61.1 us; at 2048, 5000, 6000
@@ -1786,7 +1787,7 @@ static void gemm_gate_up(GemmArgs g, hipStream_t stream, const WarmSet* warm = n
     gemm<EPI_SILU, 128, 256, 3, 1, 4, 4>(g, I / 128, stream);
   } else if (g.m > SHORT_S) {
     g.seg[0].ntiles = I / 64;
-    gemm<EPI_SILU, 128, 128, 3, 1, 4, 4>(g, I / 64, stream);
+    gemm<EPI_SILU, 128, 128, 3, 1, 4, 4>(g, I / 64, stream, 1, 0, 1, warm);
   } else if (g.m > 128) {
     g.seg[0].ntiles = I / 64;
     gemm<EPI_SILU, 64, 128, 3, 1, 2, 4>(g, I / 64, stream, 1, 0, 1, warm);

@@ -48,13 +48,14 @@ def prompt_ids(n, seed):
     return weights.random_prompt(n, seed=seed)
 
 
-@pytest.mark.parametrize("S", [1, 37, 100, 130, 256])
+@pytest.mark.parametrize("S", [1, 37, 100, 130, 256, 300])
 def test_prefill_vs_oracle_ragged(state_dict, embed_gpu, S):
     """2-layer model, prompt lengths that are not multiples of any tile: K/V slots,
     the residual stream, the final-norm row and the greedy token against the oracle.
-    The lengths cover each short-prompt tile shape (up to 64, 128 and 256 tokens)."""
+    The lengths cover each short-prompt tile shape (up to 64, 128 and 256 tokens) and
+    the S = 512 shapes with gate/up's warm-up row (257 to 384 tokens)."""
     print(f"prefill S={S}", flush=True)
-    dec, orc = small_pair(state_dict, embed_gpu, 2, 256)
+    dec, orc = small_pair(state_dict, embed_gpu, 2, 320)
     ids = prompt_ids(S, seed=10 + S)
     tok = dec.prefill_step(ids)
     otok, olg = orc.prefill(ids)
