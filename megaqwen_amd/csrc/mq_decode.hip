@@ -806,6 +806,28 @@ __device__ __forceinline__ void poll_words(const Buf& wsb, uint32_t* ws, const u
   }
 }
 
+// v[q] for q = 0..3 as two levels of selects on the bits of q (no branches)
+__device__ __forceinline__ float pick4(int q, float v0, float v1, float v2, float v3) {
+  const float lo = (q & 1) ? v1 : v0, hi = (q & 1) ? v3 : v2;
+  return (q & 2) ? hi : lo;
+}
+// For lanes 0..15: x of lanes j + 16, j + 32 and j + 48 (j = lane), the "other" results of
+// v_permlane16_swap / v_permlane32_swap of x with itself (a lane's pair of results holds its
+// own value and its partner's, in either order; equal bits either way when they are equal).
+__device__ __forceinline__ float swap_other(float own, u32x2 sw) {
+  return __uint_as_float(sw[0] == __float_as_uint(own) ? sw[1] : sw[0]);
+}
+__device__ __forceinline__ void lane_rows(float x, float& a1, float& a2, float& a3) {
+  const uint32_t u = __float_as_uint(x);
+  const auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  a1 = swap_other(x, u32x2{s16[0], s16[1]});  // lanes 0..15: lane + 16; lanes 32..47: lane + 16
+  const auto s32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  a2 = swap_other(x, u32x2{s32[0], s32[1]});  // lanes 0..31: lane + 32
+  const uint32_t u1 = __float_as_uint(a1);
+  const auto s32b = __builtin_amdgcn_permlane32_swap(u1, u1, false, false);
+  a3 = swap_other(a1, u32x2{s32b[0], s32b[1]});  // lanes 0..15: a1 of lane + 32, i.e. x of lane + 48
+}
+
 // HF Qwen3's q_norm / k_norm over one head (modeling_qwen3.py:252-253), then RoPE
 // (apply_rotary_pos_emb, :147-170), each op rounded to bf16: lane holds dims lane and
 // lane + 64 (tagged words u0, u1); nw0 selects the q_norm (0) or k_norm (64) weight words.
@@ -855,7 +877,6 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ float s_mx[8][2];                          // per-wave score maxima
   __shared__ __align__(16) float s_l[8][2];             // per-wave softmax sums
   __shared__ float s_hrow[ROWS];                       // the residual rows this workgroup reduces
-  __shared__ float s_res[ROWS];                        // stream-wave dot products for the store wave
   __shared__ uint32_t s_cnt;                           // stream-wave results published so far
   __shared__ uint32_t s_red;                           // reductions stored by the reduce wave
   __shared__ uint32_t s_nrm;                           // norm-weight sets written by the stream waves
@@ -1119,18 +1140,18 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           float r[8];
 #pragma unroll
           for (int i = 0; i < 8; i++) r[i] = dot_chunk(R.o[i], xa, 0.f);
-          half_sum_t(r);  // lane 16q holds pairs i + 4 (q & 1), i < 4, of row half q >> 1
-          if ((lane & 15) == 0) {
-            const int q = lane >> 4;
-#pragma unroll
-            for (int i = 0; i < 4; i++) s_res[16 * s + 2 * (i + 4 * (q & 1)) + (q >> 1)] = r[i];
+          half_sum_t(r);  // every lane of lane row q holds pairs i + 4 (q & 1), i < 4, of row half q >> 1
+          // lanes 16q + i (i < 4) store pair i + 4 (q & 1) of row half q >> 1, i.e. row
+          // 2 (i + 4 (q & 1)) + (q >> 1), straight from registers: the 16 lanes write the wave's
+          // 16 (value, tag) pairs, one 128-byte run (a regrouping into lanes 0..15, through LDS
+          // or by permlane swaps, measured slower)
+          {
+            const int i4 = lane & 3, q = lane >> 4;
+            const float rv = pick4(i4, r[0], r[1], r[2], r[3]);
+            if ((lane & 12) == 0)
+              st2_dev(ws + X_OPART + 2 * ((m * NXCD + g) * ROWS + 16 * s + 2 * (i4 + 4 * (q & 1)) + (q >> 1)),
+                      u32x2{__float_as_uint(rv), epoch * 32u + (uint32_t)layer + 1u});
           }
-          // the wave's 16 partials back in row order (its own slots of s_res), stored by the
-          // wave itself as one 128-byte run of (value, tag) pairs
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          if (lane < 16)
-            st2_dev(ws + X_OPART + 2 * ((m * NXCD + g) * ROWS + 16 * s + lane),
-                    u32x2{__float_as_uint(s_res[16 * s + lane]), epoch * 32u + (uint32_t)layer + 1u});
           if (lane == 0) signal_store(&s_cnt);
           AFTER(r[0] + r[1] + r[2] + r[3]);
           MQ_STAMP(layer * 40 + 5);
@@ -1209,18 +1230,21 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           float r[12];
 #pragma unroll
           for (int k = 0; k < 12; k++) r[k] = dot_chunk(R.gu[2 * k], x0, dot_chunk(R.gu[2 * k + 1], x1, 0.f));
-          wave_sum_t(r);  // lane 16q holds rows 3q .. 3q + 2
-          if ((lane & 15) == 0) {
-#pragma unroll
-            for (int k = 0; k < 3; k++) s_res[12 * s + 3 * (lane >> 4) + k] = r[k];
-          }
+          wave_sum_t(r);  // every lane of lane row q holds rows 3q .. 3q + 2
           // HF Qwen3MLP (modeling_qwen3.py:81-83): m = bf16(bf16(silu(gate)) * up) of the
-          // wave's 6 units (gate rows 0..5, up rows 6..11 of its s_res slots), stored by the wave
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          if (lane < 6) {
-            const float gt = rbf(s_res[12 * s + lane]), up = rbf(s_res[12 * s + 6 + lane]);
-            st1_plain(ws + lb + LX_M + UNITS * m + 6 * s + lane,
-                      tagged(tag_of(epoch, layer), rbf(rbf(gt / (1.0f + expf(-gt))) * up)));
+          // wave's 6 units, stored by the wave. Lane j < 6 takes unit j: its gate row j is r[j % 3]
+          // of lane row j / 3, its up row 6 + j is r[j % 3] of lane row 2 + j / 3; the values reach
+          // lanes 0..5 by permlane swaps (no regrouping through LDS)
+          {
+            const int j = lane & 15, k = j % 3;
+            float a1, a2, a3;
+            const float x = pick4(k, r[0], r[1], r[2], r[2]);
+            lane_rows(x, a1, a2, a3);
+            if (lane < 6) {
+              const float gt = rbf(lane < 3 ? x : a1), up = rbf(lane < 3 ? a2 : a3);
+              st1_plain(ws + lb + LX_M + UNITS * m + 6 * s + lane,
+                        tagged(tag_of(epoch, layer), rbf(rbf(gt / (1.0f + expf(-gt))) * up)));
+            }
           }
           if (lane == 0) signal_store(&s_cnt);
           AFTER(r[0] + r[1] + r[2]);
@@ -1234,16 +1258,17 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           float r[16];
 #pragma unroll
           for (int i = 0; i < 16; i++) r[i] = dot_chunk(R.d[i], xm, 0.f);
-          wave_sum_t(r);  // lane 16q holds rows 4q .. 4q + 3
-          if ((lane & 15) == 0) {
-#pragma unroll
-            for (int k = 0; k < 4; k++) s_res[16 * s + 4 * (lane >> 4) + k] = r[k];
+          wave_sum_t(r);  // every lane of lane row q holds rows 4q .. 4q + 3
+          // lanes 16q + k (k < 4) store row 4q + k straight from registers: the wave's 16
+          // partials as one 128-byte run of (value, tag) pairs (a regrouping into lanes 0..15
+          // measured slower)
+          {
+            const int k4 = lane & 3;
+            const float rv = pick4(k4, r[0], r[1], r[2], r[3]);
+            if ((lane & 12) == 0)
+              st2_dev(ws + X_DPART + 2 * ((m * NXCD + g) * ROWS + 16 * s + 4 * (lane >> 4) + k4),
+                      u32x2{__float_as_uint(rv), epoch * 32u + (uint32_t)layer + 1u});
           }
-          // the wave's 16 partials, stored by the wave as one 128-byte run of (value, tag) pairs
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          if (lane < 16)
-            st2_dev(ws + X_DPART + 2 * ((m * NXCD + g) * ROWS + 16 * s + lane),
-                    u32x2{__float_as_uint(s_res[16 * s + lane]), epoch * 32u + (uint32_t)layer + 1u});
           if (lane == 0) signal_store(&s_cnt);
           AFTER(r[0] + r[1] + r[2] + r[3]);
           MQ_STAMP(layer * 40 + 9);
