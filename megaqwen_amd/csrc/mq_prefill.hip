@@ -1785,9 +1785,17 @@ static void gemm_gate_up(GemmArgs g, hipStream_t stream, const WarmSet* warm = n
     // 128 x 256 tiles one; S = 768 24.6 -> 20.5 us, 1000 25.3 -> 21.6; at 640 14.6 -> 19.9)
     g.seg[0].ntiles = I / 128;
     gemm<EPI_SILU, 128, 256, 3, 1, 4, 4>(g, I / 128, stream);
-  } else if (g.m > SHORT_S) {
+  } else if (g.m > 512) {
     g.seg[0].ntiles = I / 64;
     gemm<EPI_SILU, 128, 128, 3, 1, 4, 4>(g, I / 64, stream, 1, 0, 1, warm);
+  } else if (g.m > SHORT_S) {
+    // (257..512 tokens: 128 x 96 tiles on four waves, 64 column tiles, so 256 workgroups fill
+    // the CUs where the 128 x 128 tiles leave 64 idle; same bits, whole prefill, same box:
+    // S = 300 1.722 -> 1.714 ms, 384 1.774 -> 1.759, 512 1.923 -> 1.918; at 640 1.9x the
+    // workgroups need two rounds, 2.414 -> 2.636; eight waves on two stages of two k-steps
+    // 1-3% slower)
+    g.seg[0].ntiles = I / 48;
+    gemm<EPI_SILU, 128, 96, 3, 1, 4, 1>(g, I / 48, stream, 1, 0, 1, warm);
   } else if (g.m > 128) {
     g.seg[0].ntiles = I / 64;
     gemm<EPI_SILU, 64, 128, 3, 1, 2, 4>(g, I / 64, stream, 1, 0, 1, warm);
