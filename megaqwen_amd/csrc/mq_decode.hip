@@ -654,10 +654,12 @@ __device__ __forceinline__ void norm_chunk(const float* x, float rstd, uint32_t 
 }
 
 // Waits until this XCD's own partial of the workgroup's first row carries tag64 (all lanes on
-// one word: one request a poll), before the eight-XCD poll of reduce_row8 starts. The other
+// one word: one request a poll), before the eight-XCD poll of reduce_row8 starts, where the
+// partial comes from another workgroup (group B summing group A's o_proj partials). The other
 // XCDs' partials are stored at about the same time, so the reduction ends as it would, while
 // the reduce waves' device-scope polls, 4 KB a round per wave otherwise, no longer load the
-// memory system through the long wait before the partials exist.
+// memory system through the long wait before the partials exist. (Where the workgroup's own
+// stream waves produce the partials, the reduce wave waits for their LDS signals instead.)
 __device__ __forceinline__ void wait_own_part(const Buf& wsb, uint32_t* ws, uint32_t word, uint32_t tag64) {
   uint32_t v = wsb.ld1(word * 4u), spins = 0;
   while (v != tag64) {
@@ -1652,7 +1654,9 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         MQ_STAMP(layer * 40 + 29);
         if (!b_h1) {
           // h1 = bf16(h + bf16(o)) (modeling_qwen3.py:297-298)
-          wait_own_part(wsb, ws, X_OPART + 2 * ((m * NXCD + g) * ROWS) + 1, tag64);
+          // the eight-XCD poll starts once this workgroup's stream waves have issued their
+          // o_proj partials (four signals a stage), not through the whole attention phase
+          wait_count(&s_cnt, 8u * (uint32_t)layer + 8u);
           const float h1v = rbf(hrow + rbf(reduce_row8(wsb, ws, X_OPART + 2 * (m * NXCD * ROWS + lane), tag64)));
           st1_plain(ws + lb + LX_H1 + row, tagged(tag, h1v));
           // the stream waves' next weight loads go behind this store
@@ -1675,8 +1679,9 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         BAR();  // E1
         MQ_STAMP(layer * 40 + 31);
         // h' = bf16(h1 + bf16(down)) (modeling_qwen3.py:303-304)
-        // (the down_proj reduction follows the down_proj partials by a stage, not a whole group
-        // phase, and waiting for its own partial first measured slower: p1 +6 us)
+        // the eight-XCD poll starts once this workgroup's stream waves have issued their
+        // down_proj partials (a memory poll of its own partial instead measured slower)
+        wait_count(&s_cnt, 8u * (uint32_t)layer + 8u);
         const float hn = rbf(h1row + rbf(reduce_row8(wsb, ws, X_DPART + 2 * (m * NXCD * ROWS + lane), tag64)));
         st1_plain(ws + lb + LX_H + row, tagged(tag, hn));
         hcur = hn;
