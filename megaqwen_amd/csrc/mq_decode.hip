@@ -186,8 +186,11 @@ constexpr int POLL_STAGGER = 4;
 // rows right after its o_proj partials: its burst, which grows with the K/V rows, then lands
 // before the layer ends instead of holding up its own gather of h (CU loads complete in
 // order). Shorter contexts keep the reduction in group A, whose short burst would otherwise
-// overlap that cross-XCD reduction (measured crossover: 160-180 positions).
-constexpr int B_H1_MIN_CTX = 176;
+// overlap that cross-XCD reduction. Measured crossover: 128 positions, where the attention
+// takes a second 16-row score block per wave and a second P.V trip (same box, group A summing
+// against group B: p120 288.7 against 294.8 us, p128 295.0 against 293.4, p144 298.5 against
+// 293.8).
+constexpr int B_H1_MIN_CTX = 129;
 constexpr uint32_t ERR_POLL = 1u;
 constexpr uint32_t ERR_XCD = 2u;  // a workgroup ran on an XCD numbered 8 or above
 constexpr uint32_t ERR_STEP = 4u;  // a device-resident step found an invalid token, position or count

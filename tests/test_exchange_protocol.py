@@ -51,7 +51,7 @@ def tag32(epoch, layer_plus_one):
 # launches with j < nsplit, and cleared at the start of every launch that does not write it.
 # LX_H and LX_CUE_B are written by group B (h and its cue), LX_QKV, LX_ATT, LX_PART and
 # LX_CUE_A by group A, LX_M by group B; LX_H1 by the reduce waves of group A, or of group B
-# in unsplit launches of 176 or more positions (the same rows, member m's 64, either way);
+# in unsplit launches of 129 or more positions (the same rows, member m's 64, either way);
 # the cross-XCD arrays by both.
 REGIONS = {
     "LX_H": ("16", "every"), "LX_H1": ("16", "every"), "LX_QKV": ("16", "every"), "LX_M": ("16", "every"),
