@@ -197,6 +197,13 @@ constexpr uint32_t ERR_STEP = 4u;  // a device-resident step found an invalid to
 
 constexpr int NT_LD = 2;  // non-temporal cache policy: bypasses the CU's L1, served by the XCD's L2
 
+// The first LM_ROWS LM-head rows of a workgroup are copied into its K/V LDS array before the LM
+// head (group A after its last layer's o_proj partials, group B a few a layer in its quiet
+// windows, in the instance where its array is otherwise unused), behind the first LM_OFF bytes,
+// which hold the workgroup's logits; the LM-head loop reads them from LDS.
+constexpr int LM_ROWS = 62;
+constexpr uint32_t LM_OFF = 4096;
+
 
 enum : int { MODE_INPUT_HIDDEN = 1, MODE_NO_LMHEAD = 2, MODE_LOGITS = 4, MODE_DEVICE_STEP = 8 };
 enum { W_IN = 0, W_Q, W_K, W_V, W_QN, W_KN, W_O, W_POST, W_G, W_U, W_D };
@@ -907,6 +914,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ uint32_t s_flag;
   __shared__ uint32_t s_epoch;                         // this launch's epoch
   float* s_lg = reinterpret_cast<float*>(s_kv);  // this workgroup's logits (K/V rows are dead by then)
+  static_assert(LM_OFF + LM_ROWS * H * 2 <= sizeof(s_kv) && LM_OFF >= 594 * 4, "LM rows fit behind the logits");
   // The unsplit instance: every group-A workgroup attends over the whole context in one pass,
   // and P.V writes the bf16 attention output straight into the o_proj input (s_x1), so the
   // o_proj dot products follow the attention's last barrier (B4) with no hand-out.
@@ -984,6 +992,18 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   // LM-head rows of this workgroup: 594 for w < 128, 593 after (151936 in total)
   const int r0 = w < 128 ? w * 594 : 128 * 594 + (w - 128) * 593;
   const int r1 = r0 + (w < 128 ? 594 : 593);
+  // the workgroups whose first LM-head rows sit in LDS for the LM head, and how many: group A
+  // copies LM_ROWS after its last layer, group B NSW in the quiet window of each layer but the
+  // last
+  const bool lm_lds = lm && (ga || !SPLIT);
+  const int lm_n = !lm_lds ? 0 : ga ? LM_ROWS : min(LM_ROWS, NSW * (L - 1));
+  // LM-head row r0 + i into the K/V LDS array (two 1 KB halves, non-temporal)
+  auto lm_row_dma = [&](int i) {
+    const uint16_t* src = P.lm_head + (size_t)(r0 + i) * H + 8 * (tid & 63);
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_kv + LM_OFF + 2048u * (uint32_t)i);
+    dma16_nt(src, dst);
+    dma16_nt(src + 512, dst + 1024u);
+  };
 
   float bestv = -INFINITY;
   int besti = 0x7fffffff;
@@ -1185,6 +1205,10 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
           put_norms();
           if (att) kv_dma(kv_nt, P, layer + 1, g, c0, nc0, p, lds_kv, s, lane);
           MQ_LANDED(layer * 40 + 10);
+        } else if (lm_lds) {
+          // the K/V rows are dead (the last attention is done): this wave's share of the
+          // workgroup's first LM-head rows into LDS
+          for (int i = s; i < LM_ROWS; i += NSW) lm_row_dma(i);
         }
       }
     } else {
@@ -1298,6 +1322,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         if (layer + 1 < L) {
           // hold the burst until group A has published the next layer's q/k/v rows (its
           // member 0's first word), so that it runs during A's attention
+          // (before the weight loads, so that waiting for them covers these copies too)
+          if (NSW * layer + s < lm_n) lm_row_dma(NSW * layer + s);
           R.wpost = ldw2(wp(layer + 1, W_POST) + 4 * st);
           load_gu(layer + 1);
           load_d(layer + 1);
@@ -1321,6 +1347,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         }
       }
     }
+    if (lm_lds) wait_vmem();  // the LM-head rows' copies have landed
     BAR();  // F1: final normed h in s_x0
   } else if (wave < NSW + NPW) {
     // ==================================================================== poll waves
@@ -1843,9 +1870,15 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
       for (int u = 0; u < 4; u++) {
         const int r = rb + 8 * u;
         if (r < r1) {
-          const uint16_t* rowp = P.lm_head + (size_t)r * H;
-          Wr[u][0] = ldw(rowp + 8 * lane);
-          Wr[u][1] = ldw(rowp + 512 + 8 * lane);
+          if (r - r0 < lm_n) {
+            const uint8_t* lp = s_kv + LM_OFF + 2048 * (r - r0) + 16 * lane;
+            Wr[u][0] = *reinterpret_cast<const u32x4*>(lp);
+            Wr[u][1] = *reinterpret_cast<const u32x4*>(lp + 1024);
+          } else {
+            const uint16_t* rowp = P.lm_head + (size_t)r * H;
+            Wr[u][0] = ldw(rowp + 8 * lane);
+            Wr[u][1] = ldw(rowp + 512 + 8 * lane);
+          }
         }
       }
     };
