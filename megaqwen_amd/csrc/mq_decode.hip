@@ -78,7 +78,9 @@
 // MQ_STAMP_DUMP()
 // runs once at the end of the kernel. Both compile to nothing unless a tracing build
 // (csrc/trace/mq_decode_trace.cpp) defines them before including this file.
-#ifndef MQ_STAMP
+#ifdef MQ_STAMP
+#define MQ_TRACE_BUILD 1
+#else
 #define MQ_STAMP(i) ((void)0)
 #endif
 #ifndef MQ_STAMP_DUMP
@@ -197,12 +199,23 @@ constexpr uint32_t ERR_STEP = 4u;  // a device-resident step found an invalid to
 
 constexpr int NT_LD = 2;  // non-temporal cache policy: bypasses the CU's L1, served by the XCD's L2
 
-// The first LM_ROWS LM-head rows of a workgroup are copied into its K/V LDS array before the LM
+// The first LM_KV_ROWS LM-head rows of a workgroup are copied into its K/V LDS array before the LM
 // head (group A after its last layer's o_proj partials, group B a few a layer in its quiet
 // windows, in the instance where its array is otherwise unused), behind the first LM_OFF bytes,
 // which hold the workgroup's logits; the LM-head loop reads them from LDS.
-constexpr int LM_ROWS = 62;
+constexpr int LM_KV_ROWS = 62;
 constexpr uint32_t LM_OFF = 4096;
+// and, in the split instance without the pipelined passes (where only group A copies rows), the
+// next LM_X_ROWS rows into an LDS array of their own, in what the kernel's other arrays leave of
+// the CU's 160 KB (less in the tracing build, whose stamps sit in LDS). Measured (same box):
+// p1024 330.6 -> 329.3 us, p3000 374.1 -> 371.4 in this instance; p200 288.3 -> 289.1 and
+// p8192 551.6 -> 551.9 in the other two, which keep LM_KV_ROWS
+#ifdef MQ_TRACE_BUILD
+constexpr int LM_X_ROWS = 4;
+#else
+constexpr int LM_X_ROWS = 7;
+#endif
+constexpr int LM_ROWS = LM_KV_ROWS + LM_X_ROWS;
 
 
 enum : int { MODE_INPUT_HIDDEN = 1, MODE_NO_LMHEAD = 2, MODE_LOGITS = 4, MODE_DEVICE_STEP = 8 };
@@ -914,7 +927,8 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   __shared__ uint32_t s_flag;
   __shared__ uint32_t s_epoch;                         // this launch's epoch
   float* s_lg = reinterpret_cast<float*>(s_kv);  // this workgroup's logits (K/V rows are dead by then)
-  static_assert(LM_OFF + LM_ROWS * H * 2 <= sizeof(s_kv) && LM_OFF >= 594 * 4, "LM rows fit behind the logits");
+  __shared__ __align__(16) uint8_t s_lmx[LM_X_ROWS * H * 2];   // LM-head rows LM_KV_ROWS .. LM_ROWS - 1
+  static_assert(LM_OFF + LM_KV_ROWS * H * 2 <= sizeof(s_kv) && LM_OFF >= 594 * 4, "LM rows fit behind the logits");
   // The unsplit instance: every group-A workgroup attends over the whole context in one pass,
   // and P.V writes the bf16 attention output straight into the o_proj input (s_x1), so the
   // o_proj dot products follow the attention's last barrier (B4) with no hand-out.
@@ -993,14 +1007,19 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
   const int r0 = w < 128 ? w * 594 : 128 * 594 + (w - 128) * 593;
   const int r1 = r0 + (w < 128 ? 594 : 593);
   // the workgroups whose first LM-head rows sit in LDS for the LM head, and how many: group A
-  // copies LM_ROWS after its last layer, group B NSW in the quiet window of each layer but the
+  // copies LM_N after its last layer, group B NSW in the quiet window of each layer but the
   // last
   const bool lm_lds = lm && (ga || !SPLIT);
-  const int lm_n = !lm_lds ? 0 : ga ? LM_ROWS : min(LM_ROWS, NSW * (L - 1));
+  constexpr int LM_X = SPLIT && !PIPE ? LM_X_ROWS : 0;  // rows in s_lmx in this instance
+  constexpr int LM_N = LM_KV_ROWS + LM_X;
+  const int lm_n = !lm_lds ? 0 : ga ? LM_N : min(LM_N, NSW * (L - 1));
   // LM-head row r0 + i into the K/V LDS array (two 1 KB halves, non-temporal)
   auto lm_row_dma = [&](int i) {
     const uint16_t* src = P.lm_head + (size_t)(r0 + i) * H + 8 * (tid & 63);
-    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_kv + LM_OFF + 2048u * (uint32_t)i);
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(
+        LM_X == 0 || i < LM_KV_ROWS ? lds_kv + LM_OFF + 2048u * (uint32_t)i
+                       : (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)s_lmx +
+                             2048u * (uint32_t)(i - LM_KV_ROWS));
     dma16_nt(src, dst);
     dma16_nt(src + 512, dst + 1024u);
   };
@@ -1208,7 +1227,7 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         } else if (lm_lds) {
           // the K/V rows are dead (the last attention is done): this wave's share of the
           // workgroup's first LM-head rows into LDS
-          for (int i = s; i < LM_ROWS; i += NSW) lm_row_dma(i);
+          for (int i = s; i < LM_N; i += NSW) lm_row_dma(i);
         }
       }
     } else {
@@ -1871,7 +1890,9 @@ __global__ void __launch_bounds__(NT, 1) mq_decode_kernel(DecodeParams P) {
         const int r = rb + 8 * u;
         if (r < r1) {
           if (r - r0 < lm_n) {
-            const uint8_t* lp = s_kv + LM_OFF + 2048 * (r - r0) + 16 * lane;
+            const uint8_t* lp = (LM_X == 0 || r - r0 < LM_KV_ROWS ? s_kv + LM_OFF + 2048 * (r - r0)
+                                                     : s_lmx + 2048 * (r - r0 - LM_KV_ROWS)) +
+                                16 * lane;
             Wr[u][0] = *reinterpret_cast<const u32x4*>(lp);
             Wr[u][1] = *reinterpret_cast<const u32x4*>(lp + 1024);
           } else {
